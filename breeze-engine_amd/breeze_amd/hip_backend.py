@@ -1,0 +1,286 @@
+"""ctypes bridge to the gfx950 quantized linear library.
+
+Drop-in for ``breeze.cpu_backend`` (breeze/cpu_backend.py:57-242): the same
+``available / set_threads / set_hi_prec / prepack / matmul / free`` surface,
+argument order, validation and exceptions, over ``libbreeze_qmm.so``, whose
+C ABI keeps the reference's ``i4_*`` names (include/breeze_qmm.h).
+
+GPU additions: ``matmul`` also takes a PyTorch-ROCm tensor on the GPU and
+returns one (computed on the current stream, no host round trip);
+``matmul_argmax`` adds the LM-head argmax; ``unpack`` and ``block_dots``
+expose the packed handle and the exact block integers for tests.
+
+There is no CPU fallback: without the library or a gfx950 device the calls
+raise.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.environ.get("BREEZE_HIP_KERNEL", os.path.join(_HERE, "libbreeze_qmm.so"))
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+_lib = None
+_native_prepack = None
+try:
+    _lib = ctypes.CDLL(_SO)
+    _lib.i4_prepack.restype = _vp
+    _lib.i4_prepack.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _i]
+    _lib.i4_matmul.argtypes = [_vp, _vp, _i, _vp]
+    _lib.i4_matmul.restype = None
+    _lib.i4_matmul_region.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
+    _lib.i4_matmul_region.restype = None
+    _lib.i4_free.argtypes = [_vp]
+    _lib.i4_free.restype = None
+    for _name in ("i4_set_threads", "i4_set_hi_prec", "i4_set_numa_split"):
+        getattr(_lib, _name).argtypes = [_i]
+        getattr(_lib, _name).restype = None
+    _lib.i4_last_error.restype = ctypes.c_char_p
+    _lib.i4_last_error.argtypes = []
+    _lib.i4_device_ok.restype = _i
+    _lib.i4_device_ok.argtypes = []
+    _lib.i4_matmul_dev.restype = _i
+    _lib.i4_matmul_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
+    _lib.i4_matmul_argmax_dev.restype = _i
+    _lib.i4_matmul_argmax_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
+    _lib.i4_block_dots_dev.restype = _i
+    _lib.i4_block_dots_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
+    _lib.i4_handle_info.restype = _i
+    _lib.i4_handle_info.argtypes = [_vp, _vp]
+    _lib.i4_unpack.restype = _i
+    _lib.i4_unpack.argtypes = [_vp, _vp, _vp, _vp, _vp]
+except (OSError, AttributeError):
+    _lib = None
+
+if _lib is not None:
+    _native_prepack = _lib.i4_prepack_onnx
+    _native_prepack.restype = _vp
+    _native_prepack.argtypes = [_vp] * 3 + [_i] * 4
+
+
+def available():
+    """True when the library is loaded (compute additionally needs a GPU)."""
+    return _lib is not None
+
+
+def device_available():
+    """True when the library is loaded and a gfx950 device can run it."""
+    return _lib is not None and _lib.i4_device_ok() == 1
+
+
+def last_error():
+    return _lib.i4_last_error().decode() if _lib is not None else "library not loaded"
+
+
+def set_threads(n):
+    """Accepted for API compatibility; the GPU path has no host thread pool."""
+    if _lib is not None:
+        _lib.i4_set_threads(int(n))
+
+
+def set_hi_prec(on):
+    """Select process-global INT16 two-pass (on) or INT8 activation quantization.
+
+    Configure before inference; like the reference, concurrent mutation is not
+    thread-safe and callers serialize setting changes with native work."""
+    if _lib is not None:
+        _lib.i4_set_hi_prec(1 if on else 0)
+
+
+def _p(a):
+    return a.ctypes.data_as(_vp) if a is not None else None
+
+
+def _require_lib():
+    if _lib is None:
+        raise RuntimeError(f"GPU kernel library unavailable ({_SO}); build it with "
+                           "`python -m breeze_amd._build`")
+
+
+def prepack(qweight, scales, qzeros, K, N, bits=4, block_size=32):
+    """Pack ONNX MatMulNBits weights into device memory; returns an int handle.
+
+    Same contract as breeze/cpu_backend.py:119-168: 4-bit (nibbles, zero
+    point default 8) or 8-bit (bytes, symmetric zero point 128) weights in
+    blocks of 32; scales fp16 are kept as fp16 bits, anything else is
+    converted to fp32; the handle owns device copies of everything."""
+    if bits not in (4, 8) or block_size != 32:
+        raise ValueError("quantized prepack requires 4/8-bit weights and block_size=32")
+    if (not isinstance(N, (int, np.integer)) or not isinstance(K, (int, np.integer))
+            or isinstance(N, (bool, np.bool_)) or isinstance(K, (bool, np.bool_))
+            or N > np.iinfo(np.int32).max or K > np.iinfo(np.int32).max):
+        raise ValueError("Prepack dimensions must be signed 32-bit integers")
+    N, K = int(N), int(K)
+    if N <= 0 or K <= 0 or N % 16 or K % 32:
+        raise ValueError(f"need N%16==0,K%32==0 (got N={N},K={K})")
+    qweight = np.asarray(qweight)
+    if qweight.dtype != np.uint8:
+        raise ValueError("MatMulNBits packed weights must be uint8")
+    nblk = K // 32
+    if qweight.size != N * nblk * (4 * bits):
+        raise ValueError("Incorrect packed weight size for the supplied dimensions")
+    scales = np.asarray(scales)
+    if scales.size != N * nblk:
+        raise ValueError("Incorrect scale count for the supplied dimensions")
+    if qzeros is not None and np.size(qzeros):
+        qzeros = np.asarray(qzeros)
+        if qzeros.dtype != np.uint8:
+            raise ValueError("Packed zero points must be uint8")
+        if qzeros.size != N * (nblk if bits == 8 else (nblk + 1) // 2):
+            raise ValueError("Incorrect zero-point count for the supplied dimensions")
+        if bits == 8 and np.any(qzeros != 128):
+            raise ValueError("INT8 weights require symmetric zero point 128")
+        qzeros = np.ascontiguousarray(qzeros) if bits == 4 else None
+    else:
+        qzeros = None
+    _require_lib()
+    if _native_prepack is None:
+        return _prepack_numpy(qweight, scales, qzeros, K, N, bits, block_size)
+
+    qw = np.ascontiguousarray(qweight)
+    scale_dtype = np.float16 if scales.dtype == np.float16 else np.float32
+    sc = np.require(scales, dtype=scale_dtype, requirements=["C", "A"])
+    handle = _native_prepack(_p(qw), _p(sc), _p(qzeros), N, K, int(bits), sc.itemsize * 8)
+    if not handle:
+        raise MemoryError(f"Could not allocate packed {bits}-bit weights (N={N}, K={K}): "
+                          f"{last_error()}")
+    return handle
+
+
+def _prepack_numpy(qweight, scales, qzeros, K, N, bits=4, block_size=32):
+    """Build the reference's legacy pre-transformed layout in NumPy and pack
+    it through ``i4_prepack`` (breeze/cpu_backend.py:171-227 describes the
+    layout).  Callers validate the contract first.  Tests use it to show the
+    legacy and MatMulNBits entry points agree."""
+    _require_lib()
+    nblk = K // 32
+    ntiles = N // 16
+
+    def tile16(x):  # [N, nblk] -> [ntiles, nblk, 16]
+        return np.ascontiguousarray(x.reshape(ntiles, 16, nblk).transpose(0, 2, 1))
+
+    sc = tile16(np.asarray(scales, dtype=np.float32).reshape(N, nblk))
+    if bits == 8:
+        w = np.ascontiguousarray(qweight).reshape(N, nblk, 32).astype(np.int16)
+        b = (w - 128).astype(np.int8)
+        Bv = np.ascontiguousarray(
+            b.reshape(ntiles, 16, nblk, 8, 4).transpose(0, 2, 3, 1, 4).reshape(ntiles, nblk, 8, 64))
+        corr = tile16((128 * b.astype(np.int32).sum(axis=2)).astype(np.int32))
+        handle = _lib.i4_prepack(_p(Bv), _p(sc), None, _p(corr), N, K, nblk, 8)
+    else:
+        qw = np.ascontiguousarray(qweight).reshape(N, nblk, 16)
+        w = np.empty((N, nblk, 32), np.uint8)
+        w[:, :, 0::2] = qw & 15
+        w[:, :, 1::2] = qw >> 4
+        if qzeros is not None and np.size(qzeros):
+            packed = (nblk + 1) // 2
+            qz = np.ascontiguousarray(qzeros).reshape(N, packed)
+            zpf = np.empty((N, packed * 2), np.uint8)
+            zpf[:, 0::2] = qz & 15
+            zpf[:, 1::2] = qz >> 4
+            zp = zpf[:, :nblk].astype(np.int32)
+        else:
+            zp = np.full((N, nblk), 8, np.int32)
+        w2 = w.reshape(ntiles, 16, nblk, 8, 4).transpose(0, 2, 3, 1, 4).reshape(ntiles, nblk, 8, 64)
+        Bv = np.ascontiguousarray((w2[..., 0::2] | (w2[..., 1::2] << 4)).astype(np.uint8))
+        zp_t = tile16(zp.astype(np.int8))
+        corr = tile16((128 * (w.astype(np.int32).sum(axis=2) - 32 * zp)).astype(np.int32))
+        handle = _lib.i4_prepack(_p(Bv), _p(sc), _p(zp_t), _p(corr), N, K, nblk, 4)
+    if not handle:
+        raise MemoryError(f"Could not allocate packed {bits}-bit weights (N={N}, K={K}): "
+                          f"{last_error()}")
+    return handle
+
+
+def _is_torch(x):
+    return type(x).__module__.split(".")[0] == "torch"
+
+
+def _torch_stream(t):
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _check_rc(rc, what):
+    if rc != 0:
+        raise RuntimeError(f"{what} failed ({rc}): {last_error()}")
+
+
+def matmul(handle, a2d, N):
+    """a2d: fp32 [M, K].  Returns fp32 [M, N].
+
+    NumPy in, NumPy out (blocking, like the reference); a GPU torch tensor in,
+    a GPU torch tensor out (asynchronous on the current stream)."""
+    _require_lib()
+    if _is_torch(a2d):
+        import torch
+        a = a2d.to(torch.float32).contiguous()
+        M = a.shape[0]
+        out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+        _check_rc(_lib.i4_matmul_dev(_vp(handle), _vp(a.data_ptr()), int(M), _vp(out.data_ptr()),
+                                     _torch_stream(a)), "i4_matmul_dev")
+        return out
+    a2d = np.ascontiguousarray(a2d, dtype=np.float32)
+    M = a2d.shape[0]
+    out = np.empty((M, N), dtype=np.float32)
+    _lib.i4_matmul(_vp(handle), _p(a2d), int(M), _p(out))
+    err = last_error()
+    if err:
+        raise RuntimeError(f"i4_matmul failed: {err}")
+    return out
+
+
+def matmul_argmax(handle, a2d, N):
+    """GPU torch tensor [M, K] -> (logits fp32 [M, N], argmax int64 [M])."""
+    _require_lib()
+    import torch
+    a = a2d.to(torch.float32).contiguous()
+    M = a.shape[0]
+    out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    idx = torch.empty((M,), dtype=torch.int64, device=a.device)
+    _check_rc(_lib.i4_matmul_argmax_dev(_vp(handle), _vp(a.data_ptr()), int(M), _vp(out.data_ptr()),
+                                        _vp(idx.data_ptr()), _torch_stream(a)), "i4_matmul_argmax_dev")
+    return out, idx
+
+
+def block_dots(handle, a2d, N, K):
+    """GPU torch tensor [M, K] -> int32 [M, N, K/32] exact block integers."""
+    _require_lib()
+    import torch
+    a = a2d.to(torch.float32).contiguous()
+    M = a.shape[0]
+    cs = torch.empty((M, N, K // 32), dtype=torch.int32, device=a.device)
+    _check_rc(_lib.i4_block_dots_dev(_vp(handle), _vp(a.data_ptr()), int(M), _vp(cs.data_ptr()),
+                                     _torch_stream(a)), "i4_block_dots_dev")
+    return cs
+
+
+def handle_info(handle):
+    _require_lib()
+    out = np.zeros(8, np.int64)
+    _check_rc(_lib.i4_handle_info(_vp(handle), _p(out)), "i4_handle_info")
+    keys = ("N", "K", "bits", "scale_group", "has_zero_points", "has_corr_delta", "device_bytes",
+            "device")
+    return {k: int(v) for k, v in zip(keys, out)}
+
+
+def unpack(handle):
+    """Read a handle back as MatMulNBits arrays (qweight, scales, zp, corr_delta)."""
+    info = handle_info(handle)
+    N, K, bits = info["N"], info["K"], info["bits"]
+    nblk = K // 32
+    qw = np.empty((N, nblk, 4 * bits), np.uint8)
+    sc = np.empty((N, nblk), np.float32)
+    zp = np.empty((N, nblk), np.uint8)
+    dl = np.empty((N, nblk), np.int32)
+    _check_rc(_lib.i4_unpack(_vp(handle), _p(qw), _p(sc), _p(zp), _p(dl)), "i4_unpack")
+    return dict(qweight=qw, scales=sc, zp=zp, corr_delta=dl, bits=bits)
+
+
+def free(handle):
+    if _lib is not None and handle:
+        _lib.i4_free(_vp(handle))

@@ -1,0 +1,115 @@
+/*
+ * breeze_qmm.h -- C ABI of the MI355X (gfx950) quantized linear library.
+ *
+ * The first block of entry points keeps the names, argument order and error
+ * conventions of the reference CPU kernel's C ABI (kernel/quantized_matmul.cpp,
+ * bound from Python by breeze/cpu_backend.py:15-54), so code written against
+ * that ABI can load this library instead.  Host pointers in, host pointers
+ * out, synchronous.
+ *
+ * The second block adds what a GPU caller needs: device-pointer entry points
+ * on a caller's HIP stream (for PyTorch-ROCm tensors), an error string, the
+ * fused LM-head argmax, and introspection hooks used by the parity tests.
+ *
+ * Threading: like the reference, settings are process-global and callers
+ * serialize calls that share a device (the library keeps one activation
+ * workspace per device).  A handle is bound to the device that was current
+ * when it was packed.
+ */
+#ifndef BREEZE_QMM_H
+#define BREEZE_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- reference ABI --------------------------------------------------- */
+
+/* Replaces i4_set_threads (quantized_matmul.cpp:474).  Accepted and ignored:
+ * the GPU path has no host thread pool. */
+void i4_set_threads(int n);
+
+/* Replaces i4_set_numa_split (quantized_matmul.cpp:475).  Accepted and
+ * ignored: there is no NUMA weight replica on one GPU. */
+void i4_set_numa_split(int cpu);
+
+/* Replaces i4_set_hi_prec (quantized_matmul.cpp:476): 1 = two-pass INT16
+ * activations, 0 = INT8 activations.  Process-global; default 0. */
+void i4_set_hi_prec(int on);
+
+/* Replaces i4_prepack_onnx (quantized_matmul.cpp:505-520).
+ * qw: MatMulNBits bytes [N, K/32, 4*bits]; scales: [N, K/32] fp16
+ * (scale_bits 16) or fp32 (32); qzeros: packed INT4 zero points
+ * [N, ceil(K/64)] or NULL (INT8 must pass NULL).  Host pointers; the handle
+ * owns device copies.  NULL on a contract violation (N<=0, K<=0, N%16, K%32,
+ * bits not 4/8, scale_bits not 16/32, INT8 with qzeros) or on failure;
+ * i4_last_error() says which. */
+void* i4_prepack_onnx(const uint8_t* qw, const void* scales, const uint8_t* qzeros,
+                      int N, int K, int bits, int scale_bits);
+
+/* Replaces i4_prepack (quantized_matmul.cpp:480-499): the reference's
+ * pre-transformed VNNI layout (B [N/16, nblk, 8, 32|64], scale/zp/corr
+ * [N/16, nblk, 16]).  The supplied corr is honoured exactly as the reference
+ * honours it, including values that differ from 128*sum(w - zp). */
+void* i4_prepack(const uint8_t* B, const float* scale, const int8_t* zp,
+                 const int32_t* corr, int N, int K, int nblk, int bits);
+
+/* Replaces i4_free (quantized_matmul.cpp:522-524).  NULL is ignored. */
+void i4_free(void* handle);
+
+/* Replaces i4_matmul (quantized_matmul.cpp:528-552): C[M,N] = A[M,K] times
+ * the packed weights, FP32, host pointers, blocking.  Like the reference it
+ * returns nothing; on failure C is left unwritten and i4_last_error() is set
+ * (the Python bridge turns that into RuntimeError). */
+void i4_matmul(void* handle, const float* A, int M, float* C);
+
+/* Replaces i4_matmul_region (quantized_matmul.cpp:558-572).  There is no
+ * OpenMP region on the GPU path: this is i4_matmul, and the caller's scratch
+ * and ascale buffers are not used. */
+void i4_matmul_region(void* handle, const float* A, int M, float* C,
+                      uint8_t* scratch, float* ascale);
+
+/* ---- GPU additions (no counterpart in the reference) ----------------- */
+
+/* Message for the last failure on this thread ("" if none). */
+const char* i4_last_error(void);
+
+/* 1 if a usable gfx950 device and this library's kernels are present. */
+int i4_device_ok(void);
+
+/* i4_matmul on device pointers, asynchronous on `stream` (a hipStream_t, or
+ * NULL for the null stream).  dA: fp32 [M,K], dC: fp32 [M,N], both 16-byte
+ * aligned.  Returns 0, or a negative code with i4_last_error() set. */
+int i4_matmul_dev(void* handle, const float* dA, int M, float* dC, void* stream);
+
+/* As i4_matmul_dev, and also writes, for each row m, the index of the first
+ * maximum of C[m,:] (NaN counts as the maximum, -0 equals +0; numpy.argmax
+ * semantics) to dIdx[m] (int64).  Used for the LM head. */
+int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC,
+                         int64_t* dIdx, void* stream);
+
+/* Handle facts: out[0..7] = N, K, bits, scale group (blocks per distinct
+ * scale, 0 = one per column), has_zero_points, has_corr_delta,
+ * device bytes held, device ordinal.  Returns 0 or -1. */
+int i4_handle_info(void* handle, int64_t* out);
+
+/* Reads a handle back into MatMulNBits form on the host: qw [N, K/32,
+ * 4*bits] bytes, scales fp32 [N, K/32], zp [N, K/32] (one byte per block,
+ * the zero point actually applied) and corr_delta int32 [N, K/32]
+ * (128*sum(w - zp) - corr, zero unless a legacy corr disagreed).  Any output
+ * pointer may be NULL.  Lets tests pin the packed layout semantically. */
+int i4_unpack(void* handle, uint8_t* qw, float* scales, uint8_t* zp, int32_t* corr_delta);
+
+/* Debug export of the exact per-(row, column, 32-block) integer dot products
+ * cs = sum_k q[m,k] * b[n,k] (plus the legacy corr term) that feed the FP32
+ * epilogue: dCs int32 [M, N, K/32].  Same kernels as i4_matmul_dev. */
+int i4_block_dots_dev(void* handle, const float* dA, int M, int32_t* dCs, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BREEZE_QMM_H */

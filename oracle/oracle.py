@@ -1,0 +1,422 @@
+"""TEST INFRASTRUCTURE ONLY -- the oracle for Breeze's quantized linear path.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this module, and only as the checker; the product package never
+does.  It holds:
+
+* ``C``: ctypes bindings of ``liboracle.so`` (``qmm_oracle.c``), the scalar C
+  restatement that is the authority for bit-exact parity;
+* a NumPy twin of the same arithmetic (``quantize_np``, ``block_dots_np``,
+  ``chain_np``, ``matmul_np``), written independently and cross-checked with
+  the C restatement, fast enough for mid-sized parity cases;
+* ``dequantize_matmul_nbits``: the float MatMulNBits decode
+  (breeze/quant.py:9-58) used by the reference's own accuracy tests;
+* ``make_config``: seeded MatMulNBits inputs for the five benchmark
+  workloads, drawn in a fixed order;
+* ``Ref``: ctypes bindings of the reference kernel compiled from its own
+  source into ``oracle/_ref/libref_qmm.so`` (see the Makefile), when present.
+
+Reference citations are paths inside the breeze-engine repository.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libref_qmm.so")
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+
+def _p(a):
+    return a.ctypes.data_as(_vp) if a is not None else None
+
+
+# ---------------------------------------------------------------- C oracle
+
+class _COracle:
+    def __init__(self, path=LIB_PATH):
+        lib = ctypes.CDLL(path)
+        lib.orc_half_to_float.restype = ctypes.c_float
+        lib.orc_half_to_float.argtypes = [ctypes.c_uint16]
+        lib.orc_quantize.argtypes = [_vp, _i, _i, _i, _vp, _vp, _vp]
+        lib.orc_split_hilo.argtypes = [_vp, ctypes.c_size_t, _vp, _vp]
+        lib.orc_unpack_nbits.argtypes = [_vp, _vp, _vp] + [_i] * 4 + [_vp, _vp]
+        lib.orc_unpack_legacy.argtypes = [_vp] * 4 + [_i] * 4 + [_vp] * 3
+        lib.orc_block_dots.argtypes = [_vp, _i, _vp, _i, _i, _vp]
+        lib.orc_chain.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
+        lib.orc_matmul_nbits.argtypes = [_vp, _vp, _vp] + [_i] * 4 + [_vp, _i, _i, _vp, _vp]
+        lib.orc_matmul_legacy.argtypes = [_vp] * 4 + [_i] * 4 + [_vp, _i, _i, _vp]
+        self.lib = lib
+
+    def half_to_float(self, h):
+        return self.lib.orc_half_to_float(int(h))
+
+    def quantize(self, A, hi_prec=True):
+        A = np.ascontiguousarray(A, np.float32)
+        M, K = A.shape
+        q = np.empty((M, K), np.int16)
+        sa = np.empty((M, K // 32), np.float32)
+        sq = np.empty((M, K // 32), np.int32)
+        self.lib.orc_quantize(_p(A), M, K, int(bool(hi_prec)), _p(q), _p(sa), _p(sq))
+        return q, sa, sq
+
+    def split_hilo(self, q):
+        q = np.ascontiguousarray(q, np.int16)
+        hi = np.empty(q.shape, np.uint8)
+        lo = np.empty(q.shape, np.uint8)
+        self.lib.orc_split_hilo(_p(q), q.size, _p(hi), _p(lo))
+        return hi, lo
+
+    def unpack_nbits(self, qweight, scales, qzeros, N, K, bits):
+        qw = np.ascontiguousarray(qweight, np.uint8)
+        sc = np.ascontiguousarray(scales)
+        sbits = 16 if sc.dtype == np.float16 else 32
+        sc = np.ascontiguousarray(sc, np.float16 if sbits == 16 else np.float32)
+        qz = None if qzeros is None else np.ascontiguousarray(qzeros, np.uint8)
+        b = np.empty((N, K), np.int16)
+        sb = np.empty((N, K // 32), np.float32)
+        rc = self.lib.orc_unpack_nbits(_p(qw), _p(sc), _p(qz), N, K, bits, sbits, _p(b), _p(sb))
+        if rc:
+            raise ValueError("oracle rejected the MatMulNBits contract")
+        return b, sb
+
+    def unpack_legacy(self, B, scale, zp, corr, N, K, bits):
+        B = np.ascontiguousarray(B, np.uint8)
+        scale = np.ascontiguousarray(scale, np.float32)
+        corr = np.ascontiguousarray(corr, np.int32)
+        zp = None if zp is None else np.ascontiguousarray(zp, np.int8)
+        b = np.empty((N, K), np.int16)
+        sb = np.empty((N, K // 32), np.float32)
+        delta = np.empty((N, K // 32), np.int32)
+        rc = self.lib.orc_unpack_legacy(_p(B), _p(scale), _p(zp), _p(corr), N, K, K // 32, bits,
+                                        _p(b), _p(sb), _p(delta))
+        if rc:
+            raise ValueError("oracle rejected the legacy layout")
+        return b, sb, delta
+
+    def block_dots(self, q, b):
+        q = np.ascontiguousarray(q, np.int16)
+        b = np.ascontiguousarray(b, np.int16)
+        M, K = q.shape
+        N = b.shape[0]
+        cs = np.empty((M, N, K // 32), np.int32)
+        self.lib.orc_block_dots(_p(q), M, _p(b), N, K, _p(cs))
+        return cs
+
+    def chain(self, cs, sa, sb):
+        cs = np.ascontiguousarray(cs, np.int32)
+        sa = np.ascontiguousarray(sa, np.float32)
+        sb = np.ascontiguousarray(sb, np.float32)
+        M, N, nblk = cs.shape
+        C = np.empty((M, N), np.float32)
+        self.lib.orc_chain(_p(cs), _p(sa), _p(sb), M, N, nblk, _p(C))
+        return C
+
+    def matmul(self, qweight, scales, qzeros, N, K, bits, A, hi_prec=True, want_cs=False):
+        """C [M,N] (and optionally the [M,N,K/32] block integers)."""
+        qw = np.ascontiguousarray(qweight, np.uint8)
+        sc = np.asarray(scales)
+        sbits = 16 if sc.dtype == np.float16 else 32
+        sc = np.ascontiguousarray(sc, np.float16 if sbits == 16 else np.float32)
+        qz = None if qzeros is None else np.ascontiguousarray(qzeros, np.uint8)
+        A = np.ascontiguousarray(A, np.float32)
+        M = A.shape[0]
+        C = np.empty((M, N), np.float32)
+        cs = np.empty((M, N, K // 32), np.int32) if want_cs else None
+        rc = self.lib.orc_matmul_nbits(_p(qw), _p(sc), _p(qz), N, K, bits, sbits, _p(A), M,
+                                       int(bool(hi_prec)), _p(C), _p(cs))
+        if rc:
+            raise ValueError(f"oracle matmul failed ({rc})")
+        return (C, cs) if want_cs else C
+
+    def matmul_legacy(self, B, scale, zp, corr, N, K, bits, A, hi_prec=True):
+        B = np.ascontiguousarray(B, np.uint8)
+        scale = np.ascontiguousarray(scale, np.float32)
+        corr = np.ascontiguousarray(corr, np.int32)
+        zp = None if zp is None else np.ascontiguousarray(zp, np.int8)
+        A = np.ascontiguousarray(A, np.float32)
+        M = A.shape[0]
+        C = np.empty((M, N), np.float32)
+        rc = self.lib.orc_matmul_legacy(_p(B), _p(scale), _p(zp), _p(corr), N, K, K // 32, bits,
+                                        _p(A), M, int(bool(hi_prec)), _p(C))
+        if rc:
+            raise ValueError(f"oracle legacy matmul failed ({rc})")
+        return C
+
+
+_C = None
+
+
+def c_oracle():
+    """The C restatement (loaded once)."""
+    global _C
+    if _C is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing; run `make -C oracle oracle`")
+        _C = _COracle()
+    return _C
+
+
+# ---------------------------------------------------------------- NumPy twin
+
+def fma_f32(a, b, c):
+    """Exactly rounded float32 fma(a, b, c), elementwise, in NumPy.
+
+    a*b is exact in float64; the float64 sum is turned into round-to-odd with
+    an exact TwoSum error term, and round-to-odd followed by a float32
+    round-to-nearest-even is a single correct rounding (53 >= 24 + 2)."""
+    a = np.asarray(a, np.float32).astype(np.float64)
+    b = np.asarray(b, np.float32).astype(np.float64)
+    c = np.asarray(c, np.float32).astype(np.float64)
+    p = a * b
+    with np.errstate(invalid="ignore", over="ignore"):
+        s = p + c
+        bp = s - c
+        e = (p - bp) + (c - (s - bp))
+    fix = np.isfinite(s) & np.isfinite(e) & (e != 0) & ((s.view(np.int64) & 1) == 0)
+    if np.any(fix):
+        toward = np.where(e > 0, np.inf, -np.inf)
+        s = np.where(fix, np.nextafter(s, toward), s)
+    with np.errstate(over="ignore"):
+        return s.astype(np.float32)
+
+
+def quantize_np(A, hi_prec=True):
+    """Per-(row, 32-block) quantization, as quantize_A_i16 / quantize_A
+    (kernel/quantized_matmul.cpp:215-258).  Returns q int16, sa f32, sq i32."""
+    A = np.ascontiguousarray(A, np.float32)
+    M, K = A.shape
+    qmax = 32767 if hi_prec else 127
+    blk = A.reshape(M, K // 32, 32)
+    mag = np.abs(blk)
+    amax = np.max(np.where(np.isnan(mag), np.float32(0), mag), axis=2, initial=np.float32(0))
+    sa = (amax / np.float32(qmax)).astype(np.float32)
+    with np.errstate(divide="ignore"):
+        inv = np.where(sa > 0, np.float32(1) / np.where(sa > 0, sa, np.float32(1)),
+                       np.float32(0)).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        p = (blk * inv[:, :, None]).astype(np.float32)
+    fin = np.isfinite(p)
+    r = np.rint(np.where(fin, p, np.float32(0))).astype(np.int64)
+    q = np.clip(r, -qmax, qmax).astype(np.int16)
+    sq = q.astype(np.int32).sum(axis=2, dtype=np.int32)
+    return q.reshape(M, K), sa, sq
+
+
+def unpack_nbits_np(qweight, scales, qzeros, N, K, bits):
+    """MatMulNBits -> signed b [N,K] int16 and f32 scales [N,K/32]
+    (breeze/quant.py:9-58 integer form)."""
+    nblk = K // 32
+    sc = np.asarray(scales)
+    sb = np.ascontiguousarray(sc.reshape(N, nblk)).astype(np.float32)
+    if bits == 8:
+        raw = np.ascontiguousarray(qweight).reshape(N, nblk, 32).astype(np.int16)
+        return (raw - 128).reshape(N, K), sb
+    qw = np.ascontiguousarray(qweight).reshape(N, nblk, 16)
+    nib = np.empty((N, nblk, 32), np.int16)
+    nib[:, :, 0::2] = qw & 15
+    nib[:, :, 1::2] = qw >> 4
+    if qzeros is not None and np.size(qzeros):
+        packed = (nblk + 1) // 2
+        qz = np.ascontiguousarray(qzeros).reshape(N, packed)
+        zp = np.empty((N, packed * 2), np.int16)
+        zp[:, 0::2] = qz & 15
+        zp[:, 1::2] = qz >> 4
+        zp = zp[:, :nblk]
+    else:
+        zp = np.full((N, nblk), 8, np.int16)
+    return (nib - zp[:, :, None]).reshape(N, K), sb
+
+
+def block_dots_np(q, b):
+    """cs[m,n,j] = sum_k q*b within block j (int64 arithmetic, int32 result)."""
+    M, K = q.shape
+    N = b.shape[0]
+    nblk = K // 32
+    qb = q.reshape(M, nblk, 32).astype(np.int64)
+    bb = b.reshape(N, nblk, 32).astype(np.int64)
+    cs = np.einsum("mjk,njk->mnj", qb, bb, optimize=True)
+    return cs.astype(np.int32)
+
+
+def chain_np(cs, sa, sb):
+    """acc = fma(sa, f32(cs) * sb, acc) over blocks in order, from +0
+    (kernel/quantized_matmul.cpp:311-315)."""
+    M, N, nblk = cs.shape
+    acc = np.zeros((M, N), np.float32)
+    for j in range(nblk):
+        f = (cs[:, :, j].astype(np.float32) * sb[None, :, j]).astype(np.float32)
+        acc = fma_f32(np.broadcast_to(sa[:, j:j + 1], (M, N)), f, acc)
+    return acc
+
+
+def matmul_np(qweight, scales, qzeros, N, K, bits, A, hi_prec=True, want_cs=False):
+    b, sb = unpack_nbits_np(qweight, scales, qzeros, N, K, bits)
+    q, sa, _ = quantize_np(A, hi_prec)
+    cs = block_dots_np(q, b)
+    C = chain_np(cs, sa, sb)
+    return (C, cs) if want_cs else C
+
+
+# ---------------------------------------------------------------- float contract
+
+def dequantize_matmul_nbits(qweight, scales, qzeros, *, bits, block_size, K, N):
+    """Dense fp32 W [K,N] with w = (q - zp) * scale (breeze/quant.py:9-58)."""
+    if bits not in (4, 8):
+        raise NotImplementedError(f"bits={bits}")
+    nb = (K + block_size - 1) // block_size
+    sc = np.asarray(scales, np.float32).reshape(N, nb)
+    if bits == 8:
+        q = np.ascontiguousarray(qweight).reshape(N, nb, block_size).astype(np.float32)
+        if qzeros is not None and np.size(qzeros):
+            zp = np.ascontiguousarray(qzeros).reshape(N, nb).astype(np.float32)
+        else:
+            zp = np.full((N, nb), 128.0, np.float32)
+    else:
+        qw = np.ascontiguousarray(qweight).reshape(N, nb, block_size // 2)
+        q = np.empty((N, nb, block_size), np.float32)
+        q[:, :, 0::2] = qw & 15
+        q[:, :, 1::2] = qw >> 4
+        if qzeros is not None and np.size(qzeros):
+            packed = (nb + 1) // 2
+            qz = np.ascontiguousarray(qzeros).reshape(N, packed)
+            zp = np.empty((N, packed * 2), np.float32)
+            zp[:, 0::2] = qz & 15
+            zp[:, 1::2] = qz >> 4
+            zp = zp[:, :nb]
+        else:
+            zp = np.full((N, nb), 8.0, np.float32)
+    w = (q - zp[:, :, None]) * sc[:, :, None]
+    return np.ascontiguousarray(w.reshape(N, nb * block_size)[:, :K].T)
+
+
+def compare_logits(actual, expected, min_cosine):
+    """Minimum row cosine, as breeze/validation.py:5-17 computes it."""
+    a = np.asarray(actual, np.float64).reshape(-1, actual.shape[-1])
+    b = np.asarray(expected, np.float64).reshape(a.shape)
+    denom = np.linalg.norm(a, axis=1) * np.linalg.norm(b, axis=1)
+    sim = np.divide((a * b).sum(axis=1), denom, out=np.zeros(len(a)), where=denom != 0)
+    sim[denom == 0] = np.all(a[denom == 0] == b[denom == 0], axis=1)
+    return float(sim.min())
+
+
+def rel_err(actual, expected):
+    """max|C - C_ref| / max|C_ref| (breeze/cpu_backend.py:269)."""
+    return float(np.max(np.abs(actual.astype(np.float64) - expected)) /
+                 (np.max(np.abs(expected.astype(np.float64))) + 1e-30))
+
+
+# ---------------------------------------------------------------- workloads
+
+CONFIGS = {
+    # name: (bits, M, K, N, scale group in 32-blocks (None = per column), seed, outliers)
+    "w8_gemv": (8, 1, 4096, 4096, None, 1, False),
+    "w4_gemv": (4, 1, 4096, 12288, 4, 2, False),
+    "w4_decode": (4, 8, 12288, 4096, 4, 3, True),
+    "w8_prefill": (8, 512, 5120, 17408, None, 4, False),
+    "w8_lmhead": (8, 1, 5120, 151936, None, 5, False),
+}
+
+
+def make_weights(rng, bits, N, K, group):
+    """Seeded MatMulNBits weights and fp32 [N, K/32] scales.
+
+    W8: w uniform in [-127,127] stored as uint8 w+128 (zero point 128);
+        scales |N(0,0.02)|/127 per column, repeated over the K/32 blocks.
+    W4: w uniform in [-8,7] stored as nibbles w+8, low nibble = even k;
+        scales |N(0,0.02)|/7 per (column, group of `group` blocks)."""
+    nblk = K // 32
+    if bits == 8:
+        w = rng.integers(-127, 128, (N, K), dtype=np.int16)
+        qweight = (w + 128).astype(np.uint8).reshape(N, nblk, 32)
+        s = (np.abs(rng.normal(0.0, 0.02, N)) / 127).astype(np.float32)
+        scales = np.ascontiguousarray(np.repeat(s[:, None], nblk, axis=1))
+    else:
+        w = rng.integers(-8, 8, (N, K), dtype=np.int16)
+        nib = (w + 8).astype(np.uint8)
+        qweight = np.ascontiguousarray((nib[:, 0::2] | (nib[:, 1::2] << 4)).reshape(N, nblk, 16))
+        if group is None:
+            g = (np.abs(rng.normal(0.0, 0.02, N)) / 7).astype(np.float32)
+            scales = np.ascontiguousarray(np.repeat(g[:, None], nblk, axis=1))
+        else:
+            g = (np.abs(rng.normal(0.0, 0.02, (N, nblk // group))) / 7).astype(np.float32)
+            scales = np.ascontiguousarray(np.repeat(g, group, axis=1))
+    return qweight, scales
+
+
+def make_config(name, rows=None):
+    """Inputs of one workload: dict(qweight, scales, qzeros=None, A, bits, K, N).
+
+    One default_rng(seed) stream per workload, drawn as weights, scales,
+    activations; the W4 decode workload draws 8 rows (and its 1% x20
+    outliers) once and keeps the first `rows`."""
+    bits, M, K, N, group, seed, outliers = CONFIGS[name]
+    rng = np.random.default_rng(seed)
+    qweight, scales = make_weights(rng, bits, N, K, group)
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    if outliers:
+        mask = rng.random((M, K)) < 0.01
+        A[mask] *= np.float32(20)
+    if rows is not None:
+        A = np.ascontiguousarray(A[:rows])
+    return dict(qweight=qweight, scales=scales, qzeros=None, A=A, bits=bits, K=K, N=N)
+
+
+# ---------------------------------------------------------------- reference build
+
+class Ref:
+    """The reference kernel, compiled from kernel/quantized_matmul.cpp into
+    oracle/_ref (never vendored).  Same C ABI as the product library."""
+
+    def __init__(self, path=REF_PATH, threads=1):
+        lib = ctypes.CDLL(path)
+        lib.i4_prepack_onnx.restype = _vp
+        lib.i4_prepack_onnx.argtypes = [_vp] * 3 + [_i] * 4
+        lib.i4_prepack.restype = _vp
+        lib.i4_prepack.argtypes = [_vp] * 4 + [_i] * 4
+        lib.i4_matmul.argtypes = [_vp, _vp, _i, _vp]
+        lib.i4_matmul.restype = None
+        lib.i4_free.argtypes = [_vp]
+        for name in ("i4_set_threads", "i4_set_hi_prec", "i4_set_numa_split"):
+            getattr(lib, name).argtypes = [_i]
+            getattr(lib, name).restype = None
+        lib.i4_set_numa_split(1 << 30)
+        lib.i4_set_threads(threads)
+        self.lib = lib
+
+    def prepack(self, qweight, scales, qzeros, N, K, bits):
+        qw = np.ascontiguousarray(qweight, np.uint8)
+        sc = np.asarray(scales)
+        sbits = 16 if sc.dtype == np.float16 else 32
+        sc = np.ascontiguousarray(sc, np.float16 if sbits == 16 else np.float32)
+        qz = None if qzeros is None else np.ascontiguousarray(qzeros, np.uint8)
+        h = self.lib.i4_prepack_onnx(_p(qw), _p(sc), _p(qz), N, K, bits, sbits)
+        if not h:
+            raise MemoryError("reference prepack returned NULL")
+        return h
+
+    def matmul(self, h, A, N, hi_prec=True):
+        A = np.ascontiguousarray(A, np.float32)
+        C = np.empty((A.shape[0], N), np.float32)
+        self.lib.i4_set_hi_prec(int(bool(hi_prec)))
+        self.lib.i4_matmul(h, _p(A), A.shape[0], _p(C))
+        return C
+
+    def free(self, h):
+        if h:
+            self.lib.i4_free(h)
+
+    def run(self, qweight, scales, qzeros, N, K, bits, A, hi_prec=True):
+        h = self.prepack(qweight, scales, qzeros, N, K, bits)
+        try:
+            return self.matmul(h, A, N, hi_prec)
+        finally:
+            self.free(h)
+
+
+def ref_available():
+    return os.path.exists(REF_PATH)

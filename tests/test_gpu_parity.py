@@ -1,0 +1,187 @@
+"""GPU parity: the HIP path against the C restatement of the reference.
+
+Bar: bit-exact FP32 outputs and bit-exact per-block INT32 integers on the
+same seeded inputs (the oracle is itself pinned bit-for-bit against the
+compiled reference kernel, tests/test_oracle_*.py).  Cases follow the
+reference's own tests: tests/test_cpu_packing.py:70-96 (shapes, bits,
+fp16/fp32 scales, explicit zero points, rows 1 and 9, both activation modes),
+tests/test_qwen35_cpu.py:196-208 (projection widths), plus the benchmark
+workloads.
+"""
+import numpy as np
+import pytest
+
+from conftest import bits_equal, rng_weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_both(hb, torch, h, A, N):
+    """Host-pointer entry point and device-pointer entry point."""
+    c_host = hb.matmul(h, A, N)
+    c_dev = hb.matmul(h, torch.from_numpy(A).cuda(), N)
+    torch.cuda.synchronize()
+    return c_host, c_dev.cpu().numpy()
+
+
+@pytest.mark.parametrize("N,K", [(16, 32), (48, 96), (64, 512), (32, 4096)])
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+@pytest.mark.parametrize("explicit_zeros", [False, True])
+def test_matmul_bit_exact(gpu, hb, orc, hi_prec, N, K, bits, dtype, explicit_zeros):
+    if bits == 8 and explicit_zeros:
+        pytest.skip("INT8 takes no explicit zero points")
+    rng = np.random.default_rng(N + K + bits)
+    qw, sc, qz = rng_weights(rng, N, K, bits, dtype, explicit_zeros)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        for hp in (False, True):
+            hb.set_hi_prec(hp)
+            for rows in (1, 3, 8, 9, 17):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
+                c_host, c_dev = _run_both(hb, gpu, h, A, N)
+                assert bits_equal(c_host, want), (hp, rows, np.max(np.abs(c_host - want)))
+                assert bits_equal(c_dev, want), (hp, rows)
+    finally:
+        hb.free(h)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("explicit_zeros", [False, True])
+def test_block_integers_exact(gpu, hb, orc, hi_prec, bits, explicit_zeros):
+    if bits == 8 and explicit_zeros:
+        pytest.skip("INT8 takes no explicit zero points")
+    N, K = 64, 1024
+    rng = np.random.default_rng(11 + bits)
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
+    A = (rng.normal(size=(9, K)) * rng.choice([1e-3, 1.0, 50.0], size=(9, 1))).astype(np.float32)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        for hp in (False, True):
+            hb.set_hi_prec(hp)
+            _, cs_want = orc.matmul(qw, sc, qz, N, K, bits, A, hp, want_cs=True)
+            cs = hb.block_dots(h, gpu.from_numpy(A).cuda(), N, K).cpu().numpy()
+            np.testing.assert_array_equal(cs, cs_want)
+    finally:
+        hb.free(h)
+
+
+@pytest.mark.parametrize("K,N,bits", [(5120, 48, 8), (17408, 16, 4), (6144, 64, 8), (4096, 32, 4)])
+def test_projection_widths(gpu, hb, orc, hi_prec, K, N, bits):
+    """tests/test_qwen35_cpu.py:196-208 shapes and seed, HP mode, bit-exact."""
+    rng = np.random.default_rng(3)
+    qw = rng.integers(0, 256, (N, K // 32, 32 * bits // 8), dtype=np.uint8)
+    scales = rng.uniform(0.001, 0.005, (N, K // 32)).astype(np.float32)
+    a = rng.normal(size=(3, K)).astype(np.float32)
+    hb.set_hi_prec(True)
+    h = hb.prepack(qw, scales, None, K, N, bits=bits)
+    try:
+        got = hb.matmul(h, a, N)
+    finally:
+        hb.free(h)
+    assert bits_equal(got, orc.matmul(qw, scales, None, N, K, bits, a, True))
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_legacy_layout_entry_point(gpu, hb, orc, hi_prec, bits):
+    """i4_prepack of the NumPy-built legacy layout == i4_prepack_onnx."""
+    N, K = 48, 96
+    rng = np.random.default_rng(7)
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float16, bits == 4)
+    fast = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    old = hb._prepack_numpy(qw, sc, qz, K, N, bits=bits)
+    try:
+        uf, uo = hb.unpack(fast), hb.unpack(old)
+        for key in ("qweight", "scales", "zp", "corr_delta"):
+            np.testing.assert_array_equal(uf[key], uo[key])
+        for hp in (False, True):
+            hb.set_hi_prec(hp)
+            for rows in (1, 9):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                assert bits_equal(hb.matmul(fast, A, N), hb.matmul(old, A, N))
+    finally:
+        hb.free(fast)
+        hb.free(old)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_legacy_corr_is_honoured(gpu, hb, orc, hi_prec, bits):
+    """A corr that disagrees with the weights (kernel/benchmark_matmul.cpp
+    passes zeros) changes the result exactly as the reference's hp_combine."""
+    N, K, nblk = 32, 128, 4
+    rng = np.random.default_rng(21)
+    gb = 64 if bits == 8 else 32
+    B = rng.integers(0, 256, (N // 16, nblk, 8, gb), dtype=np.uint8)
+    scale = rng.uniform(0.001, 0.02, (N // 16, nblk, 16)).astype(np.float32)
+    zp = rng.integers(0, 16, (N // 16, nblk, 16), dtype=np.int8) if bits == 4 else None
+    corr = rng.integers(-5000, 5000, (N // 16, nblk, 16), dtype=np.int32)
+    corr.reshape(-1)[:8] = 0
+    h = hb._lib.i4_prepack(hb._p(B), hb._p(scale), hb._p(zp), hb._p(corr), N, K, nblk, bits)
+    assert h, hb.last_error()
+    try:
+        for hp in (False, True):
+            hb.set_hi_prec(hp)
+            A = rng.normal(size=(5, K)).astype(np.float32)
+            want = orc.matmul_legacy(B, scale, zp, corr, N, K, bits, A, hp)
+            assert bits_equal(hb.matmul(h, A, N), want)
+    finally:
+        hb.free(h)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_unpack_round_trip(gpu, hb, bits):
+    """The device layout holds exactly the MatMulNBits inputs."""
+    N, K = 80, 160
+    rng = np.random.default_rng(5)
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float16, bits == 4)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        u = hb.unpack(h)
+        np.testing.assert_array_equal(u["qweight"], qw)
+        np.testing.assert_array_equal(u["scales"], sc.astype(np.float32))
+        if bits == 4:
+            zpf = np.empty((N, 2 * qz.shape[1]), np.uint8)
+            zpf[:, 0::2] = qz & 15
+            zpf[:, 1::2] = qz >> 4
+            np.testing.assert_array_equal(u["zp"], zpf[:, :K // 32])
+        assert not u["corr_delta"].any()
+    finally:
+        hb.free(h)
+
+
+def test_row_slices_match_single_rows(gpu, hb, orc, hi_prec):
+    """Row m of an M-row call equals a 1-row call (reference property,
+    tests/test_cpu_packing.py:155-168)."""
+    N, K = 64, 768
+    rng = np.random.default_rng(9)
+    qw, sc, _ = rng_weights(rng, N, K, 4)
+    h = hb.prepack(qw, sc, None, K, N, bits=4)
+    hb.set_hi_prec(True)
+    try:
+        A = rng.normal(size=(19, K)).astype(np.float32)
+        full = hb.matmul(h, A, N)
+        for m in (0, 7, 8, 18):
+            assert bits_equal(hb.matmul(h, A[m:m + 1], N)[0], full[m])
+    finally:
+        hb.free(h)
+
+
+def test_argmax_first_max_semantics(gpu, hb, hi_prec):
+    """Ties, -0/+0 and NaN follow numpy.argmax on the computed logits."""
+    N, K = 4096, 64
+    rng = np.random.default_rng(4)
+    # Identical weight columns produce exact ties.
+    col = rng.integers(0, 256, (1, 2, 32), dtype=np.uint8)
+    qw = np.repeat(col, N, axis=0)
+    sc = np.full((N, 2), 0.01, np.float32)
+    sc[::7] = 0.02
+    h = hb.prepack(qw, sc, None, K, N, bits=8)
+    hb.set_hi_prec(True)
+    try:
+        A = gpu.from_numpy(rng.normal(size=(3, K)).astype(np.float32)).cuda()
+        logits, idx = hb.matmul_argmax(h, A, N)
+        gpu.cuda.synchronize()
+        np.testing.assert_array_equal(idx.cpu().numpy(), np.argmax(logits.cpu().numpy(), axis=1))
+    finally:
+        hb.free(h)
