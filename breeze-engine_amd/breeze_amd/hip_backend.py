@@ -26,6 +26,35 @@ _i = ctypes.c_int
 
 _lib = None
 _native_prepack = None
+
+
+def _bind_torch_runtime():
+    """Load PyTorch's own HIP runtime (by path, without importing torch) before
+    the library, so the library's libamdhip64.so.7 dependency resolves to it.
+
+    PyTorch-ROCm ships its own libamdhip64/libhsa-runtime64 and asks for them
+    by a name that does not match the system runtime's soname; if the system
+    runtime were loaded first the process would hold two HSA runtimes and
+    only the first to initialise would see the GPU."""
+    import importlib.util
+
+    try:
+        spec = importlib.util.find_spec("torch")
+    except (ImportError, ValueError):
+        return
+    for d in (spec.submodule_search_locations or []) if spec else []:
+        path = os.path.join(d, "lib", "libamdhip64.so")
+        if os.path.exists(path):
+            ctypes.CDLL(path, mode=ctypes.RTLD_GLOBAL)
+            return
+
+
+if os.environ.get("BREEZE_HIP_SYSTEM_RUNTIME") != "1":
+    try:
+        _bind_torch_runtime()
+    except OSError:
+        pass
+
 try:
     _lib = ctypes.CDLL(_SO)
     _lib.i4_prepack.restype = _vp
