@@ -22,10 +22,9 @@
 //   * INT4 weights stay raw nibbles 0..15 (valid signed bytes); the zero
 //     point is applied as cs -= zp * sum(q), with sum(q) per (m, j) from the
 //     quantizer.  INT8 weights are stored as signed bytes (raw ^ 0x80).
-//   * The FP32 chain is evaluated in block order per (m, n): waves compute
-//     f = f32(cs)*scale for a segment of blocks into LDS, then one lane per
-//     (m, n) folds the segment into its accumulator.  Bit-identical to the
-//     reference for every M, so row m of an M-row call equals a 1-row call.
+//   * The FP32 chain is evaluated in block order per (m, n), exactly as the
+//     reference does, so outputs are bit-identical for every M and row m of
+//     an M-row call equals a 1-row call.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -66,31 +65,37 @@ bool hip_ok(hipError_t e, const char* what) {
     return false;
 }
 
-// ------------------------------------------------------------------ layout constants
+// ------------------------------------------------------------------ layout
 
-// Position p of an 8-byte MFMA operand holds k = 8*octet + kPerm8[p]: the
-// order in which the INT4 unpack (low nibbles, then high nibbles of four
-// packed bytes) delivers weights.  INT8 weights and the activations use the
-// same order, so A and B always agree on k.
-constexpr int kPerm8[8] = {0, 2, 4, 6, 1, 3, 5, 7};
-
-constexpr int kWaves = 4;          // waves per workgroup
-constexpr int kChunksPerWave = 2;  // 16-byte weight chunks per wave per segment
-constexpr int kRowsPerWG = 8;      // activation rows per workgroup (two MFMA row groups)
+// Device weight layout: chunk (t, c) of 16-column tile t is 64 lanes x 16
+// bytes; lane l serves column 16t + (l & 15) and k-octet (l >> 4) of each
+// block -- the B operand of v_mfma_i32_16x16x32_i8, in natural k order.
+//   INT8: 2 blocks per chunk, 8 signed bytes (raw ^ 0x80) per block.
+//   INT4: 4 blocks per chunk, one dword per block whose byte b holds the
+//         nibbles of k = 8*octet + b (low) and k = 8*octet + 4 + b (high), so
+//         `w & 0x0F0F0F0F` and `(w >> 4) & 0x0F0F0F0F` are k 0..3 and 4..7.
+// Activation record per (row, block): 64 bytes, part 0 then part 1, each 32
+// bytes in natural k order: INT16 mode h then l (signed halves), INT8 mode q
+// then zeros.
 
 constexpr uint32_t kMagic = 0xB2EE2E51u;
+constexpr int kFlagZp = 1, kFlagDl = 2, kFlagScBlk = 4;
 
 struct Handle {
     uint32_t magic;
     int N, K, nblk, bits;  // bits of the device representation
-    int nbg;               // 16-byte chunks per column tile along K
+    int nbg;               // 16-byte chunks per tile along K
+    int nblk_pad;          // nbg * blocks per chunk
+    int nblk4;             // nblk rounded up to 4
     int sc_shift, ngrp, sc_group;
-    bool has_zp, has_dl;
+    bool sc_blk;           // scales stored per block [N][nblk_pad]
+    bool has_zp, has_dl;   // explicit zero points / legacy corr supplied
+    bool extra;            // per-block scale, zp (INT4) and corr arrays materialized
     int device;
-    uint4* W;    // [N/16][nbg][64 lanes] 16-byte chunks
-    float* S;    // [N][ngrp]
-    int8_t* Z;   // [N][nblk] zero points, INT4 only, NULL = all 8
-    int32_t* D;  // [N][nblk] legacy corr delta, NULL = none
+    uint4* W;    // [N/16][nbg][64] 16-byte chunks
+    float* S;    // [N][ngrp], or [N][nblk_pad] when sc_blk
+    int8_t* Z;   // [N][nblk4] zero points (INT4 extra handles only)
+    int32_t* D;  // [N][nblk_pad] legacy corr delta (extra handles only)
     size_t dev_bytes;
 };
 
@@ -103,13 +108,94 @@ Handle* as_handle(void* p) {
     return h;
 }
 
-// ------------------------------------------------------------------ kernels
+// ------------------------------------------------------------------ device helpers
 
-// MatMulNBits bytes -> 16-byte lane chunks.  Chunk (t, cg) of a 16-column
-// tile is 64 lanes x 16 bytes; lane l serves column 16t + (l & 15) and
-// k-octet (l >> 4) of each block, i.e. exactly the B operand of
-// v_mfma_i32_16x16x32_i8.  INT8: 2 blocks per chunk, bytes kPerm8-ordered
-// and xor 0x80.  INT4: 4 blocks per chunk, the octet's 4 packed bytes as is.
+__device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ inline int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+__device__ inline int dpp_mirror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
+
+// max over the 8 lanes of an aligned lane octet; inputs are never NaN.
+__device__ inline float max8(float x) {
+    float y = __int_as_float(dpp_xor1(__float_as_int(x)));
+    x = y > x ? y : x;
+    y = __int_as_float(dpp_xor2(__float_as_int(x)));
+    x = y > x ? y : x;
+    y = __int_as_float(dpp_mirror8(__float_as_int(x)));
+    return y > x ? y : x;
+}
+
+// min over each 16-lane row (row rotates by 1, 2, 4, 8).
+__device__ inline int min16(int x) {
+    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x121, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x122, 0xF, 0xF, false));
+    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
+    return min(x, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+}
+
+__device__ inline int sum8(int x) {
+    x += dpp_xor1(x);
+    x += dpp_xor2(x);
+    return x + dpp_mirror8(x);
+}
+
+// Quantizes one 32-block with 8 lanes, 4 consecutive k per lane (lane e of
+// the octet holds k = 4e..4e+3).  All 64 lanes of the wave must call it.
+// Returns the block scale and sum(q) in every lane of the octet, and this
+// lane's 4 bytes of record part 0 and part 1.
+template <bool HP>
+__device__ inline void quant8(float4 v, float& s_out, int& sum_out, uint32_t& p0, uint32_t& p1) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(x[i]);
+        amax = a > amax ? a : amax;
+    }
+    amax = max8(amax);
+    constexpr int qmax = HP ? 32767 : 127;
+    const float s = amax / (float)qmax;
+    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+    int sum = 0;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float prod = x[i] * inv;
+        int q = 0;
+        if (__builtin_isfinite(prod)) {
+            q = (int)rintf(prod);
+            q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
+        }
+        sum += q;
+        if (HP) {
+            const uint32_t u = (uint32_t)(q + 32768);
+            w0 |= (((u >> 8) ^ 0x80u) & 0xFFu) << (8 * i);
+            w1 |= (((u & 0xFFu) ^ 0x80u) & 0xFFu) << (8 * i);
+        } else {
+            w0 |= ((uint32_t)q & 0xFFu) << (8 * i);
+        }
+    }
+    s_out = s;
+    sum_out = sum8(sum);
+    p0 = w0;
+    p1 = w1;
+}
+
+__device__ inline uint64_t unpack_b(const uint4& w, int jb, int bits) {
+    if (bits == 8) {
+        const uint32_t lo = jb == 0 ? w.x : w.z, hi = jb == 0 ? w.y : w.w;
+        return (uint64_t)hi << 32 | lo;
+    }
+    const uint32_t x = jb == 0 ? w.x : jb == 1 ? w.y : jb == 2 ? w.z : w.w;
+    return (uint64_t)((x >> 4) & 0x0F0F0F0Fu) << 32 | (x & 0x0F0F0F0Fu);
+}
+
+__device__ inline v4i mfma16(uint64_t a, uint64_t b) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, v4i{0, 0, 0, 0}, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ repack
+
+// MatMulNBits bytes (or signed bytes, raw_signed) -> device chunk layout.
 __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint4* __restrict__ out, int N,
                               int nblk, int nbg, int bits, int raw_signed) {
     const size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -122,198 +208,116 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint4* __restrict
     const int n = t * 16 + (lane & 15), oct = lane >> 4;
     uint32_t w[4] = {0, 0, 0, 0};
     if (bits == 8) {
-        const uint8_t x = raw_signed ? 0 : 0x80;
+        const uint32_t x = raw_signed ? 0u : 0x80808080u;
         for (int hb = 0; hb < 2; ++hb) {
             const int j = cg * 2 + hb;
             if (j >= nblk) continue;
             const uint8_t* src = raw + ((size_t)n * nblk + j) * 32 + oct * 8;
             uint32_t lo = 0, hi = 0;
-            for (int p = 0; p < 4; ++p) lo |= (uint32_t)(uint8_t)(src[kPerm8[p]] ^ x) << (8 * p);
-            for (int p = 4; p < 8; ++p) hi |= (uint32_t)(uint8_t)(src[kPerm8[p]] ^ x) << (8 * (p - 4));
-            w[2 * hb] = lo;
-            w[2 * hb + 1] = hi;
+            for (int p = 0; p < 4; ++p) lo |= (uint32_t)src[p] << (8 * p);
+            for (int p = 0; p < 4; ++p) hi |= (uint32_t)src[4 + p] << (8 * p);
+            w[2 * hb] = lo ^ x;
+            w[2 * hb + 1] = hi ^ x;
         }
     } else {
         for (int q = 0; q < 4; ++q) {
             const int j = cg * 4 + q;
             if (j >= nblk) continue;
             const uint8_t* src = raw + ((size_t)n * nblk + j) * 16 + oct * 4;
-            w[q] = (uint32_t)src[0] | (uint32_t)src[1] << 8 | (uint32_t)src[2] << 16 |
-                   (uint32_t)src[3] << 24;
+            uint32_t x = 0;
+            for (int b = 0; b < 4; ++b) {
+                const uint32_t lo = (src[b >> 1] >> (4 * (b & 1))) & 15u;
+                const uint32_t hi = (src[2 + (b >> 1)] >> (4 * (b & 1))) & 15u;
+                x |= (lo | hi << 4) << (8 * b);
+            }
+            w[q] = x;
         }
     }
     out[o] = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-// Activation quantization, one thread per (row, 32-block).  Writes the
-// 64-byte record [part 0: 32 bytes][part 1: 32 bytes], each kPerm8-ordered
-// per octet: INT16 mode part 0 = h, part 1 = l (signed halves); INT8 mode
-// part 0 = q, part 1 = 0.  Also the block scale s and sum(q).
+// ------------------------------------------------------------------ quantize
+
+// Stand-alone activation quantizer: 8 lanes per (row, block).  Records go
+// to Aq [M][nblk][64 B]; scale and sum(q) to Sa/Sq [M][nblk4].
 template <bool HP>
-__global__ void quantize_kernel(const float* __restrict__ A, int M, int K, int nblk,
-                                uint4* __restrict__ Aq, float* __restrict__ Sa,
-                                int* __restrict__ Sq) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= M * nblk) return;
-    const int m = idx / nblk, j = idx - m * nblk;
-    const float4* src = reinterpret_cast<const float4*>(A + (size_t)m * K + 32 * j);
-    float v[32];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float4 x = src[i];
-        v[4 * i] = x.x;
-        v[4 * i + 1] = x.y;
-        v[4 * i + 2] = x.z;
-        v[4 * i + 3] = x.w;
-    }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float a = fabsf(v[i]);
-        amax = a > amax ? a : amax;
-    }
-    constexpr int qmax = HP ? 32767 : 127;
-    const float s = amax / (float)qmax;
-    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-    int sum = 0;
-    uint8_t p0[32], p1[32];
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-        const float prod = v[i] * inv;
-        int q = 0;
-        if (__builtin_isfinite(prod)) {
-            q = (int)rintf(prod);
-            q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
-        }
-        sum += q;
-        if (HP) {
-            const unsigned u = (unsigned)(q + 32768);
-            p0[i] = (uint8_t)((u >> 8) ^ 0x80u);
-            p1[i] = (uint8_t)((u & 0xFFu) ^ 0x80u);
-        } else {
-            p0[i] = (uint8_t)(int8_t)q;
-            p1[i] = 0;
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ A, int M, int K,
+                                                       int nblk, int nblk4, uint8_t* __restrict__ Aq,
+                                                       float* __restrict__ Sa, int* __restrict__ Sq) {
+    const int gtid = blockIdx.x * 256 + threadIdx.x;
+    const int blk = gtid >> 3, e = gtid & 7;
+    const bool valid = blk < M * nblk;
+    const int m = valid ? blk / nblk : 0, j = valid ? blk - m * nblk : 0;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) v = *reinterpret_cast<const float4*>(A + (size_t)m * K + 32 * j + 4 * e);
+    float s;
+    int sum;
+    uint32_t p0, p1;
+    quant8<HP>(v, s, sum, p0, p1);
+    if (valid) {
+        uint8_t* rec = Aq + ((size_t)m * nblk + j) * 64;
+        *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
+        *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
+        if (e == 0) {
+            Sa[(size_t)m * nblk4 + j] = s;
+            Sq[(size_t)m * nblk4 + j] = sum;
         }
     }
-    uint32_t w[16];
-#pragma unroll
-    for (int part = 0; part < 2; ++part)
-#pragma unroll
-        for (int oct = 0; oct < 4; ++oct)
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint32_t x = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const int k = oct * 8 + kPerm8[half * 4 + b];
-                    x |= (uint32_t)(part ? p1[k] : p0[k]) << (8 * b);
-                }
-                w[part * 8 + oct * 2 + half] = x;
-            }
-    uint4* dst = Aq + (size_t)idx * 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) dst[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
-    Sa[idx] = s;
-    Sq[idx] = sum;
 }
 
-struct QmmArgs {
+// ------------------------------------------------------------------ decode GEMV (M <= 8)
+//
+// Persistent: one workgroup of 16 waves per CU, each owning a contiguous
+// range of 16-column tiles for up to 4 activation rows (M 5..8 uses two row
+// groups, placed on the same XCD so the second weight read hits its L2).
+// Waves 0..14 are producers: they stream 1 KB weight chunks in batches (all
+// loads of a batch issued back to back, then consumed), run the MFMA and the
+// in-lane epilogue, and put f = f32(cs) * scale into an LDS ring.  Wave 15
+// runs the ordered FP32 chain acc = fma(s, f, acc) over the ring in block
+// order, following the producers through their LDS progress counters; it
+// writes C (and the per-workgroup argmax partials).  Activations are
+// quantized into LDS in the prologue when small (FUSED), else copied from
+// the stand-alone quantizer.  The first batch is issued before the prologue
+// work, so the quantization overlaps the first weight loads.
+//
+// All weight loads live in straight-line code: the compiler's load waits
+// are exact there, whereas a load carried around a loop back edge is
+// drained at the loop head.
+
+constexpr int kGemvWaves = 16;
+constexpr int kProducers = kGemvWaves - 1;
+constexpr int kChainBatch = 8;
+constexpr int kSpinLimit = 1 << 22;
+
+struct GemvArgs {
     const uint4* W;
     const float* S;
     const int8_t* Z;
     const int32_t* D;
-    const uint2* Aq;   // [M][nblk][8] 8-byte operand pieces
-    const float* Sa;   // [M][nblk]
-    const int* Sq;     // [M][nblk]
-    float* C;          // [M][N]
-    int32_t* Cs;       // [M][N][nblk] (block-dot export only)
-    int M, N, nblk, nbg, sc_shift, ngrp;
+    const float* A;        // fp32 [M][K] (FUSED)
+    const uint8_t* Aq;     // [M][nblk][64] records (not FUSED)
+    const float* Sa;       // [M][nblk4]
+    const int* Sq;         // [M][nblk4]
+    float* C;              // [M][N]
+    int32_t* Cs;           // [M][N][nblk] (block-dot export)
+    unsigned long long* part;  // [NG][M] argmax partials, or NULL
+    int* err;
+    int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
+    int ntiles, NG, RG, pair_xcd, ring_mask;
+    int lds_recs, lds_sa, lds_sq, lds_consts, lds_ring, lds_sync, lds_red;
 };
 
-template <int BITS, bool HP, bool HAS_ZP, bool HAS_DL, bool DOTS>
-__global__ __launch_bounds__(kWaves * 64) void qmm_kernel(QmmArgs a) {
-    constexpr int JG = BITS == 8 ? 2 : 4;  // blocks per 16-byte chunk
-    constexpr int SEG = kWaves * kChunksPerWave * JG;
-    __shared__ float fbuf[kRowsPerWG][SEG][16];
+// Per-item loads of a producer lane.  EXTRA handles (explicit zero points,
+// legacy corr, scale groups smaller than a chunk) carry materialized
+// per-block arrays so every load is unconditional.
+template <int JG, bool EXTRA>
+struct Pre {
+    uint4 w;       // weights
+    float sc[EXTRA ? JG : 1];
+    int dl[EXTRA ? JG : 1];
+    uint32_t zp;   // INT4 zero points, one byte per block
+};
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t = blockIdx.x;
-    const int m0 = blockIdx.y * kRowsPerWG;
-    const int Mc = min(kRowsPerWG, a.M - m0);
-    const int nmf = (Mc + 3) >> 2;
-    // MFMA lane roles: B column / output column, k-octet / output row group.
-    const int col = lane & 15, grp = lane >> 4;
-    const int arow = lane & 15, arg = arow >> 2, ars = arow & 3;
-    const int n = t * 16 + col;
-    // Chain role of this thread in phase 2.
-    const int cm = threadIdx.x >> 4, ccol = threadIdx.x & 15;
-    float acc = 0.0f;
-
-    const int nseg = (a.nblk + SEG - 1) / SEG;
-    for (int s = 0; s < nseg; ++s) {
-        const int j0 = s * SEG;
-#pragma unroll
-        for (int c = 0; c < kChunksPerWave; ++c) {
-            const int cg = j0 / JG + wave * kChunksPerWave + c;
-            if (cg * JG >= a.nblk) break;
-            const uint4 wv = a.W[((size_t)t * a.nbg + cg) * 64 + lane];
-#pragma unroll
-            for (int jb = 0; jb < JG; ++jb) {
-                const int j = cg * JG + jb;
-                if (j >= a.nblk) break;
-                uint64_t bop;
-                if (BITS == 8) {
-                    const uint32_t lo = jb == 0 ? wv.x : wv.z, hi = jb == 0 ? wv.y : wv.w;
-                    bop = (uint64_t)hi << 32 | lo;
-                } else {
-                    const uint32_t w = jb == 0 ? wv.x : jb == 1 ? wv.y : jb == 2 ? wv.z : wv.w;
-                    bop = (uint64_t)((w >> 4) & 0x0F0F0F0Fu) << 32 | (w & 0x0F0F0F0Fu);
-                }
-                for (int mi = 0; mi < nmf; ++mi) {
-                    const int ml = mi * 4 + arg;
-                    uint64_t aop = 0;
-                    if (ars == 2) {
-                        aop = 0x0101010101010101ull;
-                    } else if (ars < 2 && ml < Mc) {
-                        const uint2 x = a.Aq[((size_t)(m0 + ml) * a.nblk + j) * 8 + ars * 4 + grp];
-                        aop = (uint64_t)x.y << 32 | x.x;
-                    }
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)aop, (long)bop,
-                                                                        v4i{0, 0, 0, 0}, 0, 0, 0);
-                    const int me = mi * 4 + grp;
-                    if (me < Mc) {
-                        const size_t row = (size_t)(m0 + me);
-                        int cs = HP ? d[0] * 256 + d[1] + d[2] * 128 : d[0];
-                        if (BITS == 4) {
-                            const int zp = HAS_ZP ? (int)a.Z[(size_t)n * a.nblk + j] : 8;
-                            cs -= zp * a.Sq[row * a.nblk + j];
-                        }
-                        if (HAS_DL) cs += (HP ? 256 : 1) * a.D[(size_t)n * a.nblk + j];
-                        if (DOTS) {
-                            a.Cs[(row * a.N + n) * a.nblk + j] = cs;
-                        } else {
-                            fbuf[me][j - j0][col] =
-                                (float)cs * a.S[(size_t)n * a.ngrp + (j >> a.sc_shift)];
-                        }
-                    }
-                }
-            }
-        }
-        if (!DOTS) {
-            __syncthreads();
-            if (cm < Mc) {
-                const int jn = min(SEG, a.nblk - j0);
-                const float* sa = a.Sa + (size_t)(m0 + cm) * a.nblk + j0;
-                for (int jj = 0; jj < jn; ++jj) acc = __builtin_fmaf(sa[jj], fbuf[cm][jj][ccol], acc);
-            }
-            __syncthreads();
-        }
-    }
-    if (!DOTS && cm < Mc) a.C[(size_t)(m0 + cm) * a.N + t * 16 + ccol] = acc;
-}
-
-// First-maximum argmax per row with numpy.argmax semantics.  Keys order by
-// value (NaN highest, -0 == +0) and then by lower index.
 __device__ inline unsigned long long argmax_key(float v, int idx) {
     uint32_t o;
     if (v != v) {
@@ -326,6 +330,504 @@ __device__ inline unsigned long long argmax_key(float v, int idx) {
     }
     return (unsigned long long)o << 32 | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
 }
+
+// Barrier that orders LDS only: outstanding global loads stay in flight.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ inline int lds_load_acq(int* p) {
+    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ inline void lds_store_rel(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+template <int BITS, bool HP, bool FUSED, bool DOTS, bool EXTRA>
+__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvArgs a) {
+    constexpr int JG = BITS == 8 ? 2 : 4;
+    constexpr int B = EXTRA ? 4 : 8;  // items per producer batch
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    int g, rg;
+    if (a.RG == 1) {
+        g = blockIdx.x;
+        rg = 0;
+    } else if (a.pair_xcd) {
+        const int b = blockIdx.x;
+        g = (b >> 4) * 8 + (b & 7);
+        rg = (b >> 3) & 1;
+    } else {
+        g = blockIdx.x >> 1;
+        rg = blockIdx.x & 1;
+    }
+    const int m0 = rg * 4;
+    const int Mr = min(4, a.M - m0);
+    const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
+    const int t_begin = g * base_t + min(g, rem_t);
+    const int nT = base_t + (g < rem_t ? 1 : 0);
+    const int TG = Mr == 1 ? 4 : (Mr == 2 ? 2 : 1);
+    const int TGs = Mr == 1 ? 2 : (Mr == 2 ? 1 : 0);
+    const int full_groups = nT / TG;
+    const int tg_last = nT - full_groups * TG;
+    const int per_group = TG * a.nbg;
+    const int items_full = full_groups * per_group;
+    const int n_items = nT * a.nbg;
+    constexpr int sstride = 4 * 16 * JG;  // floats per ring slot (4 rows, unused rows are scratch)
+
+    uint8_t* recs = smem + a.lds_recs;
+    float* sa_l = reinterpret_cast<float*>(smem + a.lds_sa);
+    int* sq_l = reinterpret_cast<int*>(smem + a.lds_sq);
+    float* ring = reinterpret_cast<float*>(smem + a.lds_ring);
+    int* prog = reinterpret_cast<int*>(smem + a.lds_sync);
+    int* chain_items = prog + kProducers;
+    int* abort_flag = prog + kProducers + 1;
+
+    // Items of this workgroup, in the order the chain consumes them: for
+    // each group of TG tiles, for each chunk c, the TG tiles side by side
+    // (the last group may hold tg_last < TG tiles).  Producer w walks items
+    // w, w+15, ... with an incremental iterator (no division per item).
+    struct It {
+        int i, gm, r;
+    };
+    auto it_at = [&](int i) {
+        It t;
+        t.i = i;
+        if (i < items_full) {
+            t.gm = i / per_group;
+            t.r = i - t.gm * per_group;
+        } else {
+            t.gm = full_groups;
+            t.r = i - items_full;
+        }
+        return t;
+    };
+    auto it_next = [&](It& t) {
+        t.i += kProducers;
+        if (t.i < items_full) {
+            t.r += kProducers;
+            while (t.r >= per_group) {
+                t.r -= per_group;
+                ++t.gm;
+            }
+        } else {
+            t.gm = full_groups;
+            t.r = t.i - items_full;
+        }
+    };
+    // -> (tile offset in this workgroup, chunk); past the end -> last item.
+    auto it_decode = [&](const It& t, int& toff, int& c) {
+        if (t.i >= n_items) {
+            toff = nT - 1;
+            c = a.nbg - 1;
+        } else if (t.i < items_full) {
+            c = t.r >> TGs;
+            toff = t.gm * TG + (t.r & (TG - 1));
+        } else if (tg_last == 1) {
+            c = t.r;
+            toff = full_groups * TG;
+        } else if (tg_last == 2) {
+            c = t.r >> 1;
+            toff = full_groups * TG + (t.r & 1);
+        } else {
+            c = (int)__umulhi((unsigned)t.r, 0x55555556u);  // r / 3
+            toff = full_groups * TG + (t.r - 3 * c);
+        }
+    };
+
+    const int col = lane & 15, grp = lane >> 4;
+    auto load_pre = [&](const It& t, Pre<JG, EXTRA>& p) {
+        int toff, c;
+        it_decode(t, toff, c);
+        const int tile = t_begin + toff;
+        const size_t n = (size_t)tile * 16 + col;
+        p.w = a.W[((size_t)tile * a.nbg + c) * 64 + lane];
+        if (EXTRA) {
+            if (JG == 4) {
+                const float4 s4 = *reinterpret_cast<const float4*>(a.S + n * a.nblk_pad + c * 4);
+                const int4 d4 = *reinterpret_cast<const int4*>(a.D + n * a.nblk_pad + c * 4);
+                p.sc[0] = s4.x;
+                p.sc[1 % JG] = s4.y;
+                p.sc[2 % JG] = s4.z;
+                p.sc[3 % JG] = s4.w;
+                p.dl[0] = d4.x;
+                p.dl[1 % JG] = d4.y;
+                p.dl[2 % JG] = d4.z;
+                p.dl[3 % JG] = d4.w;
+                p.zp = *reinterpret_cast<const uint32_t*>(a.Z + n * a.nblk4 + c * 4);
+            } else {
+                const float2 s2 = *reinterpret_cast<const float2*>(a.S + n * a.nblk_pad + c * 2);
+                const int2 d2 = *reinterpret_cast<const int2*>(a.D + n * a.nblk_pad + c * 2);
+                p.sc[0] = s2.x;
+                p.sc[1 % JG] = s2.y;
+                p.dl[0] = d2.x;
+                p.dl[1 % JG] = d2.y;
+            }
+        } else {
+            p.sc[0] = a.S[n * a.ngrp + ((c * JG) >> a.sc_shift)];
+        }
+    };
+
+    // Producer lane roles (A operand row/slot and k-octet; output row).
+    const int arow = lane & 15, arg = arow >> 2, ars = arow & 3, kq = lane >> 4;
+    const bool is_data = ars < 2 && arg < Mr;
+    const int data_base = a.lds_recs + arg * a.nblk * 64 + ars * 32 + kq * 8;
+    const int const_base = a.lds_consts + ((ars == 2 && arg < Mr) ? 0 : 256) + kq * 8;
+    const int me = min(grp, Mr - 1);
+    const bool out_lane = grp < Mr;  // this lane's output row exists
+    const int nu = (wave < kProducers && n_items > wave) ? (n_items - wave + kProducers - 1) / kProducers : 0;
+    int seen_chain = 0;
+
+    // One item: MFMA per block, in-lane epilogue, f into the ring (or the
+    // block integers to Cs), then publish progress.
+    auto process = [&](const Pre<JG, EXTRA>& cur, const It& t, int u) {
+        const int i = t.i;
+        int toff, c;
+        it_decode(t, toff, c);
+        const int tile = t_begin + toff;
+        const int n = tile * 16 + col;
+        const int abase = is_data ? data_base + c * JG * 64 : const_base;
+        int4 sqv = make_int4(0, 0, 0, 0);
+        if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * a.nblk4 + c * 4);
+        float* slot = ring + (size_t)(i & a.ring_mask) * sstride + (grp * 16 + col) * JG;
+        if (!DOTS) {
+            const int need = i - a.ring_mask;  // chain must have consumed items < need
+            if (need > seen_chain) {
+                int spins = 0;
+                while ((seen_chain = __builtin_amdgcn_readfirstlane(lds_load_acq(chain_items))) < need) {
+                    if (__builtin_amdgcn_readfirstlane(*abort_flag) || ++spins > kSpinLimit) {
+                        if (spins > kSpinLimit) *abort_flag = 1;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
+        }
+#pragma unroll
+        for (int jb = 0; jb < JG; ++jb) {
+            // Blocks past nblk (last chunk) read padding and produce values
+            // the chain never uses; only the integer export must skip them.
+            const int j = c * JG + jb;
+            if (DOTS && j >= a.nblk) break;
+            const uint64_t bop = unpack_b(cur.w, jb, BITS);
+            const uint64_t aop = *reinterpret_cast<const uint64_t*>(smem + abase + jb * 64);
+            const v4i dd = mfma16(aop, bop);
+            int cs = HP ? dd[0] * 256 + dd[1] + dd[2] * 128 : dd[0];
+            if (BITS == 4) {
+                const int zp = EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) : 8;
+                const int sq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
+                cs -= zp * sq;
+            }
+            if (EXTRA) cs += (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
+            if (DOTS) {
+                if (out_lane) a.Cs[((size_t)(m0 + grp) * a.N + n) * a.nblk + j] = cs;
+            } else {
+                slot[jb] = (float)cs * cur.sc[EXTRA ? jb : 0];
+            }
+        }
+        if (!DOTS && lane == 0) lds_store_rel(&prog[wave], u + 1);
+    };
+
+    // ---------------- prologue
+    // Activation loads first, then the first weight batch (every wave issues
+    // it; the chain wave's copy is unused), then the activations are
+    // quantized (or copied) while the weights are in flight.
+    Pre<JG, EXTRA> pre[B];
+    const int nb_rows = Mr * a.nblk;
+    constexpr int kCopy = 8;  // uint4 per thread for the record copy (not FUSED)
+    uint4 av[FUSED ? 4 : kCopy];
+    if (FUSED) {
+        const int npass_ld = (nb_rows + 127) >> 7;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            if (p >= npass_ld) break;
+            const int blk = min(p * 128 + (tid >> 3), nb_rows - 1);
+            const int m = blk / a.nblk, j = blk - m * a.nblk;
+            av[p] = *reinterpret_cast<const uint4*>(a.A + (size_t)(m0 + m) * a.K + 32 * j + 4 * (tid & 7));
+        }
+    } else {
+        // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
+        // scale and sum(q) rows as uint4 (Mr * nblk4 / 4 each).
+        const uint4* rsrc = reinterpret_cast<const uint4*>(a.Aq + (size_t)m0 * a.nblk * 64);
+        const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+#pragma unroll
+        for (int p = 0; p < kCopy - 2; ++p) av[p] = rsrc[min(p * 1024 + tid, nrec - 1)];
+        const int mi = min(tid, nmeta - 1);
+        const int mm = (mi * 4) / a.nblk4, mj = mi * 4 - mm * a.nblk4;
+        av[kCopy - 2] = *reinterpret_cast<const uint4*>(a.Sa + (size_t)(m0 + mm) * a.nblk4 + mj);
+        av[kCopy - 1] = *reinterpret_cast<const uint4*>(a.Sq + (size_t)(m0 + mm) * a.nblk4 + mj);
+    }
+    It ld = it_at(wave);
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+        load_pre(ld, pre[b]);
+        it_next(ld);
+    }
+    if (FUSED) {
+        const int npass = (nb_rows + 127) >> 7;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            if (p >= npass) break;
+            const int blk = p * 128 + (tid >> 3), e = tid & 7;
+            float s;
+            int sum;
+            uint32_t p0, p1;
+            quant8<HP>(make_float4(__uint_as_float(av[p].x), __uint_as_float(av[p].y),
+                                   __uint_as_float(av[p].z), __uint_as_float(av[p].w)),
+                       s, sum, p0, p1);
+            if (blk < nb_rows) {
+                const int m = blk / a.nblk, j = blk - m * a.nblk;
+                uint8_t* rec = recs + ((size_t)m * a.nblk + j) * 64;
+                *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
+                *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
+                if (e == 0) {
+                    sa_l[m * a.nblk4 + j] = s;
+                    sq_l[m * a.nblk4 + j] = sum;
+                }
+            }
+        }
+    } else {
+        uint4* dst = reinterpret_cast<uint4*>(recs);
+        const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+#pragma unroll
+        for (int p = 0; p < kCopy - 2; ++p) {
+            const int i = p * 1024 + tid;
+            if (i < nrec) dst[i] = av[p];
+        }
+        if (tid < nmeta) {
+            reinterpret_cast<uint4*>(sa_l)[tid] = av[kCopy - 2];
+            reinterpret_cast<uint4*>(sq_l)[tid] = av[kCopy - 1];
+        }
+    }
+    {
+        uint32_t* cst = reinterpret_cast<uint32_t*>(smem + a.lds_consts);
+        if (tid < 128) cst[tid] = tid < 64 ? 0x01010101u : 0u;  // [0,256) ones, [256,512) zeros
+        if (tid < kProducers + 2) prog[tid] = 0;
+    }
+    lds_barrier();
+
+    if (wave < kProducers) {
+        // ---------------- producer: first batch (already in flight), then
+        // batches issued and consumed inside the loop.
+        It pr = it_at(wave);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            if (b >= nu) break;
+            process(pre[b], pr, b);
+            it_next(pr);
+        }
+        for (int u0 = B; u0 < nu; u0 += B) {
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                load_pre(ld, pre[b]);
+                it_next(ld);
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                if (u0 + b >= nu) break;
+                process(pre[b], pr, u0 + b);
+                it_next(pr);
+            }
+        }
+    } else if (!DOTS) {
+        // ---------------- chain wave
+        int ts, cm;
+        if (Mr == 1) {
+            ts = lane >> 4;
+            cm = 0;
+        } else if (Mr == 2) {
+            ts = lane >> 5;
+            cm = (lane >> 4) & 1;
+        } else {
+            ts = 0;
+            cm = lane >> 4;
+        }
+        const int ccol = lane & 15;
+        const int cmr = min(cm, Mr - 1);  // clamped row for addressing
+        unsigned long long best = 0;
+        int frontier = 0;
+        const int ngroups = full_groups + (tg_last > 0 ? 1 : 0);
+        for (int gm = 0; gm < ngroups; ++gm) {
+            const int tg = gm < full_groups ? TG : tg_last;
+            const int ibase = gm * per_group;
+            const bool active = ts < tg && cm < Mr;
+            float acc = 0.0f;
+            int c = 0;
+            while (c < a.nbg) {
+                // Steps whose TG items are all produced: c .. ready-1.
+                int ready = 0, spins = 0;
+                while (true) {
+                    const int done = frontier - ibase;
+                    ready = tg == 4 ? done >> 2 : tg == 2 ? done >> 1 : tg == 1 ? done
+                                                                    : (int)__umulhi((unsigned)max(done, 0), 0x55555556u);
+                    ready = min(ready, a.nbg);
+                    if (ready > c) break;
+                    // All producers' progress in one LDS round trip: lane w
+                    // reads producer w, then a row min (items < frontier are
+                    // complete).  The acquire fence orders the ring reads.
+                    int f = 0x7FFFFFFF;
+                    if (lane < kProducers)
+                        f = __hip_atomic_load(&prog[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) *
+                                kProducers + lane;
+                    f = min16(f);
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+                    const int nf = __builtin_amdgcn_readfirstlane(f);
+                    if (nf > frontier) {
+                        frontier = nf;
+                        continue;
+                    }
+                    if (__builtin_amdgcn_readfirstlane(*abort_flag) || ++spins > kSpinLimit) {
+                        if (spins > kSpinLimit) *abort_flag = 1;
+                        frontier = ibase + a.nbg * tg;
+                        continue;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                // Fold the ready steps, kChainBatch at a time.  Every lane
+                // reads (inactive lanes from clamped valid slots) and the
+                // step/tail predicates are uniform, so the batch's LDS reads
+                // issue back to back before its FMAs.
+                while (c < ready) {
+                    const int cn = min(kChainBatch, ready - c);
+                    float fv[kChainBatch][JG], sv[kChainBatch][JG];
+#pragma unroll
+                    for (int st = 0; st < kChainBatch; ++st) {
+                        const int cc = c + min(st, cn - 1);
+                        const int slot = (ibase + cc * tg + ts) & a.ring_mask;
+                        const float* fp = ring + (size_t)slot * sstride + (cmr * 16 + ccol) * JG;
+                        const float* sp = sa_l + cmr * a.nblk4 + cc * JG;
+#pragma unroll
+                        for (int jb = 0; jb < JG; ++jb) {
+                            fv[st][jb] = fp[jb];
+                            sv[st][jb] = sp[jb];
+                        }
+                    }
+#pragma unroll
+                    for (int st = 0; st < kChainBatch; ++st) {
+#pragma unroll
+                        for (int jb = 0; jb < JG; ++jb) {
+                            const float nacc = __builtin_fmaf(sv[st][jb], fv[st][jb], acc);
+                            acc = (st < cn && (c + st) * JG + jb < a.nblk) ? nacc : acc;
+                        }
+                    }
+                    c += cn;
+                }
+                if (lane == 0) lds_store_rel(chain_items, ibase + c * tg);
+            }
+            if (active) {
+                const int n = (t_begin + gm * TG + ts) * 16 + ccol;
+                a.C[(size_t)(m0 + cm) * a.N + n] = acc;
+                if (a.part) {
+                    const unsigned long long k = argmax_key(acc, n);
+                    best = k > best ? k : best;
+                }
+            }
+        }
+        if (a.part) {
+            unsigned long long* red = reinterpret_cast<unsigned long long*>(smem + a.lds_red);
+            red[lane] = best;
+            __builtin_amdgcn_wave_barrier();
+            if (lane < Mr) {
+                unsigned long long b = 0;
+                for (int l = 0; l < 64; ++l) {
+                    const int lcm = Mr == 1 ? 0 : (Mr == 2 ? ((l >> 4) & 1) : (l >> 4));
+                    if (lcm == lane) b = red[l] > b ? red[l] : b;
+                }
+                a.part[(size_t)g * a.M + m0 + lane] = b;
+            }
+        }
+        // A bounded wait gave up somewhere in this workgroup: report it (the
+        // outputs are then not trustworthy; the host surfaces the flag).
+        if (lane == 0 && *abort_flag) atomicOr(a.err, 1);
+    }
+}
+
+// ------------------------------------------------------------------ generic rows kernel (M > 8)
+//
+// One workgroup per (16-column tile, 8-row chunk), all of K: waves compute a
+// segment of f values into LDS, then one lane per (m, n) folds them in order.
+
+constexpr int kRowWaves = 4;
+constexpr int kRowChunks = 2;
+constexpr int kRowsPerWG = 8;
+
+template <int BITS, bool HP, bool DOTS>
+__global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
+    constexpr int JG = BITS == 8 ? 2 : 4;
+    constexpr int SEG = kRowWaves * kRowChunks * JG;
+    __shared__ float fbuf[kRowsPerWG][SEG][16];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x;
+    const int m0 = blockIdx.y * kRowsPerWG;
+    const int Mc = min(kRowsPerWG, a.M - m0);
+    const int nmf = (Mc + 3) >> 2;
+    const int col = lane & 15, grp = lane >> 4;
+    const int arow = lane & 15, arg = arow >> 2, ars = arow & 3;
+    const size_t n = (size_t)t * 16 + col;
+    const int cm = threadIdx.x >> 4, ccol = threadIdx.x & 15;
+    float acc = 0.0f;
+    const uint2* Aq2 = reinterpret_cast<const uint2*>(a.Aq);
+
+    const int nseg = (a.nblk + SEG - 1) / SEG;
+    for (int s = 0; s < nseg; ++s) {
+        const int j0 = s * SEG;
+#pragma unroll
+        for (int cc = 0; cc < kRowChunks; ++cc) {
+            const int cg = j0 / JG + wave * kRowChunks + cc;
+            if (cg * JG >= a.nblk) break;
+            const uint4 wv = a.W[((size_t)t * a.nbg + cg) * 64 + lane];
+#pragma unroll
+            for (int jb = 0; jb < JG; ++jb) {
+                const int j = cg * JG + jb;
+                if (j >= a.nblk) break;
+                const uint64_t bop = unpack_b(wv, jb, BITS);
+                float sc;
+                if (a.flags & kFlagScBlk) sc = a.S[n * a.nblk_pad + j];
+                else sc = a.S[n * a.ngrp + (j >> a.sc_shift)];
+                for (int mi = 0; mi < nmf; ++mi) {
+                    const int ml = mi * 4 + arg;
+                    uint64_t aop = 0;
+                    if (ars == 2) {
+                        aop = 0x0101010101010101ull;
+                    } else if (ars < 2 && ml < Mc) {
+                        const uint2 x = Aq2[((size_t)(m0 + ml) * a.nblk + j) * 8 + ars * 4 + grp];
+                        aop = (uint64_t)x.y << 32 | x.x;
+                    }
+                    const v4i d = mfma16(aop, bop);
+                    const int me = mi * 4 + grp;
+                    if (me < Mc) {
+                        const size_t row = (size_t)(m0 + me);
+                        int cs = HP ? d[0] * 256 + d[1] + d[2] * 128 : d[0];
+                        if (BITS == 4) {
+                            const int zp = (a.flags & kFlagZp) ? (int)a.Z[n * a.nblk4 + j] : 8;
+                            cs -= zp * a.Sq[row * a.nblk4 + j];
+                        }
+                        if (a.flags & kFlagDl) cs += (HP ? 256 : 1) * a.D[n * a.nblk_pad + j];
+                        if (DOTS) a.Cs[(row * a.N + n) * a.nblk + j] = cs;
+                        else fbuf[me][j - j0][col] = (float)cs * sc;
+                    }
+                }
+            }
+        }
+        if (!DOTS) {
+            __syncthreads();
+            if (cm < Mc) {
+                const int jn = min(SEG, a.nblk - j0);
+                const float* sa = a.Sa + (size_t)(m0 + cm) * a.nblk4 + j0;
+                for (int jj = 0; jj < jn; ++jj) acc = __builtin_fmaf(sa[jj], fbuf[cm][jj][ccol], acc);
+            }
+            __syncthreads();
+        }
+    }
+    if (!DOTS && cm < Mc) a.C[(size_t)(m0 + cm) * a.N + t * 16 + ccol] = acc;
+}
+
+// ------------------------------------------------------------------ argmax
 
 __device__ inline unsigned long long block_max_key(unsigned long long k) {
     __shared__ unsigned long long red[256];
@@ -340,6 +842,7 @@ __device__ inline unsigned long long block_max_key(unsigned long long k) {
 
 constexpr int kArgmaxChunk = 4096;
 
+// Partial keys over chunks of C (used after the rows kernel).
 __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __restrict__ C, int N,
                                                              unsigned long long* __restrict__ part) {
     const int m = blockIdx.y, c = blockIdx.x;
@@ -348,14 +851,15 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     for (int i = lo + (int)threadIdx.x; i < hi; i += 256)
         best = max(best, argmax_key(C[(size_t)m * N + i], i));
     best = block_max_key(best);
-    if (threadIdx.x == 0) part[(size_t)m * gridDim.x + c] = best;
+    if (threadIdx.x == 0) part[(size_t)c * gridDim.y + m] = best;
 }
 
+// part [nparts][M] -> out[m].
 __global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long long* __restrict__ part,
-                                                           int nparts, int64_t* __restrict__ out) {
+                                                           int nparts, int M, int64_t* __restrict__ out) {
     const int m = blockIdx.x;
     unsigned long long best = 0;
-    for (int i = threadIdx.x; i < nparts; i += 256) best = max(best, part[(size_t)m * nparts + i]);
+    for (int i = threadIdx.x; i < nparts; i += 256) best = max(best, part[(size_t)i * M + m]);
     best = block_max_key(best);
     if (threadIdx.x == 0) out[m] = (int64_t)(0xFFFFFFFFu - (uint32_t)(best & 0xFFFFFFFFull));
 }
@@ -364,16 +868,19 @@ __global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long l
 
 struct Workspace {
     std::mutex mu;
-    uint4* aq = nullptr;
+    uint8_t* aq = nullptr;
     float* sa = nullptr;
     int* sq = nullptr;
-    size_t blocks_cap = 0;  // rows * nblk capacity
+    size_t rows_cap = 0, nblk4_cap = 0;
     unsigned long long* parts = nullptr;
     size_t parts_cap = 0;
+    int* err = nullptr;
     float* hA = nullptr;  // device staging for the host-pointer entry points
     float* hC = nullptr;
     size_t hA_cap = 0, hC_cap = 0;
     hipStream_t stream = nullptr;
+    int n_cu = 0;
+    bool attr_set[32] = {};
 };
 
 constexpr int kMaxDevices = 64;
@@ -390,16 +897,31 @@ bool grow(T** p, size_t* cap, size_t need, const char* what) {
     return true;
 }
 
-bool ensure_blocks(Workspace& w, size_t rows_blocks) {
-    if (rows_blocks <= w.blocks_cap) return true;
-    size_t cap = 0;
-    bool ok = grow(&w.aq, &cap, rows_blocks * 4, "workspace alloc");
-    cap = 0;
-    ok = ok && grow(&w.sa, &cap, rows_blocks, "workspace alloc");
-    cap = 0;
-    ok = ok && grow(&w.sq, &cap, rows_blocks, "workspace alloc");
-    w.blocks_cap = ok ? rows_blocks : 0;
-    return ok;
+bool ensure_quant(Workspace& w, size_t rows, size_t nblk4) {
+    if (rows * nblk4 <= w.rows_cap * w.nblk4_cap && nblk4 <= w.nblk4_cap && rows <= w.rows_cap &&
+        w.aq)
+        return true;
+    const size_t r = std::max(rows, w.rows_cap), nb = std::max(nblk4, w.nblk4_cap);
+    size_t c1 = 0, c2 = 0, c3 = 0;
+    if (w.aq) (void)hipFree(w.aq);
+    if (w.sa) (void)hipFree(w.sa);
+    if (w.sq) (void)hipFree(w.sq);
+    w.aq = nullptr;
+    w.sa = nullptr;
+    w.sq = nullptr;
+    w.rows_cap = w.nblk4_cap = 0;
+    if (!grow(&w.aq, &c1, r * nb * 64, "workspace alloc") || !grow(&w.sa, &c2, r * nb, "workspace alloc") ||
+        !grow(&w.sq, &c3, r * nb, "workspace alloc"))
+        return false;
+    w.rows_cap = r;
+    w.nblk4_cap = nb;
+    return true;
+}
+
+bool ensure_err(Workspace& w) {
+    if (w.err) return true;
+    if (!hip_ok(hipMalloc(&w.err, sizeof(int)), "workspace alloc")) return false;
+    return hip_ok(hipMemset(w.err, 0, sizeof(int)), "workspace init");
 }
 
 // ------------------------------------------------------------------ host helpers
@@ -429,17 +951,19 @@ float half_to_float(uint16_t h) {
 }
 
 // Builds a handle from a canonical host representation:
-//   raw: MatMulNBits bytes [N][nblk][16 or 32] (INT8 either unsigned w+128 or,
-//        with raw_signed, already signed w); scales fp32 [N][nblk];
+//   raw: MatMulNBits bytes [N][nblk][16 or 32] (INT8 unsigned w+128, or
+//        already signed with raw_signed); scales fp32 [N][nblk];
 //   zp:  INT4 zero points [N][nblk] or empty; delta: legacy [N][nblk] or empty.
 void* build_handle(const uint8_t* raw, bool raw_signed, const float* scales, int N, int K,
                    int bits, const std::vector<int8_t>& zp, const std::vector<int32_t>& delta) {
     const int nblk = K / 32;
     const int JG = bits == 8 ? 2 : 4;
     const int nbg = (nblk + JG - 1) / JG;
+    const int nblk_pad = nbg * JG;
+    const int nblk4 = (nblk + 3) / 4 * 4;
 
     // Repeated scales are stored once: per column, or per aligned group of
-    // 2^k blocks (bitwise comparison, so any value is kept as given).
+    // 2^k blocks (bitwise comparison, so every value is kept as given).
     int sc_shift = 31, ngrp = 1, sc_group = 0;
     {
         bool per_col = true;
@@ -469,11 +993,36 @@ void* build_handle(const uint8_t* raw, bool raw_signed, const float* scales, int
             }
         }
     }
-    std::vector<float> sc_compact((size_t)N * ngrp);
-    for (int n = 0; n < N; ++n)
-        for (int g = 0; g < ngrp; ++g)
-            sc_compact[(size_t)n * ngrp + g] =
-                scales[(size_t)n * nblk + (sc_shift == 31 ? 0 : (g << sc_shift))];
+    // Handles with explicit zero points, a legacy corr, or scale groups
+    // smaller than a chunk keep all three per-block arrays, so the decode
+    // kernel's loads stay unconditional.
+    const bool extra = !zp.empty() || !delta.empty() || (sc_shift != 31 && (1 << sc_shift) < JG);
+    std::vector<float> sc_dev;
+    if (extra) {
+        sc_dev.assign((size_t)N * nblk_pad, 0.0f);
+        for (int n = 0; n < N; ++n)
+            for (int j = 0; j < nblk; ++j) sc_dev[(size_t)n * nblk_pad + j] = scales[(size_t)n * nblk + j];
+    } else {
+        sc_dev.resize((size_t)N * ngrp);
+        for (int n = 0; n < N; ++n)
+            for (int g = 0; g < ngrp; ++g)
+                sc_dev[(size_t)n * ngrp + g] =
+                    scales[(size_t)n * nblk + (sc_shift == 31 ? 0 : (g << sc_shift))];
+    }
+    std::vector<int8_t> zp_dev;
+    if (extra && bits == 4) {
+        zp_dev.assign((size_t)N * nblk4, 8);
+        if (!zp.empty())
+            for (int n = 0; n < N; ++n)
+                for (int j = 0; j < nblk; ++j) zp_dev[(size_t)n * nblk4 + j] = zp[(size_t)n * nblk + j];
+    }
+    std::vector<int32_t> dl_dev;
+    if (extra) {
+        dl_dev.assign((size_t)N * nblk_pad, 0);
+        if (!delta.empty())
+            for (int n = 0; n < N; ++n)
+                for (int j = 0; j < nblk; ++j) dl_dev[(size_t)n * nblk_pad + j] = delta[(size_t)n * nblk + j];
+    }
 
     auto* h = new (std::nothrow) Handle{};
     if (!h) {
@@ -486,34 +1035,36 @@ void* build_handle(const uint8_t* raw, bool raw_signed, const float* scales, int
     h->nblk = nblk;
     h->bits = bits;
     h->nbg = nbg;
+    h->nblk_pad = nblk_pad;
+    h->nblk4 = nblk4;
     h->sc_shift = sc_shift;
     h->ngrp = ngrp;
     h->sc_group = sc_group;
+    h->sc_blk = extra;
     h->has_zp = !zp.empty();
     h->has_dl = !delta.empty();
+    h->extra = extra;
     (void)hipGetDevice(&h->device);
 
     const size_t wbytes = (size_t)(N / 16) * nbg * 64 * 16;
     const size_t rawbytes = (size_t)N * nblk * 4 * bits;
     uint8_t* draw = nullptr;
     bool ok = hip_ok(hipMalloc(&h->W, wbytes), "weight alloc") &&
-              hip_ok(hipMalloc(&h->S, sc_compact.size() * 4), "scale alloc") &&
-              (!h->has_zp || hip_ok(hipMalloc(&h->Z, zp.size()), "zero-point alloc")) &&
-              (!h->has_dl || hip_ok(hipMalloc(&h->D, delta.size() * 4), "corr alloc")) &&
+              hip_ok(hipMalloc(&h->S, sc_dev.size() * 4), "scale alloc") &&
+              (zp_dev.empty() || hip_ok(hipMalloc(&h->Z, zp_dev.size()), "zero-point alloc")) &&
+              (dl_dev.empty() || hip_ok(hipMalloc(&h->D, dl_dev.size() * 4), "corr alloc")) &&
               hip_ok(hipMalloc(&draw, rawbytes), "staging alloc");
     ok = ok && hip_ok(hipMemcpy(draw, raw, rawbytes, hipMemcpyHostToDevice), "weight upload") &&
-         hip_ok(hipMemcpy(h->S, sc_compact.data(), sc_compact.size() * 4, hipMemcpyHostToDevice),
-                "scale upload") &&
-         (!h->has_zp || hip_ok(hipMemcpy(h->Z, zp.data(), zp.size(), hipMemcpyHostToDevice),
-                               "zero-point upload")) &&
-         (!h->has_dl || hip_ok(hipMemcpy(h->D, delta.data(), delta.size() * 4, hipMemcpyHostToDevice),
-                               "corr upload"));
+         hip_ok(hipMemcpy(h->S, sc_dev.data(), sc_dev.size() * 4, hipMemcpyHostToDevice), "scale upload") &&
+         (zp_dev.empty() ||
+          hip_ok(hipMemcpy(h->Z, zp_dev.data(), zp_dev.size(), hipMemcpyHostToDevice), "zero-point upload")) &&
+         (dl_dev.empty() ||
+          hip_ok(hipMemcpy(h->D, dl_dev.data(), dl_dev.size() * 4, hipMemcpyHostToDevice), "corr upload"));
     if (ok) {
         const size_t total = (size_t)(N / 16) * nbg * 64;
         const unsigned blocks = (unsigned)((total + 255) / 256);
         repack_kernel<<<blocks, 256>>>(draw, h->W, N, nblk, nbg, bits, raw_signed ? 1 : 0);
-        ok = hip_ok(hipGetLastError(), "repack launch") &&
-             hip_ok(hipDeviceSynchronize(), "repack");
+        ok = hip_ok(hipGetLastError(), "repack launch") && hip_ok(hipDeviceSynchronize(), "repack");
     }
     if (draw) (void)hipFree(draw);
     if (!ok) {
@@ -524,38 +1075,105 @@ void* build_handle(const uint8_t* raw, bool raw_signed, const float* scales, int
         delete h;
         return nullptr;
     }
-    h->dev_bytes = wbytes + sc_compact.size() * 4 + zp.size() + delta.size() * 4;
+    h->dev_bytes = wbytes + sc_dev.size() * 4 + zp_dev.size() + dl_dev.size() * 4;
     return h;
 }
 
-template <int BITS, bool HP>
-hipError_t launch_qmm_bits(const Handle* h, const QmmArgs& a, dim3 grid, hipStream_t st, bool dots) {
-    const dim3 block(kWaves * 64);
-#define QMM_LAUNCH(ZP, DL, DT) qmm_kernel<BITS, HP, ZP, DL, DT><<<grid, block, 0, st>>>(a)
-    if (dots) {
-        if (h->has_zp) {
-            if (h->has_dl) QMM_LAUNCH(true, true, true);
-            else QMM_LAUNCH(true, false, true);
-        } else {
-            if (h->has_dl) QMM_LAUNCH(false, true, true);
-            else QMM_LAUNCH(false, false, true);
-        }
-    } else {
-        if (h->has_zp) {
-            if (h->has_dl) QMM_LAUNCH(true, true, false);
-            else QMM_LAUNCH(true, false, false);
-        } else {
-            if (h->has_dl) QMM_LAUNCH(false, true, false);
-            else QMM_LAUNCH(false, false, false);
-        }
+void fill_args(const Handle* h, GemvArgs& a, int M) {
+    a.W = h->W;
+    a.S = h->S;
+    a.Z = h->Z;
+    a.D = h->D;
+    a.M = M;
+    a.N = h->N;
+    a.K = h->K;
+    a.nblk = h->nblk;
+    a.nblk4 = h->nblk4;
+    a.nbg = h->nbg;
+    a.nblk_pad = h->nblk_pad;
+    a.sc_shift = h->sc_shift;
+    a.ngrp = h->ngrp;
+    a.flags = h->extra ? ((h->Z ? kFlagZp : 0) | kFlagDl | kFlagScBlk) : 0;
+    a.ntiles = h->N / 16;
+}
+
+constexpr int kLdsMax = 160 * 1024;
+
+// LDS plan of the decode kernel; returns false if it does not fit.
+bool plan_gemv_lds(GemvArgs& a, int Mr_max, int JG) {
+    // The prologue's record copy moves at most 6 uint4 per thread.
+    if (Mr_max * a.nblk > 512 && Mr_max * a.nblk * 4 > 6 * kGemvWaves * 64) return false;
+    int off = 0;
+    auto take = [&](int bytes) {
+        const int o = off;
+        off += (bytes + 15) / 16 * 16;
+        return o;
+    };
+    a.lds_recs = take(Mr_max * a.nblk * 64);
+    a.lds_sa = take(Mr_max * a.nblk4 * 4);
+    a.lds_sq = take(Mr_max * a.nblk4 * 4);
+    a.lds_consts = take(512);
+    a.lds_sync = take(64 * 4);
+    a.lds_red = take(64 * 8);
+    const int slot = 4 * 16 * JG * 4;  // ring slot: 4 rows x 16 columns x JG blocks of fp32
+    int R = 128;
+    while (R > 32 && off + R * slot > kLdsMax) R >>= 1;
+    if (off + R * slot > kLdsMax) return false;
+    a.lds_ring = take(R * slot);
+    a.ring_mask = R - 1;
+    return true;
+}
+
+template <int BITS, bool HP, bool FUSED, bool DOTS, bool EXTRA>
+hipError_t launch_gemv_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipStream_t st) {
+    auto kern = gemv_kernel<BITS, HP, FUSED, DOTS, EXTRA>;
+    const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (DOTS ? 8 : 0) | (EXTRA ? 16 : 0);
+    if (!w.attr_set[key]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+        if (e != hipSuccess) return e;
+        w.attr_set[key] = true;
     }
-#undef QMM_LAUNCH
+    kern<<<grid, kGemvWaves * 64, lds, st>>>(a);
     return hipGetLastError();
 }
 
+template <int BITS, bool HP, bool EXTRA>
+hipError_t launch_gemv_x(Workspace& w, const GemvArgs& a, int grid, int lds, bool fused, bool dots,
+                         hipStream_t st) {
+    if (dots) return fused ? launch_gemv_t<BITS, HP, true, true, EXTRA>(w, a, grid, lds, st)
+                           : launch_gemv_t<BITS, HP, false, true, EXTRA>(w, a, grid, lds, st);
+    return fused ? launch_gemv_t<BITS, HP, true, false, EXTRA>(w, a, grid, lds, st)
+                 : launch_gemv_t<BITS, HP, false, false, EXTRA>(w, a, grid, lds, st);
+}
+
+template <int BITS, bool HP>
+hipError_t launch_gemv_bits(Workspace& w, const GemvArgs& a, int grid, int lds, bool fused, bool dots,
+                            bool extra, hipStream_t st) {
+    return extra ? launch_gemv_x<BITS, HP, true>(w, a, grid, lds, fused, dots, st)
+                 : launch_gemv_x<BITS, HP, false>(w, a, grid, lds, fused, dots, st);
+}
+
+template <int BITS, bool HP>
+hipError_t launch_rows_bits(const GemvArgs& a, dim3 grid, bool dots, hipStream_t st) {
+    if (dots) rows_kernel<BITS, HP, true><<<grid, kRowWaves * 64, 0, st>>>(a);
+    else rows_kernel<BITS, HP, false><<<grid, kRowWaves * 64, 0, st>>>(a);
+    return hipGetLastError();
+}
+
+int device_cus(Workspace& w, int dev) {
+    if (w.n_cu == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        w.n_cu = n;
+    }
+    return w.n_cu;
+}
+
 // Quantize + block dots + epilogue for M rows on `st`.  Exactly one of
-// dC / dCs is non-null.
-int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, hipStream_t st) {
+// dC / dCs is non-null; dIdx (optional) receives the per-row argmax.
+int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dIdx, hipStream_t st) {
     if (M < 0) {
         set_err("M must be >= 0 (got %d)", M);
         return -2;
@@ -575,56 +1193,81 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, hipStream_t 
         set_err("handle lives on device %d but device %d is current", h->device, dev);
         return -3;
     }
-    Workspace& w = g_ws[dev];
-    const size_t rb = (size_t)M * h->nblk;
-    if (rb > (size_t)std::numeric_limits<int>::max() / 4) {
+    if ((size_t)M * h->nblk4 > (size_t)std::numeric_limits<int>::max() / 64) {
         set_err("M*K too large");
         return -2;
     }
-    if (!ensure_blocks(w, rb)) return -4;
+    Workspace& w = g_ws[dev];
+    if (!ensure_err(w)) return -4;
     const bool hp = g_hi_prec != 0;
-    const unsigned qb = (unsigned)((rb + 255) / 256);
-    if (hp) quantize_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, w.aq, w.sa, w.sq);
-    else quantize_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, w.aq, w.sa, w.sq);
-    if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
+    const bool dots = dCs != nullptr;
+    const int JG = h->bits == 8 ? 2 : 4;
 
-    QmmArgs a{};
-    a.W = h->W;
-    a.S = h->S;
-    a.Z = h->Z;
-    a.D = h->D;
-    a.Aq = reinterpret_cast<const uint2*>(w.aq);
-    a.Sa = w.sa;
-    a.Sq = w.sq;
+    GemvArgs a{};
+    fill_args(h, a, M);
+    a.A = dA;
     a.C = dC;
     a.Cs = dCs;
-    a.M = M;
-    a.N = h->N;
-    a.nblk = h->nblk;
-    a.nbg = h->nbg;
-    a.sc_shift = h->sc_shift;
-    a.ngrp = h->ngrp;
-    const dim3 grid(h->N / 16, (M + kRowsPerWG - 1) / kRowsPerWG);
-    const bool dots = dCs != nullptr;
-    hipError_t e;
-    if (h->bits == 8) e = hp ? launch_qmm_bits<8, true>(h, a, grid, st, dots)
-                             : launch_qmm_bits<8, false>(h, a, grid, st, dots);
-    else e = hp ? launch_qmm_bits<4, true>(h, a, grid, st, dots)
-                : launch_qmm_bits<4, false>(h, a, grid, st, dots);
-    if (!hip_ok(e, "matmul launch")) return -5;
-    return 0;
-}
+    a.err = w.err;
 
-int run_argmax(Handle* h, const float* dC, int M, int64_t* dIdx, hipStream_t st) {
-    if (M == 0) return 0;
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    Workspace& w = g_ws[dev];
-    const int nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
-    if (!grow(&w.parts, &w.parts_cap, (size_t)M * nparts, "argmax workspace")) return -4;
-    argmax_partial_kernel<<<dim3(nparts, M), 256, 0, st>>>(dC, h->N, w.parts);
-    argmax_final_kernel<<<M, 256, 0, st>>>(w.parts, nparts, dIdx);
-    return hip_ok(hipGetLastError(), "argmax launch") ? 0 : -5;
+    const int Mr_max = std::min(M, 4);
+    const bool gemv = M <= 8 && plan_gemv_lds(a, Mr_max, JG);
+    const bool fused = gemv && Mr_max * h->nblk <= 512;
+    if (!fused) {
+        if (!ensure_quant(w, M, h->nblk4)) return -4;
+        const size_t threads = (size_t)M * h->nblk * 8;
+        const unsigned qb = (unsigned)((threads + 255) / 256);
+        if (hp) quantize_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq);
+        else quantize_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq);
+        if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
+        a.Aq = w.aq;
+        a.Sa = w.sa;
+        a.Sq = w.sq;
+    }
+
+    hipError_t e;
+    int nparts = 0;
+    if (gemv) {
+        const int n_cu = device_cus(w, dev);
+        a.RG = (M + 3) / 4;
+        if (a.RG == 1) {
+            a.NG = std::min(a.ntiles, n_cu);
+            a.pair_xcd = 0;
+        } else {
+            const int ng = std::min(a.ntiles, std::max(1, n_cu / 2));
+            a.pair_xcd = ng % 8 == 0 ? 1 : 0;
+            a.NG = ng;
+        }
+        if (dIdx && !dots) {
+            if (!grow(&w.parts, &w.parts_cap, (size_t)a.NG * M, "argmax workspace")) return -4;
+            a.part = w.parts;
+            nparts = a.NG;
+        }
+        const int grid = a.NG * a.RG;
+        const int lds = a.lds_ring + (a.ring_mask + 1) * 4 * 16 * JG * 4;
+        const bool x = h->extra;
+        if (h->bits == 8) e = hp ? launch_gemv_bits<8, true>(w, a, grid, lds, fused, dots, x, st)
+                                 : launch_gemv_bits<8, false>(w, a, grid, lds, fused, dots, x, st);
+        else e = hp ? launch_gemv_bits<4, true>(w, a, grid, lds, fused, dots, x, st)
+                    : launch_gemv_bits<4, false>(w, a, grid, lds, fused, dots, x, st);
+    } else {
+        const dim3 grid(a.ntiles, (M + kRowsPerWG - 1) / kRowsPerWG);
+        if (h->bits == 8) e = hp ? launch_rows_bits<8, true>(a, grid, dots, st)
+                                 : launch_rows_bits<8, false>(a, grid, dots, st);
+        else e = hp ? launch_rows_bits<4, true>(a, grid, dots, st) : launch_rows_bits<4, false>(a, grid, dots, st);
+    }
+    if (!hip_ok(e, "matmul launch")) return -5;
+
+    if (dIdx && !dots) {
+        if (!gemv) {
+            nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
+            if (!grow(&w.parts, &w.parts_cap, (size_t)M * nparts, "argmax workspace")) return -4;
+            argmax_partial_kernel<<<dim3(nparts, M), 256, 0, st>>>(dC, h->N, w.parts);
+        }
+        argmax_final_kernel<<<M, 256, 0, st>>>(w.parts, nparts, M, dIdx);
+        if (!hip_ok(hipGetLastError(), "argmax launch")) return -5;
+    }
+    return 0;
 }
 
 bool check_dims(int N, int K, int bits) {
@@ -666,12 +1309,24 @@ int i4_device_ok(void) {
         return 0;
     }
     hipFuncAttributes attr;
-    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&qmm_kernel<8, true, false, false, false>)) !=
+    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&gemv_kernel<8, true, true, false, false>)) !=
         hipSuccess) {
         set_err("gfx950 kernels not loadable");
         return 0;
     }
     return 1;
+}
+
+int i4_debug_flags(void) {
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    Workspace& w = g_ws[dev];
+    if (!w.err) return 0;
+    int v = 0;
+    if (hipDeviceSynchronize() != hipSuccess || hipMemcpy(&v, w.err, sizeof v, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    if (v) (void)hipMemset(w.err, 0, sizeof(int));
+    return v;
 }
 
 void* i4_prepack_onnx(const uint8_t* qw, const void* scales, const uint8_t* qzeros, int N, int K,
@@ -783,8 +1438,7 @@ void* i4_prepack(const uint8_t* B, const float* scale, const int8_t* zp, const i
     if (bits == 8 || !zp_fits) {
         // Signed bytes [N][nblk][32]; INT4 with zero points below -112 would
         // wrap in int8 arithmetic, so such handles keep the wrapped values.
-        return build_handle(reinterpret_cast<const uint8_t*>(b.data()), true, sc.data(), N, K, 8,
-                            {}, delta);
+        return build_handle(reinterpret_cast<const uint8_t*>(b.data()), true, sc.data(), N, K, 8, {}, delta);
     }
     std::vector<uint8_t> raw(blocks * 16);
     for (size_t n = 0; n < (size_t)N; ++n)
@@ -816,7 +1470,7 @@ void i4_free(void* handle) {
 int i4_matmul_dev(void* handle, const float* dA, int M, float* dC, void* stream) {
     Handle* h = as_handle(handle);
     if (!h) return -1;
-    return run(h, dA, M, dC, nullptr, static_cast<hipStream_t>(stream));
+    return run(h, dA, M, dC, nullptr, nullptr, static_cast<hipStream_t>(stream));
 }
 
 int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream) {
@@ -826,15 +1480,13 @@ int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC, int64_
         set_err("null argmax output");
         return -2;
     }
-    const int rc = run(h, dA, M, dC, nullptr, static_cast<hipStream_t>(stream));
-    if (rc) return rc;
-    return run_argmax(h, dC, M, dIdx, static_cast<hipStream_t>(stream));
+    return run(h, dA, M, dC, nullptr, dIdx, static_cast<hipStream_t>(stream));
 }
 
 int i4_block_dots_dev(void* handle, const float* dA, int M, int32_t* dCs, void* stream) {
     Handle* h = as_handle(handle);
     if (!h) return -1;
-    return run(h, dA, M, nullptr, dCs, static_cast<hipStream_t>(stream));
+    return run(h, dA, M, nullptr, dCs, nullptr, static_cast<hipStream_t>(stream));
 }
 
 void i4_matmul(void* handle, const float* A, int M, float* C) {
@@ -856,10 +1508,9 @@ void i4_matmul(void* handle, const float* A, int M, float* C) {
     std::lock_guard<std::mutex> lock(w.mu);
     if (!w.stream && !hip_ok(hipStreamCreateWithFlags(&w.stream, hipStreamNonBlocking), "stream")) return;
     const size_t na = (size_t)M * h->K, nc = (size_t)M * h->N;
-    if (!grow(&w.hA, &w.hA_cap, na, "staging alloc") || !grow(&w.hC, &w.hC_cap, nc, "staging alloc"))
-        return;
+    if (!grow(&w.hA, &w.hA_cap, na, "staging alloc") || !grow(&w.hC, &w.hC_cap, nc, "staging alloc")) return;
     if (!hip_ok(hipMemcpyAsync(w.hA, A, na * 4, hipMemcpyHostToDevice, w.stream), "upload A")) return;
-    if (run(h, w.hA, M, w.hC, nullptr, w.stream) != 0) {
+    if (run(h, w.hA, M, w.hC, nullptr, nullptr, w.stream) != 0) {
         (void)hipStreamSynchronize(w.stream);
         return;
     }
@@ -894,40 +1545,55 @@ int i4_unpack(void* handle, uint8_t* qw, float* scales, uint8_t* zp, int32_t* co
     if (qw) {
         std::vector<uint4> W((size_t)(N / 16) * h->nbg * 64);
         if (!hip_ok(hipMemcpy(W.data(), h->W, W.size() * 16, hipMemcpyDeviceToHost), "download")) return -5;
+        const int JG = bits == 8 ? 2 : 4;
         for (int n = 0; n < N; ++n)
             for (int j = 0; j < nblk; ++j)
                 for (int oct = 0; oct < 4; ++oct) {
-                    const int JG = bits == 8 ? 2 : 4;
                     const int t = n / 16, lane = oct * 16 + (n % 16), cg = j / JG, jb = j % JG;
                     const uint4 v = W[((size_t)t * h->nbg + cg) * 64 + lane];
                     const uint32_t words[4] = {v.x, v.y, v.z, v.w};
                     if (bits == 8) {
                         uint8_t* dst = qw + ((size_t)n * nblk + j) * 32 + oct * 8;
-                        const uint64_t x = (uint64_t)words[2 * jb + 1] << 32 | words[2 * jb];
-                        for (int p = 0; p < 8; ++p) dst[kPerm8[p]] = (uint8_t)((x >> (8 * p)) ^ 0x80u);
+                        for (int p = 0; p < 4; ++p) dst[p] = (uint8_t)((words[2 * jb] >> (8 * p)) ^ 0x80u);
+                        for (int p = 0; p < 4; ++p) dst[4 + p] = (uint8_t)((words[2 * jb + 1] >> (8 * p)) ^ 0x80u);
                     } else {
                         uint8_t* dst = qw + ((size_t)n * nblk + j) * 16 + oct * 4;
-                        for (int p = 0; p < 4; ++p) dst[p] = (uint8_t)(words[jb] >> (8 * p));
+                        uint8_t nibs[8];
+                        for (int b = 0; b < 4; ++b) {
+                            const uint8_t t8 = (uint8_t)(words[jb] >> (8 * b));
+                            nibs[b] = t8 & 15;
+                            nibs[4 + b] = t8 >> 4;
+                        }
+                        for (int i = 0; i < 4; ++i) dst[i] = (uint8_t)(nibs[2 * i] | nibs[2 * i + 1] << 4);
                     }
                 }
     }
     if (scales) {
-        std::vector<float> S((size_t)N * h->ngrp);
-        if (!hip_ok(hipMemcpy(S.data(), h->S, S.size() * 4, hipMemcpyDeviceToHost), "download")) return -5;
+        const size_t cnt = h->sc_blk ? (size_t)N * h->nblk_pad : (size_t)N * h->ngrp;
+        std::vector<float> S(cnt);
+        if (!hip_ok(hipMemcpy(S.data(), h->S, cnt * 4, hipMemcpyDeviceToHost), "download")) return -5;
         for (int n = 0; n < N; ++n)
             for (int j = 0; j < nblk; ++j)
-                scales[(size_t)n * nblk + j] = S[(size_t)n * h->ngrp + (h->sc_shift == 31 ? 0 : j >> h->sc_shift)];
+                scales[(size_t)n * nblk + j] =
+                    h->sc_blk ? S[(size_t)n * h->nblk_pad + j]
+                              : S[(size_t)n * h->ngrp + (h->sc_shift == 31 ? 0 : j >> h->sc_shift)];
     }
     if (zp) {
-        if (h->Z) {
-            if (!hip_ok(hipMemcpy(zp, h->Z, blocks, hipMemcpyDeviceToHost), "download")) return -5;
+        if (h->Z && h->bits == 4) {
+            std::vector<int8_t> Z((size_t)N * h->nblk4);
+            if (!hip_ok(hipMemcpy(Z.data(), h->Z, Z.size(), hipMemcpyDeviceToHost), "download")) return -5;
+            for (int n = 0; n < N; ++n)
+                for (int j = 0; j < nblk; ++j) zp[(size_t)n * nblk + j] = (uint8_t)Z[(size_t)n * h->nblk4 + j];
         } else {
             std::memset(zp, bits == 8 ? 128 : 8, blocks);
         }
     }
     if (corr_delta) {
         if (h->D) {
-            if (!hip_ok(hipMemcpy(corr_delta, h->D, blocks * 4, hipMemcpyDeviceToHost), "download")) return -5;
+            std::vector<int32_t> Dv((size_t)N * h->nblk_pad);
+            if (!hip_ok(hipMemcpy(Dv.data(), h->D, Dv.size() * 4, hipMemcpyDeviceToHost), "download")) return -5;
+            for (int n = 0; n < N; ++n)
+                for (int j = 0; j < nblk; ++j) corr_delta[(size_t)n * nblk + j] = Dv[(size_t)n * h->nblk_pad + j];
         } else {
             std::memset(corr_delta, 0, blocks * 4);
         }
