@@ -108,6 +108,18 @@ Handle* as_handle(void* p) {
     return h;
 }
 
+// Per-column metadata is tile-major, so the 16 columns a lane group reads
+// for one chunk are contiguous:
+//   scales (per column or per group of 2^sc_shift blocks): [N/16][ngrp][16];
+//   per-block arrays of EXTRA handles, JG blocks per chunk:
+//     scales, corr delta: [N/16][nbg][16][JG]; INT4 zero points: [N/16][nbg][16][4] bytes.
+__host__ __device__ inline size_t grp_index(int n, int j, int ngrp, int sc_shift) {
+    return ((size_t)(n >> 4) * ngrp + (j >> sc_shift)) * 16 + (n & 15);
+}
+__host__ __device__ inline size_t blk_index(int n, int j, int nbg, int JG) {
+    return (((size_t)(n >> 4) * nbg + j / JG) * 16 + (n & 15)) * JG + j % JG;
+}
+
 // ------------------------------------------------------------------ device helpers
 
 __device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
@@ -267,55 +279,59 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
 
 // ------------------------------------------------------------------ decode GEMV (M <= 8)
 //
-// Persistent: one workgroup of 16 waves per CU, each owning a contiguous
-// range of 16-column tiles for up to 4 activation rows (M 5..8 uses two row
-// groups, placed on the same XCD so the second weight read hits its L2).
-// Waves 0..14 are producers: they stream 1 KB weight chunks in batches (all
-// loads of a batch issued back to back, then consumed), run the MFMA and the
-// in-lane epilogue, and put f = f32(cs) * scale into an LDS ring.  Wave 15
-// runs the ordered FP32 chain acc = fma(s, f, acc) over the ring in block
-// order, following the producers through their LDS progress counters; it
-// writes C (and the per-workgroup argmax partials).  Activations are
-// quantized into LDS in the prologue when small (FUSED), else copied from
-// the stand-alone quantizer.  The first batch is issued before the prologue
-// work, so the quantization overlaps the first weight loads.
+// One workgroup of 16 waves per CU owns a contiguous range of 16-column
+// tiles for up to 4 activation rows (M 5..8: one workgroup per row group of
+// 4, the pair placed on the same XCD so the second read of every weight
+// chunk hits its L2).  Waves 0..14 produce: a tile's K range is cut into
+// phases of 15 chunks and producer w takes chunk 15p + w of phase p, so
+// every producer streams its weights in K order and the chunks of a phase
+// arrive together.  Per phase each producer runs the MFMA and the in-lane
+// epilogue of its chunk and writes f = f32(cs) * scale to an LDS phase
+// buffer.  Wave 15 loads no weights: after each phase's workgroup barrier
+// it folds that phase's blocks in order, acc = fma(s, f, acc), while the
+// producers work on the next phase (two phase buffers), and it writes C at
+// each tile end.  The phase buffer holds each output lane's f values
+// contiguously, so the fold of a full phase is wide LDS reads and one FMA
+// per block.
 //
-// All weight loads live in straight-line code: the compiler's load waits
-// are exact there, whereas a load carried around a loop back edge is
-// drained at the loop head.
+// Weight chunks are loaded R units ahead through a register ring; the first
+// R units go out at kernel start, behind only the activation loads, and
+// stream in while the activations are quantized into LDS (FUSED) or their
+// records, made by the stand-alone quantizer, are copied there.  Every load
+// is unconditional (units past the end read one line) and the ring is
+// unrolled, so the compiler's load waits stay exact across the loop back
+// edge.
 
-constexpr int kGemvWaves = 16;
-constexpr int kProducers = kGemvWaves - 1;
-constexpr int kChainBatch = 8;
-constexpr int kSpinLimit = 1 << 22;
+constexpr int kDecWaves = 16;
+constexpr int kChainWave = kDecWaves - 1;
+constexpr int kProducers = kDecWaves - 1;
 
 struct GemvArgs {
     const uint4* W;
     const float* S;
     const int8_t* Z;
     const int32_t* D;
-    const float* A;        // fp32 [M][K] (FUSED)
-    const uint8_t* Aq;     // [M][nblk][64] records (not FUSED)
+    const float* A;        // fp32 [M][K]
+    const uint8_t* Aq;     // [M][nblk][64] records (stand-alone quantizer)
     const float* Sa;       // [M][nblk4]
     const int* Sq;         // [M][nblk4]
     float* C;              // [M][N]
     int32_t* Cs;           // [M][N][nblk] (block-dot export)
     unsigned long long* part;  // [NG][M] argmax partials, or NULL
-    int* err;
     int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
-    int ntiles, NG, RG, pair_xcd, ring_mask;
-    int lds_recs, lds_sa, lds_sq, lds_consts, lds_ring, lds_sync, lds_red;
+    int ntiles, NG, RG, pair_xcd;
+    int lds_recs, lds_sa, lds_sq, lds_consts, lds_fbuf;
 };
 
-// Per-item loads of a producer lane.  EXTRA handles (explicit zero points,
-// legacy corr, scale groups smaller than a chunk) carry materialized
-// per-block arrays so every load is unconditional.
+// One weight chunk of a wave plus its per-column metadata.  EXTRA handles
+// (explicit zero points, legacy corr, scale groups smaller than a chunk)
+// carry materialized per-block arrays so every load is unconditional.
 template <int JG, bool EXTRA>
-struct Pre {
-    uint4 w;       // weights
+struct Unit {
+    uint4 w;
     float sc[EXTRA ? JG : 1];
     int dl[EXTRA ? JG : 1];
-    uint32_t zp;   // INT4 zero points, one byte per block
+    uint32_t zp;  // INT4 zero points, one byte per block
 };
 
 __device__ inline unsigned long long argmax_key(float v, int idx) {
@@ -338,17 +354,16 @@ __device__ inline void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-__device__ inline int lds_load_acq(int* p) {
-    return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-__device__ inline void lds_store_rel(int* p, int v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
+// f row pitch (floats) of the phase buffer: 15 chunks of JG blocks plus
+// padding that keeps the JG-wide stores and reads free of bank conflicts.
+__host__ __device__ constexpr int dec_pitch(int JG) { return kProducers * JG + (JG == 4 ? 8 : 4); }
 
-template <int BITS, bool HP, bool FUSED, bool DOTS, bool EXTRA>
-__global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvArgs a) {
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R>
+__global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
     constexpr int JG = BITS == 8 ? 2 : 4;
-    constexpr int B = EXTRA ? 4 : 8;  // items per producer batch
+    constexpr int PP = dec_pitch(JG);
+    typedef float fvec __attribute__((ext_vector_type(JG)));
+    typedef int ivec __attribute__((ext_vector_type(JG)));
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -370,379 +385,249 @@ __global__ __launch_bounds__(kGemvWaves * 64) void gemv_kernel(GemvArgs a) {
     const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
     const int t_begin = g * base_t + min(g, rem_t);
     const int nT = base_t + (g < rem_t ? 1 : 0);
-    const int TG = Mr == 1 ? 4 : (Mr == 2 ? 2 : 1);
-    const int TGs = Mr == 1 ? 2 : (Mr == 2 ? 1 : 0);
-    const int full_groups = nT / TG;
-    const int tg_last = nT - full_groups * TG;
-    const int per_group = TG * a.nbg;
-    const int items_full = full_groups * per_group;
-    const int n_items = nT * a.nbg;
-    constexpr int sstride = 4 * 16 * JG;  // floats per ring slot (4 rows, unused rows are scratch)
+    const int nbg = a.nbg;
+    const int npw = (nbg + kProducers - 1) / kProducers;  // phases per tile
+    const int U = nT * npw;                                // phases of this workgroup
 
     uint8_t* recs = smem + a.lds_recs;
     float* sa_l = reinterpret_cast<float*>(smem + a.lds_sa);
     int* sq_l = reinterpret_cast<int*>(smem + a.lds_sq);
-    float* ring = reinterpret_cast<float*>(smem + a.lds_ring);
-    int* prog = reinterpret_cast<int*>(smem + a.lds_sync);
-    int* chain_items = prog + kProducers;
-    int* abort_flag = prog + kProducers + 1;
-
-    // Items of this workgroup, in the order the chain consumes them: for
-    // each group of TG tiles, for each chunk c, the TG tiles side by side
-    // (the last group may hold tg_last < TG tiles).  Producer w walks items
-    // w, w+15, ... with an incremental iterator (no division per item).
-    struct It {
-        int i, gm, r;
-    };
-    auto it_at = [&](int i) {
-        It t;
-        t.i = i;
-        if (i < items_full) {
-            t.gm = i / per_group;
-            t.r = i - t.gm * per_group;
-        } else {
-            t.gm = full_groups;
-            t.r = i - items_full;
-        }
-        return t;
-    };
-    auto it_next = [&](It& t) {
-        t.i += kProducers;
-        if (t.i < items_full) {
-            t.r += kProducers;
-            while (t.r >= per_group) {
-                t.r -= per_group;
-                ++t.gm;
-            }
-        } else {
-            t.gm = full_groups;
-            t.r = t.i - items_full;
-        }
-    };
-    // -> (tile offset in this workgroup, chunk); past the end -> last item.
-    auto it_decode = [&](const It& t, int& toff, int& c) {
-        if (t.i >= n_items) {
-            toff = nT - 1;
-            c = a.nbg - 1;
-        } else if (t.i < items_full) {
-            c = t.r >> TGs;
-            toff = t.gm * TG + (t.r & (TG - 1));
-        } else if (tg_last == 1) {
-            c = t.r;
-            toff = full_groups * TG;
-        } else if (tg_last == 2) {
-            c = t.r >> 1;
-            toff = full_groups * TG + (t.r & 1);
-        } else {
-            c = (int)__umulhi((unsigned)t.r, 0x55555556u);  // r / 3
-            toff = full_groups * TG + (t.r - 3 * c);
-        }
-    };
+    float* fbuf = reinterpret_cast<float*>(smem + a.lds_fbuf);  // [2][64][PP]
 
     const int col = lane & 15, grp = lane >> 4;
-    auto load_pre = [&](const It& t, Pre<JG, EXTRA>& p) {
-        int toff, c;
-        it_decode(t, toff, c);
-        const int tile = t_begin + toff;
-        const size_t n = (size_t)tile * 16 + col;
-        p.w = a.W[((size_t)tile * a.nbg + c) * 64 + lane];
+    const int me = min(grp, Mr - 1);
+
+    // Load cursor: unit (ld_t, ld_p) is chunk wave + 15 * ld_p of local tile
+    // ld_t (clamped to the tile's last chunk).  Units past the end read one
+    // line at the start of each array.
+    int ld_t = 0, ld_p = 0;
+    auto load_unit = [&](Unit<JG, EXTRA>& p) {
+        const int c = min(wave + kProducers * ld_p, nbg - 1);
+        const int tc = (t_begin + ld_t) * nbg + c;  // chunk index in the tile-major arrays
+        uint32_t wi = (uint32_t)tc * 64 + lane;     // weight uint4 index
+        uint32_t mi = (uint32_t)tc * 16 + col;      // per-block metadata index (EXTRA)
+        uint32_t si = (uint32_t)((t_begin + ld_t) * a.ngrp + ((c * JG) >> a.sc_shift)) * 16 + col;
+        if (ld_t >= nT) wi = mi = si = 0;
+        // Opaque to the optimizer, so the loads are not split into
+        // uniform-address copies on branches of their own.
+        asm("" : "+v"(wi), "+v"(mi), "+v"(si));
+        p.w = a.W[wi];
         if (EXTRA) {
-            if (JG == 4) {
-                const float4 s4 = *reinterpret_cast<const float4*>(a.S + n * a.nblk_pad + c * 4);
-                const int4 d4 = *reinterpret_cast<const int4*>(a.D + n * a.nblk_pad + c * 4);
-                p.sc[0] = s4.x;
-                p.sc[1 % JG] = s4.y;
-                p.sc[2 % JG] = s4.z;
-                p.sc[3 % JG] = s4.w;
-                p.dl[0] = d4.x;
-                p.dl[1 % JG] = d4.y;
-                p.dl[2 % JG] = d4.z;
-                p.dl[3 % JG] = d4.w;
-                p.zp = *reinterpret_cast<const uint32_t*>(a.Z + n * a.nblk4 + c * 4);
-            } else {
-                const float2 s2 = *reinterpret_cast<const float2*>(a.S + n * a.nblk_pad + c * 2);
-                const int2 d2 = *reinterpret_cast<const int2*>(a.D + n * a.nblk_pad + c * 2);
-                p.sc[0] = s2.x;
-                p.sc[1 % JG] = s2.y;
-                p.dl[0] = d2.x;
-                p.dl[1 % JG] = d2.y;
+            const fvec sv = *reinterpret_cast<const fvec*>(a.S + (size_t)mi * JG);
+            const ivec dv = *reinterpret_cast<const ivec*>(a.D + (size_t)mi * JG);
+#pragma unroll
+            for (int jb = 0; jb < JG; ++jb) {
+                p.sc[EXTRA ? jb : 0] = sv[jb];
+                p.dl[EXTRA ? jb : 0] = dv[jb];
             }
+            if (JG == 4) p.zp = *reinterpret_cast<const uint32_t*>(a.Z + (size_t)mi * 4);
         } else {
-            p.sc[0] = a.S[n * a.ngrp + ((c * JG) >> a.sc_shift)];
+            p.sc[0] = a.S[si];
+        }
+        if (++ld_p == npw) {
+            ld_p = 0;
+            ++ld_t;
         }
     };
 
-    // Producer lane roles (A operand row/slot and k-octet; output row).
+    // ---------------- prologue
+    // Activation loads first, then the first R weight units, then the
+    // activations are quantized (or their records copied) into LDS while the
+    // weights stream in.  The scheduling barriers keep this issue order.
+    const int nb_rows = Mr * a.nblk;
+    uint4 av[4];
+    uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
+    auto load_acts = [&]() {
+        if (FUSED) {
+            const int npass_ld = (nb_rows + 127) >> 7;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                if (p >= npass_ld) break;
+                const int blk = min(p * 128 + (tid >> 3), nb_rows - 1);
+                const int m = blk / a.nblk, j = blk - m * a.nblk;
+                av[p] = *reinterpret_cast<const uint4*>(a.A + (size_t)(m0 + m) * a.K + 32 * j + 4 * (tid & 7));
+            }
+        } else {
+            // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
+            // scale and sum(q) rows as uint4 (Mr * nblk4 / 4 each).
+            const uint4* rsrc = reinterpret_cast<const uint4*>(a.Aq + (size_t)m0 * a.nblk * 64);
+            const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+            r0 = rsrc[min(tid, nrec - 1)];
+            r1 = rsrc[min(1024 + tid, nrec - 1)];
+            r2 = rsrc[min(2048 + tid, nrec - 1)];
+            r3 = rsrc[min(3072 + tid, nrec - 1)];
+            r4 = rsrc[min(4096 + tid, nrec - 1)];
+            r5 = rsrc[min(5120 + tid, nrec - 1)];
+            const int mi = min(tid, nmeta - 1);
+            const int mm = (mi * 4) / a.nblk4, mj = mi * 4 - mm * a.nblk4;
+            rsa = *reinterpret_cast<const uint4*>(a.Sa + (size_t)(m0 + mm) * a.nblk4 + mj);
+            rsq = *reinterpret_cast<const uint4*>(a.Sq + (size_t)(m0 + mm) * a.nblk4 + mj);
+        }
+    };
+    auto store_acts = [&]() {
+        if (FUSED) {
+            const int npass = (nb_rows + 127) >> 7;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                if (p >= npass) break;
+                const int blk = p * 128 + (tid >> 3), e = tid & 7;
+                float s;
+                int sum;
+                uint32_t p0, p1;
+                quant8<HP>(make_float4(__uint_as_float(av[p].x), __uint_as_float(av[p].y),
+                                       __uint_as_float(av[p].z), __uint_as_float(av[p].w)),
+                           s, sum, p0, p1);
+                if (blk < nb_rows) {
+                    const int m = blk / a.nblk, j = blk - m * a.nblk;
+                    uint8_t* rec = recs + ((size_t)m * a.nblk + j) * 64;
+                    *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
+                    *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
+                    if (e == 0) {
+                        sa_l[m * a.nblk4 + j] = s;
+                        sq_l[m * a.nblk4 + j] = sum;
+                    }
+                }
+            }
+        } else {
+            // Unconditional stores: threads past the end rewrite the last
+            // element with the value they loaded from it.
+            uint4* dst = reinterpret_cast<uint4*>(recs);
+            const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+            dst[min(tid, nrec - 1)] = r0;
+            dst[min(1024 + tid, nrec - 1)] = r1;
+            dst[min(2048 + tid, nrec - 1)] = r2;
+            dst[min(3072 + tid, nrec - 1)] = r3;
+            dst[min(4096 + tid, nrec - 1)] = r4;
+            dst[min(5120 + tid, nrec - 1)] = r5;
+            const int mi = min(tid, nmeta - 1);
+            reinterpret_cast<uint4*>(sa_l)[mi] = rsa;
+            reinterpret_cast<uint4*>(sq_l)[mi] = rsq;
+        }
+        {
+            uint32_t* cst = reinterpret_cast<uint32_t*>(smem + a.lds_consts);
+            if (tid < 128) cst[tid] = tid < 64 ? 0x01010101u : 0u;  // [0,256) ones, [256,512) zeros
+        }
+    };
+
+    if (wave == kChainWave) {
+        // ================= chain wave
+        load_acts();
+        store_acts();
+        lds_barrier();
+        // Lane (row me, column col) of the current tile.
+        const float* sa_row = sa_l + me * a.nblk4;
+        const bool tail_pad = a.nblk != nbg * JG;  // the last chunk has padding blocks
+        float acc = 0.0f;
+        unsigned long long best = 0;
+        int pr_t = 0, pr_p = 0;
+        for (int u = 0; u < U; ++u) {
+            lds_barrier();
+            const float* fp = fbuf + ((u & 1) * 64 + lane) * PP;
+            const int c0 = kProducers * pr_p;
+            const float* sp = sa_row + c0 * JG;
+            if (c0 + kProducers < nbg || (c0 + kProducers == nbg && !tail_pad)) {
+                // Full phase: every block is real.  Groups of chunks: all
+                // reads of a group, then its FMAs.
+                constexpr int G = JG == 4 ? 4 : 8;
+#pragma unroll
+                for (int h = 0; h < kProducers; h += G) {
+                    fvec fv[G], sv[G];
+#pragma unroll
+                    for (int i = 0; i < G; ++i) {
+                        if (h + i >= kProducers) break;
+                        fv[i] = *reinterpret_cast<const fvec*>(fp + (h + i) * JG);
+                        sv[i] = *reinterpret_cast<const fvec*>(sp + (h + i) * JG);
+                    }
+#pragma unroll
+                    for (int i = 0; i < G; ++i) {
+                        if (h + i >= kProducers) break;
+#pragma unroll
+                        for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[i][jb], fv[i][jb], acc);
+                    }
+                }
+            } else {
+                const int nb = a.nblk - c0 * JG;
+                for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
+            }
+            if (++pr_p == npw) {
+                if (grp < Mr) {
+                    const int n = (t_begin + pr_t) * 16 + col;
+                    a.C[(size_t)(m0 + grp) * a.N + n] = acc;
+                    if (a.part) {
+                        const unsigned long long k = argmax_key(acc, n);
+                        best = k > best ? k : best;
+                    }
+                }
+                acc = 0.0f;
+                pr_p = 0;
+                ++pr_t;
+            }
+        }
+        if (a.part) {
+            // Row maximum over the lanes of each row (lanes 16r..16r+15).
+#pragma unroll
+            for (int s = 1; s < 16; s <<= 1) {
+                const unsigned long long o = __shfl_xor(best, s, 16);
+                best = o > best ? o : best;
+            }
+            if (col == 0 && grp < Mr) a.part[(size_t)g * a.M + m0 + grp] = best;
+        }
+        return;
+    }
+
+    // ================= producers (waves 0..14)
+    Unit<JG, EXTRA> ring[R];
+    load_acts();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < R; ++d) load_unit(ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    store_acts();
+    lds_barrier();
+
+    // A operand: lane row arow = 4 * group + slot (slots h, l, ones, zero),
+    // k-octet kq.  Output lane (col, grp) holds row grp.
     const int arow = lane & 15, arg = arow >> 2, ars = arow & 3, kq = lane >> 4;
     const bool is_data = ars < 2 && arg < Mr;
     const int data_base = a.lds_recs + arg * a.nblk * 64 + ars * 32 + kq * 8;
     const int const_base = a.lds_consts + ((ars == 2 && arg < Mr) ? 0 : 256) + kq * 8;
-    const int me = min(grp, Mr - 1);
-    const bool out_lane = grp < Mr;  // this lane's output row exists
-    const int nu = (wave < kProducers && n_items > wave) ? (n_items - wave + kProducers - 1) / kProducers : 0;
-    int seen_chain = 0;
 
-    // One item: MFMA per block, in-lane epilogue, f into the ring (or the
-    // block integers to Cs), then publish progress.
-    auto process = [&](const Pre<JG, EXTRA>& cur, const It& t, int u) {
-        const int i = t.i;
-        int toff, c;
-        it_decode(t, toff, c);
-        const int tile = t_begin + toff;
-        const int n = tile * 16 + col;
-        const int abase = is_data ? data_base + c * JG * 64 : const_base;
-        int4 sqv = make_int4(0, 0, 0, 0);
-        if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * a.nblk4 + c * 4);
-        float* slot = ring + (size_t)(i & a.ring_mask) * sstride + (grp * 16 + col) * JG;
-        if (!DOTS) {
-            const int need = i - a.ring_mask;  // chain must have consumed items < need
-            if (need > seen_chain) {
-                int spins = 0;
-                while ((seen_chain = __builtin_amdgcn_readfirstlane(lds_load_acq(chain_items))) < need) {
-                    if (__builtin_amdgcn_readfirstlane(*abort_flag) || ++spins > kSpinLimit) {
-                        if (spins > kSpinLimit) *abort_flag = 1;
-                        break;
+    int pr_p = 0;  // phase of the unit being processed
+    for (int u0 = 0; u0 < U; u0 += R) {
+#pragma unroll
+        for (int d = 0; d < R; ++d) {
+            const bool live = u0 + d < U;  // uniform over the workgroup
+            const int c = wave + kProducers * pr_p;
+            const int buf = (u0 + d) & 1;
+            if (live && c < nbg) {
+                const Unit<JG, EXTRA>& cur = ring[d];
+                const int abase = is_data ? data_base + c * JG * 64 : const_base;
+                int4 sqv = make_int4(0, 0, 0, 0);
+                if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * a.nblk4 + c * 4);
+                fvec fo;
+#pragma unroll
+                for (int jb = 0; jb < JG; ++jb) {
+                    // Blocks past nblk (last chunk) read padding; the chain
+                    // never folds them.
+                    const uint64_t bop = unpack_b(cur.w, jb, BITS);
+                    const uint64_t aop = *reinterpret_cast<const uint64_t*>(smem + abase + jb * 64);
+                    const v4i dd = mfma16(aop, bop);
+                    int cs = HP ? dd[0] * 256 + dd[1] + dd[2] * 128 : dd[0];
+                    if (BITS == 4) {
+                        const int zp = EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) : 8;
+                        const int sq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
+                        cs -= zp * sq;
                     }
-                    __builtin_amdgcn_s_sleep(1);
+                    if (EXTRA) cs += (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
+                    fo[jb] = (float)cs * cur.sc[EXTRA ? jb : 0];
                 }
+                *reinterpret_cast<fvec*>(fbuf + (buf * 64 + lane) * PP + wave * JG) = fo;
             }
+            load_unit(ring[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) lds_barrier();
+            if (++pr_p == npw) pr_p = 0;
         }
-#pragma unroll
-        for (int jb = 0; jb < JG; ++jb) {
-            // Blocks past nblk (last chunk) read padding and produce values
-            // the chain never uses; only the integer export must skip them.
-            const int j = c * JG + jb;
-            if (DOTS && j >= a.nblk) break;
-            const uint64_t bop = unpack_b(cur.w, jb, BITS);
-            const uint64_t aop = *reinterpret_cast<const uint64_t*>(smem + abase + jb * 64);
-            const v4i dd = mfma16(aop, bop);
-            int cs = HP ? dd[0] * 256 + dd[1] + dd[2] * 128 : dd[0];
-            if (BITS == 4) {
-                const int zp = EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) : 8;
-                const int sq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
-                cs -= zp * sq;
-            }
-            if (EXTRA) cs += (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
-            if (DOTS) {
-                if (out_lane) a.Cs[((size_t)(m0 + grp) * a.N + n) * a.nblk + j] = cs;
-            } else {
-                slot[jb] = (float)cs * cur.sc[EXTRA ? jb : 0];
-            }
-        }
-        if (!DOTS && lane == 0) lds_store_rel(&prog[wave], u + 1);
-    };
-
-    // ---------------- prologue
-    // Activation loads first, then the first weight batch (every wave issues
-    // it; the chain wave's copy is unused), then the activations are
-    // quantized (or copied) while the weights are in flight.
-    Pre<JG, EXTRA> pre[B];
-    const int nb_rows = Mr * a.nblk;
-    constexpr int kCopy = 8;  // uint4 per thread for the record copy (not FUSED)
-    uint4 av[FUSED ? 4 : kCopy];
-    if (FUSED) {
-        const int npass_ld = (nb_rows + 127) >> 7;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            if (p >= npass_ld) break;
-            const int blk = min(p * 128 + (tid >> 3), nb_rows - 1);
-            const int m = blk / a.nblk, j = blk - m * a.nblk;
-            av[p] = *reinterpret_cast<const uint4*>(a.A + (size_t)(m0 + m) * a.K + 32 * j + 4 * (tid & 7));
-        }
-    } else {
-        // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
-        // scale and sum(q) rows as uint4 (Mr * nblk4 / 4 each).
-        const uint4* rsrc = reinterpret_cast<const uint4*>(a.Aq + (size_t)m0 * a.nblk * 64);
-        const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
-#pragma unroll
-        for (int p = 0; p < kCopy - 2; ++p) av[p] = rsrc[min(p * 1024 + tid, nrec - 1)];
-        const int mi = min(tid, nmeta - 1);
-        const int mm = (mi * 4) / a.nblk4, mj = mi * 4 - mm * a.nblk4;
-        av[kCopy - 2] = *reinterpret_cast<const uint4*>(a.Sa + (size_t)(m0 + mm) * a.nblk4 + mj);
-        av[kCopy - 1] = *reinterpret_cast<const uint4*>(a.Sq + (size_t)(m0 + mm) * a.nblk4 + mj);
-    }
-    It ld = it_at(wave);
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-        load_pre(ld, pre[b]);
-        it_next(ld);
-    }
-    if (FUSED) {
-        const int npass = (nb_rows + 127) >> 7;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            if (p >= npass) break;
-            const int blk = p * 128 + (tid >> 3), e = tid & 7;
-            float s;
-            int sum;
-            uint32_t p0, p1;
-            quant8<HP>(make_float4(__uint_as_float(av[p].x), __uint_as_float(av[p].y),
-                                   __uint_as_float(av[p].z), __uint_as_float(av[p].w)),
-                       s, sum, p0, p1);
-            if (blk < nb_rows) {
-                const int m = blk / a.nblk, j = blk - m * a.nblk;
-                uint8_t* rec = recs + ((size_t)m * a.nblk + j) * 64;
-                *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
-                *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
-                if (e == 0) {
-                    sa_l[m * a.nblk4 + j] = s;
-                    sq_l[m * a.nblk4 + j] = sum;
-                }
-            }
-        }
-    } else {
-        uint4* dst = reinterpret_cast<uint4*>(recs);
-        const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
-#pragma unroll
-        for (int p = 0; p < kCopy - 2; ++p) {
-            const int i = p * 1024 + tid;
-            if (i < nrec) dst[i] = av[p];
-        }
-        if (tid < nmeta) {
-            reinterpret_cast<uint4*>(sa_l)[tid] = av[kCopy - 2];
-            reinterpret_cast<uint4*>(sq_l)[tid] = av[kCopy - 1];
-        }
-    }
-    {
-        uint32_t* cst = reinterpret_cast<uint32_t*>(smem + a.lds_consts);
-        if (tid < 128) cst[tid] = tid < 64 ? 0x01010101u : 0u;  // [0,256) ones, [256,512) zeros
-        if (tid < kProducers + 2) prog[tid] = 0;
-    }
-    lds_barrier();
-
-    if (wave < kProducers) {
-        // ---------------- producer: first batch (already in flight), then
-        // batches issued and consumed inside the loop.
-        It pr = it_at(wave);
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            if (b >= nu) break;
-            process(pre[b], pr, b);
-            it_next(pr);
-        }
-        for (int u0 = B; u0 < nu; u0 += B) {
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                load_pre(ld, pre[b]);
-                it_next(ld);
-            }
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                if (u0 + b >= nu) break;
-                process(pre[b], pr, u0 + b);
-                it_next(pr);
-            }
-        }
-    } else if (!DOTS) {
-        // ---------------- chain wave
-        int ts, cm;
-        if (Mr == 1) {
-            ts = lane >> 4;
-            cm = 0;
-        } else if (Mr == 2) {
-            ts = lane >> 5;
-            cm = (lane >> 4) & 1;
-        } else {
-            ts = 0;
-            cm = lane >> 4;
-        }
-        const int ccol = lane & 15;
-        const int cmr = min(cm, Mr - 1);  // clamped row for addressing
-        unsigned long long best = 0;
-        int frontier = 0;
-        const int ngroups = full_groups + (tg_last > 0 ? 1 : 0);
-        for (int gm = 0; gm < ngroups; ++gm) {
-            const int tg = gm < full_groups ? TG : tg_last;
-            const int ibase = gm * per_group;
-            const bool active = ts < tg && cm < Mr;
-            float acc = 0.0f;
-            int c = 0;
-            while (c < a.nbg) {
-                // Steps whose TG items are all produced: c .. ready-1.
-                int ready = 0, spins = 0;
-                while (true) {
-                    const int done = frontier - ibase;
-                    ready = tg == 4 ? done >> 2 : tg == 2 ? done >> 1 : tg == 1 ? done
-                                                                    : (int)__umulhi((unsigned)max(done, 0), 0x55555556u);
-                    ready = min(ready, a.nbg);
-                    if (ready > c) break;
-                    // All producers' progress in one LDS round trip: lane w
-                    // reads producer w, then a row min (items < frontier are
-                    // complete).  The acquire fence orders the ring reads.
-                    int f = 0x7FFFFFFF;
-                    if (lane < kProducers)
-                        f = __hip_atomic_load(&prog[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) *
-                                kProducers + lane;
-                    f = min16(f);
-                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-                    const int nf = __builtin_amdgcn_readfirstlane(f);
-                    if (nf > frontier) {
-                        frontier = nf;
-                        continue;
-                    }
-                    if (__builtin_amdgcn_readfirstlane(*abort_flag) || ++spins > kSpinLimit) {
-                        if (spins > kSpinLimit) *abort_flag = 1;
-                        frontier = ibase + a.nbg * tg;
-                        continue;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                }
-                // Fold the ready steps, kChainBatch at a time.  Every lane
-                // reads (inactive lanes from clamped valid slots) and the
-                // step/tail predicates are uniform, so the batch's LDS reads
-                // issue back to back before its FMAs.
-                while (c < ready) {
-                    const int cn = min(kChainBatch, ready - c);
-                    float fv[kChainBatch][JG], sv[kChainBatch][JG];
-#pragma unroll
-                    for (int st = 0; st < kChainBatch; ++st) {
-                        const int cc = c + min(st, cn - 1);
-                        const int slot = (ibase + cc * tg + ts) & a.ring_mask;
-                        const float* fp = ring + (size_t)slot * sstride + (cmr * 16 + ccol) * JG;
-                        const float* sp = sa_l + cmr * a.nblk4 + cc * JG;
-#pragma unroll
-                        for (int jb = 0; jb < JG; ++jb) {
-                            fv[st][jb] = fp[jb];
-                            sv[st][jb] = sp[jb];
-                        }
-                    }
-#pragma unroll
-                    for (int st = 0; st < kChainBatch; ++st) {
-#pragma unroll
-                        for (int jb = 0; jb < JG; ++jb) {
-                            const float nacc = __builtin_fmaf(sv[st][jb], fv[st][jb], acc);
-                            acc = (st < cn && (c + st) * JG + jb < a.nblk) ? nacc : acc;
-                        }
-                    }
-                    c += cn;
-                }
-                if (lane == 0) lds_store_rel(chain_items, ibase + c * tg);
-            }
-            if (active) {
-                const int n = (t_begin + gm * TG + ts) * 16 + ccol;
-                a.C[(size_t)(m0 + cm) * a.N + n] = acc;
-                if (a.part) {
-                    const unsigned long long k = argmax_key(acc, n);
-                    best = k > best ? k : best;
-                }
-            }
-        }
-        if (a.part) {
-            unsigned long long* red = reinterpret_cast<unsigned long long*>(smem + a.lds_red);
-            red[lane] = best;
-            __builtin_amdgcn_wave_barrier();
-            if (lane < Mr) {
-                unsigned long long b = 0;
-                for (int l = 0; l < 64; ++l) {
-                    const int lcm = Mr == 1 ? 0 : (Mr == 2 ? ((l >> 4) & 1) : (l >> 4));
-                    if (lcm == lane) b = red[l] > b ? red[l] : b;
-                }
-                a.part[(size_t)g * a.M + m0 + lane] = b;
-            }
-        }
-        // A bounded wait gave up somewhere in this workgroup: report it (the
-        // outputs are then not trustworthy; the host surfaces the flag).
-        if (lane == 0 && *abort_flag) atomicOr(a.err, 1);
     }
 }
 
@@ -786,9 +671,9 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
                 const int j = cg * JG + jb;
                 if (j >= a.nblk) break;
                 const uint64_t bop = unpack_b(wv, jb, BITS);
-                float sc;
-                if (a.flags & kFlagScBlk) sc = a.S[n * a.nblk_pad + j];
-                else sc = a.S[n * a.ngrp + (j >> a.sc_shift)];
+                const int JGh = BITS == 8 ? 2 : 4;
+                const float sc = (a.flags & kFlagScBlk) ? a.S[blk_index((int)n, j, a.nbg, JGh)]
+                                                        : a.S[grp_index((int)n, j, a.ngrp, a.sc_shift)];
                 for (int mi = 0; mi < nmf; ++mi) {
                     const int ml = mi * 4 + arg;
                     uint64_t aop = 0;
@@ -804,10 +689,10 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
                         const size_t row = (size_t)(m0 + me);
                         int cs = HP ? d[0] * 256 + d[1] + d[2] * 128 : d[0];
                         if (BITS == 4) {
-                            const int zp = (a.flags & kFlagZp) ? (int)a.Z[n * a.nblk4 + j] : 8;
+                            const int zp = (a.flags & kFlagZp) ? (int)a.Z[blk_index((int)n, j, a.nbg, 4)] : 8;
                             cs -= zp * a.Sq[row * a.nblk4 + j];
                         }
-                        if (a.flags & kFlagDl) cs += (HP ? 256 : 1) * a.D[n * a.nblk_pad + j];
+                        if (a.flags & kFlagDl) cs += (HP ? 256 : 1) * a.D[blk_index((int)n, j, a.nbg, JGh)];
                         if (DOTS) a.Cs[(row * a.N + n) * a.nblk + j] = cs;
                         else fbuf[me][j - j0][col] = (float)cs * sc;
                     }
@@ -874,13 +759,12 @@ struct Workspace {
     size_t rows_cap = 0, nblk4_cap = 0;
     unsigned long long* parts = nullptr;
     size_t parts_cap = 0;
-    int* err = nullptr;
     float* hA = nullptr;  // device staging for the host-pointer entry points
     float* hC = nullptr;
     size_t hA_cap = 0, hC_cap = 0;
     hipStream_t stream = nullptr;
     int n_cu = 0;
-    bool attr_set[32] = {};
+    bool attr_set[64] = {};
 };
 
 constexpr int kMaxDevices = 64;
@@ -916,12 +800,6 @@ bool ensure_quant(Workspace& w, size_t rows, size_t nblk4) {
     w.rows_cap = r;
     w.nblk4_cap = nb;
     return true;
-}
-
-bool ensure_err(Workspace& w) {
-    if (w.err) return true;
-    if (!hip_ok(hipMalloc(&w.err, sizeof(int)), "workspace alloc")) return false;
-    return hip_ok(hipMemset(w.err, 0, sizeof(int)), "workspace init");
 }
 
 // ------------------------------------------------------------------ host helpers
@@ -1001,27 +879,27 @@ void* build_handle(const uint8_t* raw, bool raw_signed, const float* scales, int
     if (extra) {
         sc_dev.assign((size_t)N * nblk_pad, 0.0f);
         for (int n = 0; n < N; ++n)
-            for (int j = 0; j < nblk; ++j) sc_dev[(size_t)n * nblk_pad + j] = scales[(size_t)n * nblk + j];
+            for (int j = 0; j < nblk; ++j) sc_dev[blk_index(n, j, nbg, JG)] = scales[(size_t)n * nblk + j];
     } else {
         sc_dev.resize((size_t)N * ngrp);
         for (int n = 0; n < N; ++n)
-            for (int g = 0; g < ngrp; ++g)
-                sc_dev[(size_t)n * ngrp + g] =
-                    scales[(size_t)n * nblk + (sc_shift == 31 ? 0 : (g << sc_shift))];
+            for (int gi = 0; gi < ngrp; ++gi)
+                sc_dev[grp_index(n, sc_shift == 31 ? 0 : gi << sc_shift, ngrp, sc_shift)] =
+                    scales[(size_t)n * nblk + (sc_shift == 31 ? 0 : (gi << sc_shift))];
     }
     std::vector<int8_t> zp_dev;
     if (extra && bits == 4) {
         zp_dev.assign((size_t)N * nblk4, 8);
         if (!zp.empty())
             for (int n = 0; n < N; ++n)
-                for (int j = 0; j < nblk; ++j) zp_dev[(size_t)n * nblk4 + j] = zp[(size_t)n * nblk + j];
+                for (int j = 0; j < nblk; ++j) zp_dev[blk_index(n, j, nbg, 4)] = zp[(size_t)n * nblk + j];
     }
     std::vector<int32_t> dl_dev;
     if (extra) {
         dl_dev.assign((size_t)N * nblk_pad, 0);
         if (!delta.empty())
             for (int n = 0; n < N; ++n)
-                for (int j = 0; j < nblk; ++j) dl_dev[(size_t)n * nblk_pad + j] = delta[(size_t)n * nblk + j];
+                for (int j = 0; j < nblk; ++j) dl_dev[blk_index(n, j, nbg, JG)] = delta[(size_t)n * nblk + j];
     }
 
     auto* h = new (std::nothrow) Handle{};
@@ -1098,11 +976,13 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 }
 
 constexpr int kLdsMax = 160 * 1024;
+constexpr int kFusedMaxBlocks = 512;  // row-blocks the prologue quantizes (4 passes of 128)
 
-// LDS plan of the decode kernel; returns false if it does not fit.
-bool plan_gemv_lds(GemvArgs& a, int Mr_max, int JG) {
-    // The prologue's record copy moves at most 6 uint4 per thread.
-    if (Mr_max * a.nblk > 512 && Mr_max * a.nblk * 4 > 6 * kGemvWaves * 64) return false;
+// LDS plan of the decode kernel; returns the bytes used, or 0 if the
+// activation records of a row group do not fit (in LDS, or in the
+// prologue's 6-uint4-per-thread record copy).
+int plan_dec_lds(GemvArgs& a, int Mr_max, int JG) {
+    if (Mr_max * a.nblk > kFusedMaxBlocks && Mr_max * a.nblk * 4 > 6 * kDecWaves * 64) return 0;
     int off = 0;
     auto take = [&](int bytes) {
         const int o = off;
@@ -1113,45 +993,41 @@ bool plan_gemv_lds(GemvArgs& a, int Mr_max, int JG) {
     a.lds_sa = take(Mr_max * a.nblk4 * 4);
     a.lds_sq = take(Mr_max * a.nblk4 * 4);
     a.lds_consts = take(512);
-    a.lds_sync = take(64 * 4);
-    a.lds_red = take(64 * 8);
-    const int slot = 4 * 16 * JG * 4;  // ring slot: 4 rows x 16 columns x JG blocks of fp32
-    int R = 128;
-    while (R > 32 && off + R * slot > kLdsMax) R >>= 1;
-    if (off + R * slot > kLdsMax) return false;
-    a.lds_ring = take(R * slot);
-    a.ring_mask = R - 1;
-    return true;
+    a.lds_fbuf = take(2 * 64 * dec_pitch(JG) * 4);
+    return off <= kLdsMax ? off : 0;
 }
 
-template <int BITS, bool HP, bool FUSED, bool DOTS, bool EXTRA>
-hipError_t launch_gemv_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipStream_t st) {
-    auto kern = gemv_kernel<BITS, HP, FUSED, DOTS, EXTRA>;
-    const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (DOTS ? 8 : 0) | (EXTRA ? 16 : 0);
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R>
+hipError_t launch_dec_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipStream_t st) {
+    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R>;
+    const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (EXTRA ? 8 : 0) | ((R / 2 - 1) << 4);
     if (!w.attr_set[key]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
         if (e != hipSuccess) return e;
         w.attr_set[key] = true;
     }
-    kern<<<grid, kGemvWaves * 64, lds, st>>>(a);
+    kern<<<grid, kDecWaves * 64, lds, st>>>(a);
     return hipGetLastError();
 }
 
-template <int BITS, bool HP, bool EXTRA>
-hipError_t launch_gemv_x(Workspace& w, const GemvArgs& a, int grid, int lds, bool fused, bool dots,
-                         hipStream_t st) {
-    if (dots) return fused ? launch_gemv_t<BITS, HP, true, true, EXTRA>(w, a, grid, lds, st)
-                           : launch_gemv_t<BITS, HP, false, true, EXTRA>(w, a, grid, lds, st);
-    return fused ? launch_gemv_t<BITS, HP, true, false, EXTRA>(w, a, grid, lds, st)
-                 : launch_gemv_t<BITS, HP, false, false, EXTRA>(w, a, grid, lds, st);
+// Ring depth R (weight units in flight per wave).  Two units per producer
+// (30 KB per CU) measured fastest on every decode workload: deeper rings
+// put more requests in flight than the memory system turns into bandwidth.
+constexpr int kDecRing = 2;
+
+template <int BITS, bool HP, bool FUSED, bool EXTRA>
+hipError_t launch_dec_r(Workspace& w, const GemvArgs& a, int grid, int lds, int, hipStream_t st) {
+    return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing>(w, a, grid, lds, st);
 }
 
 template <int BITS, bool HP>
-hipError_t launch_gemv_bits(Workspace& w, const GemvArgs& a, int grid, int lds, bool fused, bool dots,
-                            bool extra, hipStream_t st) {
-    return extra ? launch_gemv_x<BITS, HP, true>(w, a, grid, lds, fused, dots, st)
-                 : launch_gemv_x<BITS, HP, false>(w, a, grid, lds, fused, dots, st);
+hipError_t launch_dec_bits(Workspace& w, const GemvArgs& a, int grid, int lds, int units, bool fused,
+                           bool extra, hipStream_t st) {
+    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(w, a, grid, lds, units, st)
+                            : launch_dec_r<BITS, HP, false, true>(w, a, grid, lds, units, st);
+    return fused ? launch_dec_r<BITS, HP, true, false>(w, a, grid, lds, units, st)
+                 : launch_dec_r<BITS, HP, false, false>(w, a, grid, lds, units, st);
 }
 
 template <int BITS, bool HP>
@@ -1198,7 +1074,6 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
         return -2;
     }
     Workspace& w = g_ws[dev];
-    if (!ensure_err(w)) return -4;
     const bool hp = g_hi_prec != 0;
     const bool dots = dCs != nullptr;
     const int JG = h->bits == 8 ? 2 : 4;
@@ -1208,11 +1083,16 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     a.A = dA;
     a.C = dC;
     a.Cs = dCs;
-    a.err = w.err;
 
+    // Decode kernel for M <= 8 (one or two row groups of 4); the rows kernel
+    // serves larger M, the block-integer export and shapes whose activation
+    // records do not fit in LDS.  The decode kernel quantizes small
+    // activations itself; larger ones go through the stand-alone quantizer
+    // once instead of once per workgroup.
     const int Mr_max = std::min(M, 4);
-    const bool gemv = M <= 8 && plan_gemv_lds(a, Mr_max, JG);
-    const bool fused = gemv && Mr_max * h->nblk <= 512;
+    const int lds = (M <= 8 && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
+    const bool dec = lds > 0;
+    const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
     if (!fused) {
         if (!ensure_quant(w, M, h->nblk4)) return -4;
         const size_t threads = (size_t)M * h->nblk * 8;
@@ -1227,7 +1107,7 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
 
     hipError_t e;
     int nparts = 0;
-    if (gemv) {
+    if (dec) {
         const int n_cu = device_cus(w, dev);
         a.RG = (M + 3) / 4;
         if (a.RG == 1) {
@@ -1238,18 +1118,18 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
             a.pair_xcd = ng % 8 == 0 ? 1 : 0;
             a.NG = ng;
         }
-        if (dIdx && !dots) {
+        const int units = (a.ntiles + a.NG - 1) / a.NG * ((a.nbg + kProducers - 1) / kProducers);
+        if (dIdx) {
             if (!grow(&w.parts, &w.parts_cap, (size_t)a.NG * M, "argmax workspace")) return -4;
             a.part = w.parts;
             nparts = a.NG;
         }
         const int grid = a.NG * a.RG;
-        const int lds = a.lds_ring + (a.ring_mask + 1) * 4 * 16 * JG * 4;
         const bool x = h->extra;
-        if (h->bits == 8) e = hp ? launch_gemv_bits<8, true>(w, a, grid, lds, fused, dots, x, st)
-                                 : launch_gemv_bits<8, false>(w, a, grid, lds, fused, dots, x, st);
-        else e = hp ? launch_gemv_bits<4, true>(w, a, grid, lds, fused, dots, x, st)
-                    : launch_gemv_bits<4, false>(w, a, grid, lds, fused, dots, x, st);
+        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w, a, grid, lds, units, fused, x, st)
+                                 : launch_dec_bits<8, false>(w, a, grid, lds, units, fused, x, st);
+        else e = hp ? launch_dec_bits<4, true>(w, a, grid, lds, units, fused, x, st)
+                    : launch_dec_bits<4, false>(w, a, grid, lds, units, fused, x, st);
     } else {
         const dim3 grid(a.ntiles, (M + kRowsPerWG - 1) / kRowsPerWG);
         if (h->bits == 8) e = hp ? launch_rows_bits<8, true>(a, grid, dots, st)
@@ -1259,7 +1139,7 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     if (!hip_ok(e, "matmul launch")) return -5;
 
     if (dIdx && !dots) {
-        if (!gemv) {
+        if (!dec) {
             nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
             if (!grow(&w.parts, &w.parts_cap, (size_t)M * nparts, "argmax workspace")) return -4;
             argmax_partial_kernel<<<dim3(nparts, M), 256, 0, st>>>(dC, h->N, w.parts);
@@ -1309,24 +1189,12 @@ int i4_device_ok(void) {
         return 0;
     }
     hipFuncAttributes attr;
-    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&gemv_kernel<8, true, true, false, false>)) !=
+    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&dec_kernel<8, true, true, false, kDecRing>)) !=
         hipSuccess) {
         set_err("gfx950 kernels not loadable");
         return 0;
     }
     return 1;
-}
-
-int i4_debug_flags(void) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
-    Workspace& w = g_ws[dev];
-    if (!w.err) return 0;
-    int v = 0;
-    if (hipDeviceSynchronize() != hipSuccess || hipMemcpy(&v, w.err, sizeof v, hipMemcpyDeviceToHost) != hipSuccess)
-        return -1;
-    if (v) (void)hipMemset(w.err, 0, sizeof(int));
-    return v;
 }
 
 void* i4_prepack_onnx(const uint8_t* qw, const void* scales, const uint8_t* qzeros, int N, int K,
@@ -1574,16 +1442,15 @@ int i4_unpack(void* handle, uint8_t* qw, float* scales, uint8_t* zp, int32_t* co
         if (!hip_ok(hipMemcpy(S.data(), h->S, cnt * 4, hipMemcpyDeviceToHost), "download")) return -5;
         for (int n = 0; n < N; ++n)
             for (int j = 0; j < nblk; ++j)
-                scales[(size_t)n * nblk + j] =
-                    h->sc_blk ? S[(size_t)n * h->nblk_pad + j]
-                              : S[(size_t)n * h->ngrp + (h->sc_shift == 31 ? 0 : j >> h->sc_shift)];
+                scales[(size_t)n * nblk + j] = h->sc_blk ? S[blk_index(n, j, h->nbg, bits == 8 ? 2 : 4)]
+                                                         : S[grp_index(n, j, h->ngrp, h->sc_shift)];
     }
     if (zp) {
         if (h->Z && h->bits == 4) {
             std::vector<int8_t> Z((size_t)N * h->nblk4);
             if (!hip_ok(hipMemcpy(Z.data(), h->Z, Z.size(), hipMemcpyDeviceToHost), "download")) return -5;
             for (int n = 0; n < N; ++n)
-                for (int j = 0; j < nblk; ++j) zp[(size_t)n * nblk + j] = (uint8_t)Z[(size_t)n * h->nblk4 + j];
+                for (int j = 0; j < nblk; ++j) zp[(size_t)n * nblk + j] = (uint8_t)Z[blk_index(n, j, h->nbg, 4)];
         } else {
             std::memset(zp, bits == 8 ? 128 : 8, blocks);
         }
@@ -1593,7 +1460,8 @@ int i4_unpack(void* handle, uint8_t* qw, float* scales, uint8_t* zp, int32_t* co
             std::vector<int32_t> Dv((size_t)N * h->nblk_pad);
             if (!hip_ok(hipMemcpy(Dv.data(), h->D, Dv.size() * 4, hipMemcpyDeviceToHost), "download")) return -5;
             for (int n = 0; n < N; ++n)
-                for (int j = 0; j < nblk; ++j) corr_delta[(size_t)n * nblk + j] = Dv[(size_t)n * h->nblk_pad + j];
+                for (int j = 0; j < nblk; ++j)
+                    corr_delta[(size_t)n * nblk + j] = Dv[blk_index(n, j, h->nbg, bits == 8 ? 2 : 4)];
         } else {
             std::memset(corr_delta, 0, blocks * 4);
         }
