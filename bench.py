@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 quantized linear path; prints ONE JSON line.
+
+A step is one call of the device entry point (``i4_matmul_dev``: activation
+quantization, MFMA block dots and the FP32 epilogue chain) over one batch of
+synthetic input already resident in HBM.  The timed workload is the W4 GEMV
+M=1 K=4096 N=12288 with group-128 scales; ``value`` is its algorithmic HBM
+throughput (packed weights + one fp32 per distinct scale + fp32 activations
+in + fp32 outputs out, divided by the time per call).  Packed weights rotate
+over >= 512 MB of copies so no call is served from the 256 MB last-level
+cache.  The other workloads are timed the same way and reported under
+``workloads``.
+
+``cpu_baseline`` times the reference CPU kernel (kernel/quantized_matmul.cpp
+of breeze-engine, compiled from its own source into oracle/_ref) on this
+host's cores for the same workload; without it, the oracle's scalar C port.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
+                       [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "breeze-engine_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HEADLINE = "w4_gemv"
+METRIC = "W4/W8 GEMV us + achieved HBM GB/s at M=1; prefill INT8 TOPS at M=512"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+ROTATE_BYTES = 512 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_w4_gemv.json")
+
+
+def _handles(hb, d, min_bytes):
+    """Enough packed copies of one workload's weights to cover min_bytes."""
+    n = max(1, -(-min_bytes // d["qweight"].nbytes))
+    return [hb.prepack(d["qweight"], d["scales"], d["qzeros"], d["K"], d["N"], bits=d["bits"])
+            for _ in range(n)]
+
+
+def time_workload(hb, torch, name, rows, steps, warmup, argmax=False):
+    """Per-call time (s) of one workload: `warmup` untimed calls, then
+    `steps` calls bracketed by synchronisation and HIP events on the stream
+    the library launches on."""
+    from breeze_amd import workloads
+
+    d = workloads.make_config(name, rows)
+    hs = _handles(hb, d, ROTATE_BYTES)
+    N = d["N"]
+    A = torch.from_numpy(d["A"]).cuda()
+    M = A.shape[0]
+    out = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    idx = torch.empty((M,), dtype=torch.int64, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = hb._vp(stream.cuda_stream)
+    ap, op, ip = hb._vp(A.data_ptr()), hb._vp(out.data_ptr()), hb._vp(idx.data_ptr())
+    lib = hb._lib
+    if argmax:
+        def call(h):
+            return lib.i4_matmul_argmax_dev(hb._vp(h), ap, M, op, ip, sp)
+    else:
+        def call(h):
+            return lib.i4_matmul_dev(hb._vp(h), ap, M, op, sp)
+    try:
+        for i in range(warmup):
+            if call(hs[i % len(hs)]) != 0:
+                raise RuntimeError(f"{name}: {hb.last_error()}")
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
+            call(hs[i % len(hs)])
+        e1.record(stream)
+        torch.cuda.synchronize()
+        err = hb.last_error()
+        if err:
+            raise RuntimeError(f"{name}: {err}")
+        return e0.elapsed_time(e1) * 1e-3 / steps, M
+    finally:
+        for h in hs:
+            hb.free(h)
+
+
+def cpu_baseline(name):
+    """The reference CPU kernel on this host, same workload, bounded sample:
+    3 warmup calls, then calls until 3 s or 200 calls, whichever comes
+    first."""
+    from breeze_amd import workloads
+    from oracle import oracle
+
+    d = workloads.make_config(name)
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
+    ref = h = None
+    if oracle.ref_available():
+        kind = "reference"
+        ref = oracle.Ref(threads=cores)
+        h = ref.prepack(d["qweight"], d["scales"], None, d["N"], d["K"], d["bits"])
+
+        def run():
+            ref.matmul(h, d["A"], d["N"], hi_prec=True)
+    else:
+        kind, cores = "port", 1
+        orc = oracle.c_oracle()
+
+        def run():
+            orc.matmul(d["qweight"], d["scales"], None, d["N"], d["K"], d["bits"], d["A"], True)
+    try:
+        for _ in range(3):
+            run()
+        n, t0 = 0, time.perf_counter()
+        while n < 200 and (n < 3 or time.perf_counter() - t0 < 3.0):
+            run()
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+    finally:
+        if ref is not None:
+            ref.free(h)
+    return {
+        "value": round(workloads.algorithmic_bytes(name) / dt / 1e9, 2),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": kind,
+        "sample": f"{workloads.LABELS[name]}, hi-prec mode, {n} timed calls after 3 warmup "
+                  f"({dt * 1e6:.1f} us/call), {cores} OpenMP thread(s)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB fp32 elementwise copy 5 times (counter calibration)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported. "
+              "The path would shard by output columns (N) across GPUs with no reduction, "
+              "but no multi-GPU run is part of it.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    if args.copy_calibration:
+        # Known traffic for scaling the FETCH_SIZE / WRITE_SIZE counters:
+        # each launch reads and writes exactly 256 MiB.
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": 256 << 20, "copy_calibration_bytes_written": 256 << 20}))
+        return
+
+    from breeze_amd import hip_backend as hb
+    from breeze_amd import workloads
+
+    if not hb.device_available():
+        raise SystemExit(f"bench.py: gfx950 path unavailable: {hb.last_error()}")
+    hb.set_hi_prec(True)
+
+    t_step, M = time_workload(hb, torch, HEADLINE, None, args.steps, args.warmup)
+    nbytes = workloads.algorithmic_bytes(HEADLINE)
+    gbs = nbytes / t_step / 1e9
+
+    traffic = None
+    traffic_note = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            tr = json.load(f)
+        traffic = tr.get("bytes_per_launch")
+        traffic_note = tr.get("source")
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded MatMulNBits weights and N(0,1) activations, breeze_amd.workloads)",
+        "config": {
+            "workload": workloads.LABELS[HEADLINE],
+            "M": 1, "K": 4096, "N": 12288, "bits": 4, "scale_group": 128,
+            "activations": "two-pass INT16 (hi-prec)",
+            "algorithmic_bytes": nbytes,
+            "us_per_call": round(t_step * 1e6, 3),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "kernel": "dec_kernel (one launch per call)",
+            "traffic_source": traffic_note,
+        },
+    }
+
+    if not args.headline_only:
+        rows = []
+        steps2 = max(10, args.steps // 4)
+        for name, r in (("w8_gemv", None), ("w4_gemv", None), ("w4_decode", 1), ("w4_decode", 2),
+                        ("w4_decode", 4), ("w4_decode", 8), ("w8_lmhead", None), ("w8_prefill", None)):
+            t, m = time_workload(hb, torch, name, r, steps2 if name != "w8_lmhead" else 20,
+                                 max(3, args.warmup // 4), argmax=name == "w8_lmhead")
+            entry = {"workload": workloads.LABELS[name].format(M=m), "us": round(t * 1e6, 2)}
+            if name == "w8_prefill":
+                tops = workloads.algorithmic_ops(name, m) / t / 1e12
+                entry.update(tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
+            else:
+                g = workloads.algorithmic_bytes(name, m) / t / 1e9
+                entry.update(gbs=round(g, 1), frac_hbm_peak=round(g / HBM_PEAK_GBS, 4))
+            rows.append(entry)
+        result["workloads"] = rows
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(HEADLINE)
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

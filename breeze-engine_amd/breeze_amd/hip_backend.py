@@ -180,12 +180,13 @@ def prepack(qweight, scales, qzeros, K, N, bits=4, block_size=32):
     return handle
 
 
-def _prepack_numpy(qweight, scales, qzeros, K, N, bits=4, block_size=32):
-    """Build the reference's legacy pre-transformed layout in NumPy and pack
-    it through ``i4_prepack`` (breeze/cpu_backend.py:171-227 describes the
-    layout).  Callers validate the contract first.  Tests use it to show the
-    legacy and MatMulNBits entry points agree."""
-    _require_lib()
+def _legacy_layout(qweight, scales, qzeros, K, N, bits=4):
+    """MatMulNBits -> the reference's legacy pre-transformed layout, in NumPy
+    (the layout breeze/cpu_backend.py:171-227 builds): tiles of 16 columns,
+    per 32-block 8 groups of 4 k; INT8 signed bytes [N/16, nblk, 8, 64],
+    INT4 nibble pairs [N/16, nblk, 8, 32]; scale, zp (INT4) and
+    corr = 128 * (sum(q) - 32 * zp) as [N/16, nblk, 16].
+    Returns (B, scale, zp or None, corr)."""
     nblk = K // 32
     ntiles = N // 16
 
@@ -199,26 +200,34 @@ def _prepack_numpy(qweight, scales, qzeros, K, N, bits=4, block_size=32):
         Bv = np.ascontiguousarray(
             b.reshape(ntiles, 16, nblk, 8, 4).transpose(0, 2, 3, 1, 4).reshape(ntiles, nblk, 8, 64))
         corr = tile16((128 * b.astype(np.int32).sum(axis=2)).astype(np.int32))
-        handle = _lib.i4_prepack(_p(Bv), _p(sc), None, _p(corr), N, K, nblk, 8)
+        return Bv, sc, None, corr
+    qw = np.ascontiguousarray(qweight).reshape(N, nblk, 16)
+    w = np.empty((N, nblk, 32), np.uint8)
+    w[:, :, 0::2] = qw & 15
+    w[:, :, 1::2] = qw >> 4
+    if qzeros is not None and np.size(qzeros):
+        packed = (nblk + 1) // 2
+        qz = np.ascontiguousarray(qzeros).reshape(N, packed)
+        zpf = np.empty((N, packed * 2), np.uint8)
+        zpf[:, 0::2] = qz & 15
+        zpf[:, 1::2] = qz >> 4
+        zp = zpf[:, :nblk].astype(np.int32)
     else:
-        qw = np.ascontiguousarray(qweight).reshape(N, nblk, 16)
-        w = np.empty((N, nblk, 32), np.uint8)
-        w[:, :, 0::2] = qw & 15
-        w[:, :, 1::2] = qw >> 4
-        if qzeros is not None and np.size(qzeros):
-            packed = (nblk + 1) // 2
-            qz = np.ascontiguousarray(qzeros).reshape(N, packed)
-            zpf = np.empty((N, packed * 2), np.uint8)
-            zpf[:, 0::2] = qz & 15
-            zpf[:, 1::2] = qz >> 4
-            zp = zpf[:, :nblk].astype(np.int32)
-        else:
-            zp = np.full((N, nblk), 8, np.int32)
-        w2 = w.reshape(ntiles, 16, nblk, 8, 4).transpose(0, 2, 3, 1, 4).reshape(ntiles, nblk, 8, 64)
-        Bv = np.ascontiguousarray((w2[..., 0::2] | (w2[..., 1::2] << 4)).astype(np.uint8))
-        zp_t = tile16(zp.astype(np.int8))
-        corr = tile16((128 * (w.astype(np.int32).sum(axis=2) - 32 * zp)).astype(np.int32))
-        handle = _lib.i4_prepack(_p(Bv), _p(sc), _p(zp_t), _p(corr), N, K, nblk, 4)
+        zp = np.full((N, nblk), 8, np.int32)
+    w2 = w.reshape(ntiles, 16, nblk, 8, 4).transpose(0, 2, 3, 1, 4).reshape(ntiles, nblk, 8, 64)
+    Bv = np.ascontiguousarray((w2[..., 0::2] | (w2[..., 1::2] << 4)).astype(np.uint8))
+    zp_t = tile16(zp.astype(np.int8))
+    corr = tile16((128 * (w.astype(np.int32).sum(axis=2) - 32 * zp)).astype(np.int32))
+    return Bv, sc, zp_t, corr
+
+
+def _prepack_numpy(qweight, scales, qzeros, K, N, bits=4, block_size=32):
+    """Pack through the legacy entry point ``i4_prepack`` from the layout
+    ``_legacy_layout`` builds.  Callers validate the contract first.  Tests
+    use it to show the legacy and MatMulNBits entry points agree."""
+    _require_lib()
+    Bv, sc, zp, corr = _legacy_layout(qweight, scales, qzeros, K, N, bits)
+    handle = _lib.i4_prepack(_p(Bv), _p(sc), _p(zp), _p(corr), N, K, K // 32, bits)
     if not handle:
         raise MemoryError(f"Could not allocate packed {bits}-bit weights (N={N}, K={K}): "
                           f"{last_error()}")
