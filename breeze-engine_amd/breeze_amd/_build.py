@@ -31,6 +31,9 @@ FLAGS = [
     "-fno-gpu-flush-denormals-to-zero",
     # No packed-FP32 instructions in any kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the epilogues read every MFMA result
+    # with VALU instructions, and the AGPR form adds a copy for each.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-Wall",
 ]
 

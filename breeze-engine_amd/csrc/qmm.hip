@@ -96,6 +96,7 @@ struct Handle {
     float* S;    // [N][ngrp], or [N][nblk_pad] when sc_blk
     int8_t* Z;   // [N][nblk4] zero points (INT4 extra handles only)
     int32_t* D;  // [N][nblk_pad] legacy corr delta (extra handles only)
+    int32_t* WS; // INT8 handles: 128 * per-block weight sums, [N/16][nbg][16][2]
     size_t dev_bytes;
 };
 
@@ -251,11 +252,13 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint4* __restrict
 // ------------------------------------------------------------------ quantize
 
 // Stand-alone activation quantizer: 8 lanes per (row, block).  Records go
-// to Aq [M][nblk][64 B]; scale and sum(q) to Sa/Sq [M][nblk4].
+// to Aq [M][nblk][64 B]; scale and sum(q) to Sa/Sq [M][nblk4]; with SaT, the
+// scales also block-major to SaT [nblk][Mpad] (for the prefill GEMM).
 template <bool HP>
 __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ A, int M, int K,
                                                        int nblk, int nblk4, uint8_t* __restrict__ Aq,
-                                                       float* __restrict__ Sa, int* __restrict__ Sq) {
+                                                       float* __restrict__ Sa, int* __restrict__ Sq,
+                                                       float* __restrict__ SaT, int Mpad) {
     const int gtid = blockIdx.x * 256 + threadIdx.x;
     const int blk = gtid >> 3, e = gtid & 7;
     const bool valid = blk < M * nblk;
@@ -273,8 +276,31 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         if (e == 0) {
             Sa[(size_t)m * nblk4 + j] = s;
             Sq[(size_t)m * nblk4 + j] = sum;
+            if (SaT) SaT[(size_t)j * Mpad + m] = s;
         }
     }
+}
+
+// 128 * sum of the signed INT8 weights of each (column, block), tile-major
+// per chunk ([N/16][nbg][16][2]): the bias term of the two-pass product,
+// cs = 256*H + L + 128*S.  One thread per (tile, chunk, column).
+__global__ __launch_bounds__(256) void wsum_kernel(const uint4* __restrict__ W, int32_t* __restrict__ WS,
+                                                   int ntiles, int nbg) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)ntiles * nbg * 16) return;
+    const int col = (int)(i & 15);
+    const size_t tc = i >> 4;
+    auto sum4 = [](uint32_t x) {
+        return (int)(int8_t)x + (int)(int8_t)(x >> 8) + (int)(int8_t)(x >> 16) + (int)(int8_t)(x >> 24);
+    };
+    int s0 = 0, s1 = 0;
+    for (int oct = 0; oct < 4; ++oct) {
+        const uint4 w = W[tc * 64 + oct * 16 + col];
+        s0 += sum4(w.x) + sum4(w.y);
+        s1 += sum4(w.z) + sum4(w.w);
+    }
+    WS[i * 2] = 128 * s0;
+    WS[i * 2 + 1] = 128 * s1;
 }
 
 // ------------------------------------------------------------------ decode GEMV (M <= 8)
@@ -712,6 +738,198 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
     if (!DOTS && cm < Mc) a.C[(size_t)(m0 + cm) * a.N + t * 16 + ccol] = acc;
 }
 
+// ------------------------------------------------------------------ prefill GEMM (M > 8, INT8 weights)
+//
+// Workgroup tile 64 rows x 128 columns over all K; four waves as 2 x 2, each
+// 32 rows (two 16-row MFMA tiles) x 64 columns (four 16-column tiles).  Per
+// 32-block and 16 x 16 tile: H = sum(h*b) by one v_mfma_i32_16x16x32_i8, then
+// (H << 8) + 128*S as the accumulator input of the l-byte MFMA gives the
+// exact block integer cs, and the in-lane epilogue folds
+// acc = fma(s_a, f32(cs) * s_b, acc) in block order.  The weights are read in
+// their decode layout (the B operand directly), the activations from the
+// stand-alone quantizer's records, block-major scales and weight sums.
+
+constexpr int kPreRows = 64, kPreCols = 128;
+
+struct PreArgs {
+    const uint4* W;
+    const float* S;
+    const int32_t* WS;
+    const uint8_t* Aq;   // [M][nblk][64]
+    const float* SaT;    // [nblk][Mpad]
+    float* C;            // [M][N]
+    int M, N, nblk, nbg, ngrp, sc_shift, ntiles, Mpad, scm;
+};
+
+// SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
+template <bool HP, int SCM>
+__global__ __launch_bounds__(256) void prefill_w8_kernel(PreArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wr = wave >> 1, wc = wave & 1;
+    const int col = lane & 15, grp = lane >> 4;  // output lane: column col, rows 4*grp .. 4*grp+3
+    const int arow = lane & 15, kq = lane >> 4;  // A operand lane: row arow, k-octet kq
+    const int m_base = blockIdx.y * kPreRows + wr * 32;
+    const int t_base = blockIdx.x * (kPreCols / 16) + wc * 4;
+    const char* Wb = reinterpret_cast<const char*>(a.W);
+    const char* WSb = reinterpret_cast<const char*>(a.WS);
+    const char* Sb = reinterpret_cast<const char*>(a.S);
+    const char* Ab = reinterpret_cast<const char*>(a.Aq);
+    const char* SaTb = reinterpret_cast<const char*>(a.SaT);
+
+    // 32-bit byte offsets from the uniform base pointers, so every load is a
+    // base + offset form.  Chunk c covers blocks 2c and 2c+1.
+    uint32_t ao0[2], wo0[4], so0[4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const int r = min(m_base + rt * 16 + arow, a.M - 1);
+        ao0[rt] = (uint32_t)r * a.nblk * 64 + kq * 8;
+    }
+    float scv[4];
+    int tl[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+        tl[ct] = min(t_base + ct, a.ntiles - 1);
+        wo0[ct] = ((uint32_t)tl[ct] * a.nbg * 64 + lane) * 16;
+        so0[ct] = ((uint32_t)tl[ct] * a.nbg * 16 + col) * 8;  // int2 / float2 per (chunk, column)
+        scv[ct] = SCM == 0 ? a.S[grp_index(tl[ct] * 16 + col, 0, a.ngrp, a.sc_shift)] : 0.0f;
+    }
+    const uint32_t sao0 = (uint32_t)(m_base + 4 * grp) * 4;
+    const uint32_t sa_step = (uint32_t)a.Mpad * 4;
+    const int nch = a.nbg;  // chunks; the last one has one block when nblk is odd
+    const int last_blk = a.nblk - 1;
+
+    // Everything one chunk needs: weights, weight sums, scales, and the A
+    // operands and activation scales of both blocks.
+    struct Chunk {
+        uint4 w[4];
+        int2 s2[4];
+        float sc[4][2];
+        uint64_t ah[2][2], al[2][2];
+        float4 sav[2][2];
+    };
+    auto load_chunk = [&](Chunk& k, int c) {
+        c = min(c, nch - 1);  // past the end: reload the last chunk (not used)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const uint32_t wo = wo0[ct] + (uint32_t)c * 1024, so = so0[ct] + (uint32_t)c * 128;
+            k.w[ct] = *reinterpret_cast<const uint4*>(Wb + wo);
+            k.s2[ct] = *reinterpret_cast<const int2*>(WSb + so);
+            if (SCM == 2) {
+                const float2 f2 = *reinterpret_cast<const float2*>(Sb + so);
+                k.sc[ct][0] = f2.x;
+                k.sc[ct][1] = f2.y;
+            } else if (SCM == 1) {
+                k.sc[ct][0] = k.sc[ct][1] = a.S[grp_index(tl[ct] * 16 + col, 2 * c, a.ngrp, a.sc_shift)];
+            } else {
+                k.sc[ct][0] = k.sc[ct][1] = scv[ct];
+            }
+        }
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb) {
+            const int j = min(2 * c + jb, last_blk);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const uint32_t ao = ao0[rt] + (uint32_t)j * 64;
+                k.ah[jb][rt] = *reinterpret_cast<const uint64_t*>(Ab + ao);
+                k.al[jb][rt] = HP ? *reinterpret_cast<const uint64_t*>(Ab + ao + 32) : 0;
+                k.sav[jb][rt] = *reinterpret_cast<const float4*>(SaTb + sao0 + (uint32_t)j * sa_step + rt * 64);
+            }
+        }
+    };
+
+    float acc[2][4][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[rt][ct][i] = 0.0f;
+
+    // One 32-block: all h-byte MFMAs, then all l-byte MFMAs with
+    // (H << 8) + 128*S as accumulator input, then the in-lane epilogues, so
+    // the MFMA latencies overlap.
+    auto block = [&](const Chunk& k, int jb) {
+        uint64_t bop[4];
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) bop[ct] = unpack_b(k.w[ct], jb, 8);
+        v4i d[2][4];
+        if (HP) {
+            v4i hh[2][4];
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) hh[rt][ct] = mfma16(k.ah[jb][rt], bop[ct]);
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) {
+                const int s128 = jb ? k.s2[ct].y : k.s2[ct].x;
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    const v4i ci = {(hh[rt][ct][0] << 8) + s128, (hh[rt][ct][1] << 8) + s128,
+                                    (hh[rt][ct][2] << 8) + s128, (hh[rt][ct][3] << 8) + s128};
+                    d[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)k.al[jb][rt], (long)bop[ct], ci, 0, 0, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) d[rt][ct] = mfma16(k.ah[jb][rt], bop[ct]);
+        }
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const float sb = k.sc[ct][jb];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                const float sa4[4] = {k.sav[jb][rt].x, k.sav[jb][rt].y, k.sav[jb][rt].z, k.sav[jb][rt].w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[rt][ct][i] = __builtin_fmaf(sa4[i], (float)d[rt][ct][i] * sb, acc[rt][ct][i]);
+            }
+        }
+    };
+
+    // Two-slot ring over chunks: chunk c+1 is in flight while c computes.
+    // Loads are unconditional (clamped), so the compiler's waits stay exact.
+    // The last chunk has one block when nblk is odd.
+    Chunk k0, k1;
+    load_chunk(k0, 0);
+    const bool odd = a.nblk & 1;
+    const int pairs = nch >> 1;
+    for (int pc = 0; pc < pairs; ++pc) {
+        const int c = 2 * pc;
+        load_chunk(k1, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        block(k0, 0);
+        block(k0, 1);
+        load_chunk(k0, c + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        block(k1, 0);
+        if (!(odd && c + 1 == nch - 1)) block(k1, 1);
+    }
+    if (nch & 1) {
+        block(k0, 0);
+        if (!odd) block(k0, 1);
+    }
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            if (t_base + ct >= a.ntiles) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int m = m_base + rt * 16 + 4 * grp + i;
+                if (m < a.M) a.C[(size_t)m * a.N + (t_base + ct) * 16 + col] = acc[rt][ct][i];
+            }
+        }
+}
+
+template <bool HP>
+void launch_prefill(const PreArgs& p, dim3 grid, hipStream_t st) {
+    if (p.scm == 2) prefill_w8_kernel<HP, 2><<<grid, 256, 0, st>>>(p);
+    else if (p.scm == 1) prefill_w8_kernel<HP, 1><<<grid, 256, 0, st>>>(p);
+    else prefill_w8_kernel<HP, 0><<<grid, 256, 0, st>>>(p);
+}
+
 // ------------------------------------------------------------------ argmax
 
 __device__ inline unsigned long long block_max_key(unsigned long long k) {
@@ -759,6 +977,8 @@ struct Workspace {
     size_t rows_cap = 0, nblk4_cap = 0;
     unsigned long long* parts = nullptr;
     size_t parts_cap = 0;
+    float* sat = nullptr;  // block-major activation scales for the prefill GEMM
+    size_t sat_cap = 0;
     float* hA = nullptr;  // device staging for the host-pointer entry points
     float* hC = nullptr;
     size_t hA_cap = 0, hC_cap = 0;
@@ -942,7 +1162,16 @@ void* build_handle(const uint8_t* raw, bool raw_signed, const float* scales, int
         const size_t total = (size_t)(N / 16) * nbg * 64;
         const unsigned blocks = (unsigned)((total + 255) / 256);
         repack_kernel<<<blocks, 256>>>(draw, h->W, N, nblk, nbg, bits, raw_signed ? 1 : 0);
-        ok = hip_ok(hipGetLastError(), "repack launch") && hip_ok(hipDeviceSynchronize(), "repack");
+        ok = hip_ok(hipGetLastError(), "repack launch");
+        if (ok && bits == 8) {
+            const size_t n_ws = (size_t)(N / 16) * nbg * 16;
+            ok = hip_ok(hipMalloc(&h->WS, n_ws * 2 * sizeof(int32_t)), "weight-sum alloc");
+            if (ok) {
+                wsum_kernel<<<(unsigned)((n_ws + 255) / 256), 256>>>(h->W, h->WS, N / 16, nbg);
+                ok = hip_ok(hipGetLastError(), "weight-sum launch");
+            }
+        }
+        ok = ok && hip_ok(hipDeviceSynchronize(), "repack");
     }
     if (draw) (void)hipFree(draw);
     if (!ok) {
@@ -950,10 +1179,12 @@ void* build_handle(const uint8_t* raw, bool raw_signed, const float* scales, int
         if (h->S) (void)hipFree(h->S);
         if (h->Z) (void)hipFree(h->Z);
         if (h->D) (void)hipFree(h->D);
+        if (h->WS) (void)hipFree(h->WS);
         delete h;
         return nullptr;
     }
-    h->dev_bytes = wbytes + sc_dev.size() * 4 + zp_dev.size() + dl_dev.size() * 4;
+    h->dev_bytes = wbytes + sc_dev.size() * 4 + zp_dev.size() + dl_dev.size() * 4 +
+                   (h->WS ? (size_t)(N / 16) * nbg * 16 * 2 * 4 : 0);
     return h;
 }
 
@@ -1093,12 +1324,17 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     const int lds = (M <= 8 && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     const bool dec = lds > 0;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
+    // Prefill GEMM: more than 8 rows of INT8 weights without a legacy corr.
+    const bool pre = !dec && !dots && M > 8 && h->bits == 8 && h->WS && !h->D;
+    const int Mpad = (M + kPreRows - 1) / kPreRows * kPreRows;
     if (!fused) {
         if (!ensure_quant(w, M, h->nblk4)) return -4;
+        if (pre && !grow(&w.sat, &w.sat_cap, (size_t)h->nblk * Mpad, "workspace alloc")) return -4;
+        float* sat = pre ? w.sat : nullptr;
         const size_t threads = (size_t)M * h->nblk * 8;
         const unsigned qb = (unsigned)((threads + 255) / 256);
-        if (hp) quantize_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq);
-        else quantize_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq);
+        if (hp) quantize_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq, sat, Mpad);
+        else quantize_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq, sat, Mpad);
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
         a.Aq = w.aq;
         a.Sa = w.sa;
@@ -1130,6 +1366,27 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
                                  : launch_dec_bits<8, false>(w, a, grid, lds, units, fused, x, st);
         else e = hp ? launch_dec_bits<4, true>(w, a, grid, lds, units, fused, x, st)
                     : launch_dec_bits<4, false>(w, a, grid, lds, units, fused, x, st);
+    } else if (pre) {
+        PreArgs p{};
+        p.W = h->W;
+        p.S = h->S;
+        p.WS = h->WS;
+        p.Aq = w.aq;
+        p.SaT = w.sat;
+        p.C = dC;
+        p.M = M;
+        p.N = h->N;
+        p.nblk = h->nblk;
+        p.nbg = h->nbg;
+        p.ngrp = h->ngrp;
+        p.sc_shift = h->sc_shift;
+        p.ntiles = h->N / 16;
+        p.Mpad = Mpad;
+        p.scm = h->sc_blk ? 2 : (h->sc_shift == 31 ? 0 : 1);
+        const dim3 grid((unsigned)((h->N + kPreCols - 1) / kPreCols), (unsigned)(Mpad / kPreRows));
+        if (hp) launch_prefill<true>(p, grid, st);
+        else launch_prefill<false>(p, grid, st);
+        e = hipGetLastError();
     } else {
         const dim3 grid(a.ntiles, (M + kRowsPerWG - 1) / kRowsPerWG);
         if (h->bits == 8) e = hp ? launch_rows_bits<8, true>(a, grid, dots, st)
@@ -1330,6 +1587,7 @@ void i4_free(void* handle) {
     (void)hipFree(h->S);
     if (h->Z) (void)hipFree(h->Z);
     if (h->D) (void)hipFree(h->D);
+    if (h->WS) (void)hipFree(h->WS);
     (void)hipSetDevice(cur);
     h->magic = 0;
     delete h;
