@@ -32,6 +32,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <limits>
 #include <mutex>
@@ -252,13 +253,11 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint4* __restrict
 // ------------------------------------------------------------------ quantize
 
 // Stand-alone activation quantizer: 8 lanes per (row, block).  Records go
-// to Aq [M][nblk][64 B]; scale and sum(q) to Sa/Sq [M][nblk4]; with SaT, the
-// scales also block-major to SaT [nblk][Mpad] (for the prefill GEMM).
+// to Aq [M][nblk][64 B]; scale and sum(q) to Sa/Sq [M][nblk4].
 template <bool HP>
 __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ A, int M, int K,
                                                        int nblk, int nblk4, uint8_t* __restrict__ Aq,
-                                                       float* __restrict__ Sa, int* __restrict__ Sq,
-                                                       float* __restrict__ SaT, int Mpad) {
+                                                       float* __restrict__ Sa, int* __restrict__ Sq) {
     const int gtid = blockIdx.x * 256 + threadIdx.x;
     const int blk = gtid >> 3, e = gtid & 7;
     const bool valid = blk < M * nblk;
@@ -276,7 +275,6 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         if (e == 0) {
             Sa[(size_t)m * nblk4 + j] = s;
             Sq[(size_t)m * nblk4 + j] = sum;
-            if (SaT) SaT[(size_t)j * Mpad + m] = s;
         }
     }
 }
@@ -740,194 +738,295 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
 
 // ------------------------------------------------------------------ prefill GEMM (M > 8, INT8 weights)
 //
-// Workgroup tile 64 rows x 128 columns over all K; four waves as 2 x 2, each
-// 32 rows (two 16-row MFMA tiles) x 64 columns (four 16-column tiles).  Per
-// 32-block and 16 x 16 tile: H = sum(h*b) by one v_mfma_i32_16x16x32_i8, then
-// (H << 8) + 128*S as the accumulator input of the l-byte MFMA gives the
-// exact block integer cs, and the in-lane epilogue folds
-// acc = fma(s_a, f32(cs) * s_b, acc) in block order.  The weights are read in
-// their decode layout (the B operand directly), the activations from the
-// stand-alone quantizer's records, block-major scales and weight sums.
+// One workgroup of 8 waves computes 128 rows x 16*CT columns over all of K;
+// wave w owns the 16-row tile w of the group and all CT column tiles.  Per
+// 32-block and tile, H = sum(h*b) comes from one v_mfma_i32_16x16x32_i8,
+// (H << 8) + 128*S is the accumulator input of the l-byte MFMA, which then
+// holds the exact block integer cs, and the lane folds
+// acc = fma(s_a, f32(cs) * s_b, acc) in block order.
+//
+// Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4,
+// 16 bytes per lane to LDS address M0 + 16*lane) through a ring of
+// kPfStages stages.  A stage holds one chunk (two blocks): the CT weight
+// tiles (1 KB each; the decode layout is the MFMA B operand), their weight
+// sums and scales (the shared part, loaded by all waves together), and each
+// wave's activation record.  The compiler does not see these loads: every
+// wave waits for its own with an explicit vmcnt, then the workgroup barrier
+// publishes the stage.
 
-constexpr int kPreRows = 64, kPreCols = 128;
+constexpr int kPfWaves = 8, kPfRows = 16 * kPfWaves, kPfStages = 3;
+// Activation record per (16-row tile, chunk): [block 2][lane 64][h 8 B, l 8 B]
+// in MFMA A-operand order (lane: row lane&15, k-octet lane>>4), then the
+// block scales [block 2][row 16] float.
+constexpr int kRecA = 2048, kRecBytes = kRecA + 128;
 
-struct PreArgs {
-    const uint4* W;
-    const float* S;
-    const int32_t* WS;
-    const uint8_t* Aq;   // [M][nblk][64]
-    const float* SaT;    // [nblk][Mpad]
-    float* C;            // [M][N]
-    int M, N, nblk, nbg, ngrp, sc_shift, ntiles, Mpad, scm;
+struct PfArgs {
+    const char* W;   // [ntiles][nch][64 lanes][16 B]
+    const char* WS;  // [ntiles][nch][16][2] int32
+    const char* S;   // scales (grp_index / blk_index layouts)
+    const char* R;   // activation records [Mpad/16][nch][kRecBytes]
+    float* C;        // [M][N]
+    int M, N, nblk, nch, ngrp, sc_shift, ntiles;
 };
 
 // SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
-template <bool HP, int SCM>
-__global__ __launch_bounds__(256) void prefill_w8_kernel(PreArgs a) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wr = wave >> 1, wc = wave & 1;
-    const int col = lane & 15, grp = lane >> 4;  // output lane: column col, rows 4*grp .. 4*grp+3
-    const int arow = lane & 15, kq = lane >> 4;  // A operand lane: row arow, k-octet kq
-    const int m_base = blockIdx.y * kPreRows + wr * 32;
-    const int t_base = blockIdx.x * (kPreCols / 16) + wc * 4;
-    const char* Wb = reinterpret_cast<const char*>(a.W);
-    const char* WSb = reinterpret_cast<const char*>(a.WS);
-    const char* Sb = reinterpret_cast<const char*>(a.S);
-    const char* Ab = reinterpret_cast<const char*>(a.Aq);
-    const char* SaTb = reinterpret_cast<const char*>(a.SaT);
+template <int CT, int SCM>
+struct PfLayout {
+    static constexpr int kWS = CT * 1024;
+    static constexpr int kSB = kWS + CT * 128;
+    static constexpr int kShared = kSB + (SCM == 2 ? CT * 128 : SCM == 1 ? CT * 64 : 0);
+    static constexpr int kA = kShared;
+    static constexpr int kStage = kA + kPfWaves * kRecBytes;
+    static constexpr int kUnits = (kShared + 1023) / 1024;
+    static constexpr int kPerWave = (kUnits + kPfWaves - 1) / kPfWaves;
+    static constexpr int kDma = kPerWave + 3;  // loads per wave per chunk
+    static constexpr int kBytes = kPfStages * kStage;
+    static_assert(kShared % 64 == 0 && kDma < 64, "layout");
+};
 
-    // 32-bit byte offsets from the uniform base pointers, so every load is a
-    // base + offset form.  Chunk c covers blocks 2c and 2c+1.
-    uint32_t ao0[2], wo0[4], so0[4];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const int r = min(m_base + rt * 16 + arow, a.M - 1);
-        ao0[rt] = (uint32_t)r * a.nblk * 64 + kq * 8;
-    }
-    float scv[4];
-    int tl[4];
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-        tl[ct] = min(t_base + ct, a.ntiles - 1);
-        wo0[ct] = ((uint32_t)tl[ct] * a.nbg * 64 + lane) * 16;
-        so0[ct] = ((uint32_t)tl[ct] * a.nbg * 16 + col) * 8;  // int2 / float2 per (chunk, column)
-        scv[ct] = SCM == 0 ? a.S[grp_index(tl[ct] * 16 + col, 0, a.ngrp, a.sc_shift)] : 0.0f;
-    }
-    const uint32_t sao0 = (uint32_t)(m_base + 4 * grp) * 4;
-    const uint32_t sa_step = (uint32_t)a.Mpad * 4;
-    const int nch = a.nbg;  // chunks; the last one has one block when nblk is odd
-    const int last_blk = a.nblk - 1;
-
-    // Everything one chunk needs: weights, weight sums, scales, and the A
-    // operands and activation scales of both blocks.
-    struct Chunk {
-        uint4 w[4];
-        int2 s2[4];
-        float sc[4][2];
-        uint64_t ah[2][2], al[2][2];
-        float4 sav[2][2];
-    };
-    auto load_chunk = [&](Chunk& k, int c) {
-        c = min(c, nch - 1);  // past the end: reload the last chunk (not used)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            const uint32_t wo = wo0[ct] + (uint32_t)c * 1024, so = so0[ct] + (uint32_t)c * 128;
-            k.w[ct] = *reinterpret_cast<const uint4*>(Wb + wo);
-            k.s2[ct] = *reinterpret_cast<const int2*>(WSb + so);
-            if (SCM == 2) {
-                const float2 f2 = *reinterpret_cast<const float2*>(Sb + so);
-                k.sc[ct][0] = f2.x;
-                k.sc[ct][1] = f2.y;
-            } else if (SCM == 1) {
-                k.sc[ct][0] = k.sc[ct][1] = a.S[grp_index(tl[ct] * 16 + col, 2 * c, a.ngrp, a.sc_shift)];
-            } else {
-                k.sc[ct][0] = k.sc[ct][1] = scv[ct];
-            }
-        }
-#pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-            const int j = min(2 * c + jb, last_blk);
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const uint32_t ao = ao0[rt] + (uint32_t)j * 64;
-                k.ah[jb][rt] = *reinterpret_cast<const uint64_t*>(Ab + ao);
-                k.al[jb][rt] = HP ? *reinterpret_cast<const uint64_t*>(Ab + ao + 32) : 0;
-                k.sav[jb][rt] = *reinterpret_cast<const float4*>(SaTb + sao0 + (uint32_t)j * sa_step + rt * 64);
-            }
-        }
-    };
-
-    float acc[2][4][4];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[rt][ct][i] = 0.0f;
-
-    // One 32-block: all h-byte MFMAs, then all l-byte MFMAs with
-    // (H << 8) + 128*S as accumulator input, then the in-lane epilogues, so
-    // the MFMA latencies overlap.
-    auto block = [&](const Chunk& k, int jb) {
-        uint64_t bop[4];
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) bop[ct] = unpack_b(k.w[ct], jb, 8);
-        v4i d[2][4];
-        if (HP) {
-            v4i hh[2][4];
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) hh[rt][ct] = mfma16(k.ah[jb][rt], bop[ct]);
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) {
-                const int s128 = jb ? k.s2[ct].y : k.s2[ct].x;
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    const v4i ci = {(hh[rt][ct][0] << 8) + s128, (hh[rt][ct][1] << 8) + s128,
-                                    (hh[rt][ct][2] << 8) + s128, (hh[rt][ct][3] << 8) + s128};
-                    d[rt][ct] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)k.al[jb][rt], (long)bop[ct], ci, 0, 0, 0);
-                }
-            }
-        } else {
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) d[rt][ct] = mfma16(k.ah[jb][rt], bop[ct]);
-        }
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            const float sb = k.sc[ct][jb];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                const float sa4[4] = {k.sav[jb][rt].x, k.sav[jb][rt].y, k.sav[jb][rt].z, k.sav[jb][rt].w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[rt][ct][i] = __builtin_fmaf(sa4[i], (float)d[rt][ct][i] * sb, acc[rt][ct][i]);
-            }
-        }
-    };
-
-    // Two-slot ring over chunks: chunk c+1 is in flight while c computes.
-    // Loads are unconditional (clamped), so the compiler's waits stay exact.
-    // The last chunk has one block when nblk is odd.
-    Chunk k0, k1;
-    load_chunk(k0, 0);
-    const bool odd = a.nblk & 1;
-    const int pairs = nch >> 1;
-    for (int pc = 0; pc < pairs; ++pc) {
-        const int c = 2 * pc;
-        load_chunk(k1, c + 1);
-        __builtin_amdgcn_sched_barrier(0);
-        block(k0, 0);
-        block(k0, 1);
-        load_chunk(k0, c + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        block(k1, 0);
-        if (!(odd && c + 1 == nch - 1)) block(k1, 1);
-    }
-    if (nch & 1) {
-        block(k0, 0);
-        if (!odd) block(k0, 1);
-    }
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            if (t_base + ct >= a.ntiles) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int m = m_base + rt * 16 + 4 * grp + i;
-                if (m < a.M) a.C[(size_t)m * a.N + (t_base + ct) * 16 + col] = acc[rt][ct][i];
-            }
-        }
+__device__ inline uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
 
+// 16 bytes per lane from global `src` to LDS byte address lds + 16*lane.
+__device__ inline void dma16(const void* src, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+// s_waitcnt immediate: vmcnt(n), no wait on the other counters.
+__host__ __device__ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+
+template <bool HP, int SCM, int CT>
+__global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
+    using L = PfLayout<CT, SCM>;
+    extern __shared__ __align__(16) char pf_lds[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const int t0 = blockIdx.x * CT;
+    const int rt = blockIdx.y * kPfWaves + wave;  // this wave's 16-row tile
+    const bool active = rt * 16 < a.M;
+    const uint32_t lds0 = lds_address(pf_lds);
+    const int nch = a.nch;
+
+    // Per-column scales (SCM 0) are loaded and waited for before the first
+    // direct load, so no compiler wait inside the loop counts those.
+    float sbc[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        sbc[ct] = 0.0f;
+        if (SCM == 0) {
+            sbc[ct] = reinterpret_cast<const float*>(a.S)[(size_t)min(t0 + ct, a.ntiles - 1) * a.ngrp * 16 + col];
+            asm volatile("" ::"v"(sbc[ct]));
+        }
+    }
+
+    // Shared part: slot k of this wave loads the 1 KB at
+    // x0 = min(u * 1024, kShared - 1024), u = k * kPfWaves + wave (clamped),
+    // lane bytes x0 + 16*lane.  Overlapping slots write equal bytes.
+    const char* src0[L::kPerWave];
+    uint32_t step[L::kPerWave], gstep[L::kPerWave], x0s[L::kPerWave];
+#pragma unroll
+    for (int k = 0; k < L::kPerWave; ++k) {
+        const int u = min(k * kPfWaves + wave, L::kUnits - 1);
+        const int x0 = min(u * 1024, L::kShared - 1024);
+        const int x = x0 + 16 * lane;
+        x0s[k] = (uint32_t)x0;
+        gstep[k] = 0;
+        if (x < L::kWS) {
+            const int tc = min(t0 + (x >> 10), a.ntiles - 1);
+            src0[k] = a.W + (size_t)tc * nch * 1024 + (x & 1023);
+            step[k] = 1024;
+        } else if (x < L::kSB) {
+            const int y = x - L::kWS;
+            const int tc = min(t0 + (y >> 7), a.ntiles - 1);
+            src0[k] = a.WS + (size_t)tc * nch * 128 + (y & 127);
+            step[k] = 128;
+        } else if (SCM == 2) {
+            const int y = x - L::kSB;
+            const int tc = min(t0 + (y >> 7), a.ntiles - 1);
+            src0[k] = a.S + (size_t)tc * nch * 128 + (y & 127);
+            step[k] = 128;
+        } else {
+            const int y = x - L::kSB;
+            const int tc = min(t0 + (y >> 6), a.ntiles - 1);
+            src0[k] = a.S + (size_t)tc * a.ngrp * 64 + (y & 63);
+            step[k] = 0;
+            gstep[k] = 64;
+        }
+    }
+    const char* rec0 = a.R + (size_t)rt * nch * kRecBytes + 16 * lane;
+
+    auto issue = [&](int c, int stage) {
+        const uint32_t sbase = lds0 + (uint32_t)(stage * L::kStage);
+        const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
+#pragma unroll
+        for (int k = 0; k < L::kPerWave; ++k)
+            dma16(src0[k] + (size_t)c * step[k] + g * gstep[k], sbase + x0s[k]);
+        const char* rec = rec0 + (size_t)c * kRecBytes;
+        const uint32_t abase = sbase + (uint32_t)(L::kA + wave * kRecBytes);
+        dma16(rec, abase);
+        dma16(rec + 1024, abase + 1024);
+        dma16(rec + 1152, abase + 1152);
+    };
+
+    float acc[CT][4];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ct][i] = 0.0f;
+
+    // One chunk (NB = 2 blocks, or 1 for the last chunk of an odd block
+    // count) from stage memory st.
+    auto compute = [&](const char* st, auto nb_tag) {
+        constexpr int NB = decltype(nb_tag)::value;
+        const char* ar = st + L::kA + wave * kRecBytes;
+        uint64_t ah[2], al[2];
+        float sa[2][4];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const uint4 r = *reinterpret_cast<const uint4*>(ar + b * 1024 + 16 * lane);
+            ah[b] = (uint64_t)r.y << 32 | r.x;
+            al[b] = (uint64_t)r.w << 32 | r.z;
+            const float4 s4 = *reinterpret_cast<const float4*>(ar + kRecA + b * 64 + 16 * grp);
+            sa[b][0] = s4.x;
+            sa[b][1] = s4.y;
+            sa[b][2] = s4.z;
+            sa[b][3] = s4.w;
+        }
+        constexpr int G = 4;
+#pragma unroll
+        for (int g0 = 0; g0 < CT; g0 += G) {
+            uint4 bw[G];
+            int2 ws[G];
+            float sb[G][2];
+#pragma unroll
+            for (int t = 0; t < G; ++t) {
+                const int ct = g0 + t;
+                if (ct >= CT) continue;
+                bw[t] = *reinterpret_cast<const uint4*>(st + ct * 1024 + 16 * lane);
+                ws[t] = *reinterpret_cast<const int2*>(st + L::kWS + ct * 128 + 8 * col);
+                if (SCM == 2) {
+                    const float2 f = *reinterpret_cast<const float2*>(st + L::kSB + ct * 128 + 8 * col);
+                    sb[t][0] = f.x;
+                    sb[t][1] = f.y;
+                } else if (SCM == 1) {
+                    sb[t][0] = sb[t][1] = *reinterpret_cast<const float*>(st + L::kSB + ct * 64 + 4 * col);
+                } else {
+                    sb[t][0] = sb[t][1] = sbc[ct];
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                v4i d[G];
+#pragma unroll
+                for (int t = 0; t < G; ++t) {
+                    if (g0 + t >= CT) continue;
+                    const uint64_t bop = b == 0 ? ((uint64_t)bw[t].y << 32 | bw[t].x)
+                                                : ((uint64_t)bw[t].w << 32 | bw[t].z);
+                    if (HP) {
+                        const v4i hh = mfma16(ah[b], bop);
+                        const int s128 = b == 0 ? ws[t].x : ws[t].y;
+                        const v4i ci = {(hh[0] << 8) + s128, (hh[1] << 8) + s128, (hh[2] << 8) + s128,
+                                        (hh[3] << 8) + s128};
+                        d[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)al[b], (long)bop, ci, 0, 0, 0);
+                    } else {
+                        d[t] = mfma16(ah[b], bop);
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < G; ++t) {
+                    const int ct = g0 + t;
+                    if (ct >= CT) continue;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[ct][i] = __builtin_fmaf(sa[b][i], (float)d[t][i] * sb[t][b], acc[ct][i]);
+                }
+            }
+        }
+    };
+
+#pragma unroll
+    for (int s = 0; s < kPfStages - 1; ++s)
+        if (s < nch) issue(s, s);
+    const bool odd = a.nblk & 1;
+    int st = 0;
+    for (int c = 0; c < nch; ++c) {
+        // This wave's loads of chunk c have landed once at most the loads of
+        // chunk c+1 (issued later) are outstanding.
+        if (c + 1 < nch) __builtin_amdgcn_s_waitcnt(vm_wait(L::kDma));
+        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        lds_barrier();  // every wave's part of chunk c is in; chunk c-1 is consumed
+        if (c + kPfStages - 1 < nch) issue(c + kPfStages - 1, st == 0 ? kPfStages - 1 : st - 1);
+        if (active) {
+            const char* sp = pf_lds + st * L::kStage;
+            if (c + 1 < nch || !odd) compute(sp, std::integral_constant<int, 2>{});
+            else compute(sp, std::integral_constant<int, 1>{});
+        }
+        st = st == kPfStages - 1 ? 0 : st + 1;
+    }
+    if (!active) return;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+        const int tile = t0 + ct;
+        if (tile >= a.ntiles) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int m = rt * 16 + 4 * grp + i;
+            if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + col] = acc[ct][i];
+        }
+    }
+}
+
+// Activation records for the prefill GEMM: 8 lanes per (row, block) over
+// Mpad rows and 2*nch blocks; padding rows and blocks quantize zeros.
 template <bool HP>
-void launch_prefill(const PreArgs& p, dim3 grid, hipStream_t st) {
-    if (p.scm == 2) prefill_w8_kernel<HP, 2><<<grid, 256, 0, st>>>(p);
-    else if (p.scm == 1) prefill_w8_kernel<HP, 1><<<grid, 256, 0, st>>>(p);
-    else prefill_w8_kernel<HP, 0><<<grid, 256, 0, st>>>(p);
+__global__ __launch_bounds__(256) void quantize_rec_kernel(const float* __restrict__ A, int M, int K, int nblk,
+                                                           int nch, int Mpad, uint8_t* __restrict__ R) {
+    const int gtid = blockIdx.x * 256 + threadIdx.x;
+    const int blk = gtid >> 3, e = gtid & 7;
+    const int nb2 = 2 * nch;
+    const int m = blk / nb2, j = blk - m * nb2;
+    const bool inside = m < Mpad;
+    const bool valid = m < M && j < nblk;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) v = *reinterpret_cast<const float4*>(A + (size_t)m * K + 32 * j + 4 * e);
+    float s;
+    int sum;
+    uint32_t p0, p1;
+    quant8<HP>(v, s, sum, p0, p1);
+    if (inside) {
+        uint8_t* rec = R + ((size_t)(m >> 4) * nch + (j >> 1)) * kRecBytes;
+        const int b = j & 1, r = m & 15;
+        uint8_t* p = rec + b * 1024 + ((e >> 1) * 16 + r) * 16 + (e & 1) * 4;
+        *reinterpret_cast<uint32_t*>(p) = p0;
+        *reinterpret_cast<uint32_t*>(p + 8) = p1;
+        if (e == 0) *reinterpret_cast<float*>(rec + kRecA + (b * 16 + r) * 4) = s;
+    }
+}
+
+// Column tiles per workgroup: the instantiated widths, and the choice that
+// minimizes (workgroup rounds) x (tiles per workgroup) at one workgroup per
+// CU.  `force` (the BREEZE_HIP_PREFILL_CT environment variable) selects an
+// instantiated width instead, for tests and tuning.
+constexpr int kPfCts[] = {17, 16, 8, 4};
+
+int pick_pf_ct(int ntiles, int gy, int n_cu, const char* force) {
+    if (force) {
+        const int v = std::atoi(force);
+        for (int ct : kPfCts)
+            if (ct == v) return ct;
+    }
+    int best = kPfCts[0];
+    long best_cost = -1;
+    for (int ct : kPfCts) {
+        const long wgs = (long)((ntiles + ct - 1) / ct) * gy;
+        const long cost = (wgs + n_cu - 1) / n_cu * ct;
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = ct;
+        }
+    }
+    return best;
 }
 
 // ------------------------------------------------------------------ argmax
@@ -977,8 +1076,9 @@ struct Workspace {
     size_t rows_cap = 0, nblk4_cap = 0;
     unsigned long long* parts = nullptr;
     size_t parts_cap = 0;
-    float* sat = nullptr;  // block-major activation scales for the prefill GEMM
-    size_t sat_cap = 0;
+    uint8_t* rec = nullptr;  // prefill activation records
+    size_t rec_cap = 0;
+    bool pf_attr[64] = {};
     float* hA = nullptr;  // device staging for the host-pointer entry points
     float* hC = nullptr;
     size_t hA_cap = 0, hC_cap = 0;
@@ -1268,6 +1368,40 @@ hipError_t launch_rows_bits(const GemvArgs& a, dim3 grid, bool dots, hipStream_t
     return hipGetLastError();
 }
 
+template <bool HP, int SCM, int CT>
+hipError_t launch_pf_t(Workspace& w, const PfArgs& p, dim3 grid, hipStream_t st) {
+    using L = PfLayout<CT, SCM>;
+    auto kern = prefill_w8_kernel<HP, SCM, CT>;
+    int slot = 0;
+    while (kPfCts[slot] != CT) ++slot;
+    const int key = (HP ? 1 : 0) | SCM << 1 | slot << 3;
+    if (!w.pf_attr[key]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+        if (e != hipSuccess) return e;
+        w.pf_attr[key] = true;
+    }
+    kern<<<grid, kPfWaves * 64, L::kBytes, st>>>(p);
+    return hipGetLastError();
+}
+
+template <bool HP, int SCM>
+hipError_t launch_pf_scm(Workspace& w, const PfArgs& p, int ct, dim3 grid, hipStream_t st) {
+    switch (ct) {
+        case 17: return launch_pf_t<HP, SCM, 17>(w, p, grid, st);
+        case 16: return launch_pf_t<HP, SCM, 16>(w, p, grid, st);
+        case 8: return launch_pf_t<HP, SCM, 8>(w, p, grid, st);
+        default: return launch_pf_t<HP, SCM, 4>(w, p, grid, st);
+    }
+}
+
+template <bool HP>
+hipError_t launch_pf(Workspace& w, const PfArgs& p, int scm, int ct, dim3 grid, hipStream_t st) {
+    if (scm == 2) return launch_pf_scm<HP, 2>(w, p, ct, grid, st);
+    if (scm == 1) return launch_pf_scm<HP, 1>(w, p, ct, grid, st);
+    return launch_pf_scm<HP, 0>(w, p, ct, grid, st);
+}
+
 int device_cus(Workspace& w, int dev) {
     if (w.n_cu == 0) {
         int n = 0;
@@ -1325,16 +1459,22 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     const bool dec = lds > 0;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
     // Prefill GEMM: more than 8 rows of INT8 weights without a legacy corr.
-    const bool pre = !dec && !dots && M > 8 && h->bits == 8 && h->WS && !h->D;
-    const int Mpad = (M + kPreRows - 1) / kPreRows * kPreRows;
-    if (!fused) {
+    const bool pre = !dec && !dots && M > 8 && h->bits == 8 && h->WS && !h->has_dl;
+    const int Mpad = (M + kPfRows - 1) / kPfRows * kPfRows;
+    if (pre) {
+        // Records in MFMA operand order for the prefill GEMM.
+        if (!grow(&w.rec, &w.rec_cap, (size_t)(Mpad / 16) * h->nbg * kRecBytes, "workspace alloc")) return -4;
+        const size_t threads = (size_t)Mpad * h->nbg * 2 * 8;
+        const unsigned qb = (unsigned)((threads + 255) / 256);
+        if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nbg, Mpad, w.rec);
+        else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nbg, Mpad, w.rec);
+        if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
+    } else if (!fused) {
         if (!ensure_quant(w, M, h->nblk4)) return -4;
-        if (pre && !grow(&w.sat, &w.sat_cap, (size_t)h->nblk * Mpad, "workspace alloc")) return -4;
-        float* sat = pre ? w.sat : nullptr;
         const size_t threads = (size_t)M * h->nblk * 8;
         const unsigned qb = (unsigned)((threads + 255) / 256);
-        if (hp) quantize_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq, sat, Mpad);
-        else quantize_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq, sat, Mpad);
+        if (hp) quantize_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq);
+        else quantize_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, w.aq, w.sa, w.sq);
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
         a.Aq = w.aq;
         a.Sa = w.sa;
@@ -1367,25 +1507,24 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
         else e = hp ? launch_dec_bits<4, true>(w, a, grid, lds, units, fused, x, st)
                     : launch_dec_bits<4, false>(w, a, grid, lds, units, fused, x, st);
     } else if (pre) {
-        PreArgs p{};
-        p.W = h->W;
-        p.S = h->S;
-        p.WS = h->WS;
-        p.Aq = w.aq;
-        p.SaT = w.sat;
+        PfArgs p{};
+        p.W = reinterpret_cast<const char*>(h->W);
+        p.WS = reinterpret_cast<const char*>(h->WS);
+        p.S = reinterpret_cast<const char*>(h->S);
+        p.R = reinterpret_cast<const char*>(w.rec);
         p.C = dC;
         p.M = M;
         p.N = h->N;
         p.nblk = h->nblk;
-        p.nbg = h->nbg;
+        p.nch = h->nbg;
         p.ngrp = h->ngrp;
         p.sc_shift = h->sc_shift;
         p.ntiles = h->N / 16;
-        p.Mpad = Mpad;
-        p.scm = h->sc_blk ? 2 : (h->sc_shift == 31 ? 0 : 1);
-        const dim3 grid((unsigned)((h->N + kPreCols - 1) / kPreCols), (unsigned)(Mpad / kPreRows));
-        if (hp) launch_prefill<true>(p, grid, st);
-        else launch_prefill<false>(p, grid, st);
+        const int scm = h->sc_blk ? 2 : (h->sc_shift == 31 ? 0 : 1);
+        const int gy = Mpad / kPfRows;
+        const int ct = pick_pf_ct(p.ntiles, gy, device_cus(w, dev), std::getenv("BREEZE_HIP_PREFILL_CT"));
+        const dim3 grid((unsigned)((p.ntiles + ct - 1) / ct), (unsigned)gy);
+        e = hp ? launch_pf<true>(w, p, scm, ct, grid, st) : launch_pf<false>(w, p, scm, ct, grid, st);
         e = hipGetLastError();
     } else {
         const dim3 grid(a.ntiles, (M + kRowsPerWG - 1) / kRowsPerWG);

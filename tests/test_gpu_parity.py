@@ -185,3 +185,35 @@ def test_argmax_first_max_semantics(gpu, hb, hi_prec):
         np.testing.assert_array_equal(idx.cpu().numpy(), np.argmax(logits.cpu().numpy(), axis=1))
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("scales", ["channel", "group", "block"])
+@pytest.mark.parametrize("ct", ["auto", "17", "16", "8", "4"])
+def test_prefill_gemm_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
+    """The M > 8 INT8 GEMM against the oracle: per-column, per-group (4 blocks)
+    and per-block scales; every column-tile width, with a partial last column
+    group (19 tiles); an odd block count (33, so the last chunk and the last
+    scale group are partial); row counts around the 128-row workgroup; and
+    activations with x20 outliers for the hi/lo split."""
+    if ct != "auto":
+        monkeypatch.setenv("BREEZE_HIP_PREFILL_CT", ct)
+    N, K = 304, 1056
+    rng = np.random.default_rng(11)
+    qw, sc, _ = rng_weights(rng, N, K, 8)
+    if scales == "channel":
+        sc = np.repeat(sc[:, :1], K // 32, axis=1)
+    elif scales == "group":
+        sc = np.repeat(sc[:, ::4], 4, axis=1)[:, :K // 32]
+    h = hb.prepack(qw, sc, None, K, N, bits=8)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for rows in (9, 130, 300):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                A[rng.random(A.shape) < 0.01] *= 20.0
+                want = orc.matmul(qw, sc, None, N, K, 8, A, hp)
+                got = hb.matmul(h, gpu.from_numpy(A).cuda(), N)
+                gpu.cuda.synchronize()
+                assert bits_equal(got.cpu().numpy(), want), (hp, rows)
+    finally:
+        hb.free(h)
