@@ -754,7 +754,9 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
 // wave waits for its own with an explicit vmcnt, then the workgroup barrier
 // publishes the stage.
 
-constexpr int kPfWaves = 8, kPfRows = 16 * kPfWaves, kPfStages = 3;
+constexpr int kPfWaves = 8, kPfRows = 16 * kPfWaves;
+// Ring of kPfStages stages of kPfChunks chunks each.
+constexpr int kPfStages = 2, kPfChunks = 2;
 // Activation record per (16-row tile, chunk): [block 2][lane 64][h 8 B, l 8 B]
 // in MFMA A-operand order (lane: row lane&15, k-octet lane>>4), then the
 // block scales [block 2][row 16] float.
@@ -770,18 +772,20 @@ struct PfArgs {
 };
 
 // SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
+// One chunk's LDS region: [CT weight tiles, 1 KB each][weight sums, 128 B
+// per tile][block or group scales][8 activation records].
 template <int CT, int SCM>
 struct PfLayout {
     static constexpr int kWS = CT * 1024;
     static constexpr int kSB = kWS + CT * 128;
     static constexpr int kShared = kSB + (SCM == 2 ? CT * 128 : SCM == 1 ? CT * 64 : 0);
     static constexpr int kA = kShared;
-    static constexpr int kStage = kA + kPfWaves * kRecBytes;
+    static constexpr int kChunk = kA + kPfWaves * kRecBytes;
+    static constexpr int kStage = kPfChunks * kChunk;
     static constexpr int kUnits = (kShared + 1023) / 1024;
     static constexpr int kPerWave = (kUnits + kPfWaves - 1) / kPfWaves;
-    static constexpr int kDma = kPerWave + 3;  // loads per wave per chunk
     static constexpr int kBytes = kPfStages * kStage;
-    static_assert(kShared % 64 == 0 && kDma < 64, "layout");
+    static_assert(kShared % 64 == 0 && kBytes <= 160 * 1024, "layout");
 };
 
 __device__ inline uint32_t lds_address(const void* p) {
@@ -800,27 +804,21 @@ template <bool HP, int SCM, int CT>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
     using L = PfLayout<CT, SCM>;
     extern __shared__ __align__(16) char pf_lds[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int col = lane & 15, grp = lane >> 4;
+    // Wave w: row pair w&3 (two 16-row tiles) and column half w>>2, so each
+    // SIMD (waves w and w+4) holds one wave of each half.
+    const int rp = wave & 3, half = wave >> 2;
     const int t0 = blockIdx.x * CT;
-    const int rt = blockIdx.y * kPfWaves + wave;  // this wave's 16-row tile
-    const bool active = rt * 16 < a.M;
-    const uint32_t lds0 = lds_address(pf_lds);
+    const int rt0 = blockIdx.y * kPfWaves + 2 * rp;
+    const bool active = rt0 * 16 < a.M;
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(pf_lds));
     const int nch = a.nch;
+    const int nst = (nch + kPfChunks - 1) / kPfChunks;
+    const bool odd = a.nblk & 1;
 
-    // Per-column scales (SCM 0) are loaded and waited for before the first
-    // direct load, so no compiler wait inside the loop counts those.
-    float sbc[CT];
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-        sbc[ct] = 0.0f;
-        if (SCM == 0) {
-            sbc[ct] = reinterpret_cast<const float*>(a.S)[(size_t)min(t0 + ct, a.ntiles - 1) * a.ngrp * 16 + col];
-            asm volatile("" ::"v"(sbc[ct]));
-        }
-    }
-
-    // Shared part: slot k of this wave loads the 1 KB at
+    // Shared part of a chunk: slot k of this wave loads the 1 KB at
     // x0 = min(u * 1024, kShared - 1024), u = k * kPfWaves + wave (clamped),
     // lane bytes x0 + 16*lane.  Overlapping slots write equal bytes.
     const char* src0[L::kPerWave];
@@ -854,127 +852,198 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
             gstep[k] = 64;
         }
     }
-    const char* rec0 = a.R + (size_t)rt * nch * kRecBytes + 16 * lane;
+    // This wave's two activation records per chunk.
+    const char* rec0 = a.R + (size_t)rt0 * nch * kRecBytes + 16 * lane;
+    const size_t rec_step = (size_t)nch * kRecBytes;  // next row tile
 
-    auto issue = [&](int c, int stage) {
-        const uint32_t sbase = lds0 + (uint32_t)(stage * L::kStage);
+    auto issue_chunk = [&](int c, uint32_t cbase) {
         const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
 #pragma unroll
         for (int k = 0; k < L::kPerWave; ++k)
-            dma16(src0[k] + (size_t)c * step[k] + g * gstep[k], sbase + x0s[k]);
-        const char* rec = rec0 + (size_t)c * kRecBytes;
-        const uint32_t abase = sbase + (uint32_t)(L::kA + wave * kRecBytes);
-        dma16(rec, abase);
-        dma16(rec + 1024, abase + 1024);
-        dma16(rec + 1152, abase + 1152);
+            dma16(src0[k] + (size_t)c * step[k] + g * gstep[k], cbase + x0s[k]);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            const char* rec = rec0 + r * rec_step + (size_t)c * kRecBytes;
+            const uint32_t abase = cbase + (uint32_t)(L::kA + (2 * rp + r) * kRecBytes);
+            dma16(rec, abase);
+            dma16(rec + 1024, abase + 1024);
+            dma16(rec + 1152, abase + 1152);
+        }
+    };
+    auto issue_stage = [&](int g, int buf) {
+        const uint32_t sbase = lds0 + (uint32_t)(buf * L::kStage);
+#pragma unroll
+        for (int cc = 0; cc < kPfChunks; ++cc) {
+            const int c = g * kPfChunks + cc;
+            if (c < nch) issue_chunk(c, sbase + (uint32_t)(cc * L::kChunk));
+        }
     };
 
-    float acc[CT][4];
+    // The whole K loop of one column half: CTW tiles starting at WG tile toff.
+    auto run = [&](auto ctw_tag, int toff) {
+        constexpr int CTW = decltype(ctw_tag)::value;
+        // Per-column scales (SCM 0) are loaded and waited for before the
+        // first direct load, so no compiler wait inside the loop counts them.
+        float sbc[CTW];
 #pragma unroll
-    for (int ct = 0; ct < CT; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[ct][i] = 0.0f;
-
-    // One chunk (NB = 2 blocks, or 1 for the last chunk of an odd block
-    // count) from stage memory st.
-    auto compute = [&](const char* st, auto nb_tag) {
-        constexpr int NB = decltype(nb_tag)::value;
-        const char* ar = st + L::kA + wave * kRecBytes;
-        uint64_t ah[2], al[2];
-        float sa[2][4];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            const uint4 r = *reinterpret_cast<const uint4*>(ar + b * 1024 + 16 * lane);
-            ah[b] = (uint64_t)r.y << 32 | r.x;
-            al[b] = (uint64_t)r.w << 32 | r.z;
-            const float4 s4 = *reinterpret_cast<const float4*>(ar + kRecA + b * 64 + 16 * grp);
-            sa[b][0] = s4.x;
-            sa[b][1] = s4.y;
-            sa[b][2] = s4.z;
-            sa[b][3] = s4.w;
-        }
-        constexpr int G = 4;
-#pragma unroll
-        for (int g0 = 0; g0 < CT; g0 += G) {
-            uint4 bw[G];
-            int2 ws[G];
-            float sb[G][2];
-#pragma unroll
-            for (int t = 0; t < G; ++t) {
-                const int ct = g0 + t;
-                if (ct >= CT) continue;
-                bw[t] = *reinterpret_cast<const uint4*>(st + ct * 1024 + 16 * lane);
-                ws[t] = *reinterpret_cast<const int2*>(st + L::kWS + ct * 128 + 8 * col);
-                if (SCM == 2) {
-                    const float2 f = *reinterpret_cast<const float2*>(st + L::kSB + ct * 128 + 8 * col);
-                    sb[t][0] = f.x;
-                    sb[t][1] = f.y;
-                } else if (SCM == 1) {
-                    sb[t][0] = sb[t][1] = *reinterpret_cast<const float*>(st + L::kSB + ct * 64 + 4 * col);
-                } else {
-                    sb[t][0] = sb[t][1] = sbc[ct];
-                }
+        for (int ct = 0; ct < CTW; ++ct) {
+            sbc[ct] = 0.0f;
+            if (SCM == 0) {
+                sbc[ct] = reinterpret_cast<const float*>(a.S)[(size_t)min(t0 + toff + ct, a.ntiles - 1) * a.ngrp * 16 + col];
+                asm volatile("" ::"v"(sbc[ct]));
             }
+        }
+        float acc[2][CTW][4];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                v4i d[G];
+        for (int r = 0; r < 2; ++r)
 #pragma unroll
-                for (int t = 0; t < G; ++t) {
-                    if (g0 + t >= CT) continue;
-                    const uint64_t bop = b == 0 ? ((uint64_t)bw[t].y << 32 | bw[t].x)
-                                                : ((uint64_t)bw[t].w << 32 | bw[t].z);
+            for (int ct = 0; ct < CTW; ++ct)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[r][ct][i] = 0.0f;
+
+        // One chunk (NB = 2 blocks, or 1 for the last chunk of an odd block
+        // count) from LDS region cp, software-pipelined over the CTW*NB
+        // (tile, block) steps: step s issues the h-byte MFMAs of step s+2,
+        // the shift-adds and l-byte MFMAs of step s+1 and the epilogue of
+        // step s, so every step carries four MFMAs per 32 VALU instructions
+        // and no instruction waits on the one just before it.  Tile
+        // operands are read from LDS three tiles ahead; both row tiles
+        // share each weight operand.
+        auto compute = [&](const char* cp, auto nb_tag) {
+            constexpr int NB = decltype(nb_tag)::value;
+            constexpr int NS = CTW * NB;
+            const char* ar = cp + L::kA + 2 * rp * kRecBytes;
+            uint64_t ah[2][2], al[2][2];
+            float sa[2][2][4];
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const uint4 q = *reinterpret_cast<const uint4*>(ar + r * kRecBytes + b * 1024 + 16 * lane);
+                    ah[r][b] = (uint64_t)q.y << 32 | q.x;
+                    al[r][b] = (uint64_t)q.w << 32 | q.z;
+                    const float4 s4 = *reinterpret_cast<const float4*>(ar + r * kRecBytes + kRecA + b * 64 + 16 * grp);
+                    sa[r][b][0] = s4.x;
+                    sa[r][b][1] = s4.y;
+                    sa[r][b][2] = s4.z;
+                    sa[r][b][3] = s4.w;
+                }
+            uint4 bw[CTW];
+            int2 ws[CTW];
+            float sb[CTW][2];
+            auto load_tile = [&](int ct) {
+                if (ct >= CTW) return;
+                const int t = toff + ct;
+                bw[ct] = *reinterpret_cast<const uint4*>(cp + t * 1024 + 16 * lane);
+                if (HP) ws[ct] = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * col);
+                if (SCM == 2) {
+                    const float2 f = *reinterpret_cast<const float2*>(cp + L::kSB + t * 128 + 8 * col);
+                    sb[ct][0] = f.x;
+                    sb[ct][1] = f.y;
+                } else if (SCM == 1) {
+                    sb[ct][0] = sb[ct][1] = *reinterpret_cast<const float*>(cp + L::kSB + t * 64 + 4 * col);
+                } else {
+                    sb[ct][0] = sb[ct][1] = sbc[ct];
+                }
+            };
+            auto bop = [&](int s) -> uint64_t {
+                const uint4& w4 = bw[s / NB];
+                return s % NB == 0 ? ((uint64_t)w4.y << 32 | w4.x) : ((uint64_t)w4.w << 32 | w4.z);
+            };
+            v4i hh[NS][2], dd[NS][2];
+            auto step_h = [&](int s) {
+                if (!HP || s >= NS) return;
+#pragma unroll
+                for (int r = 0; r < 2; ++r) hh[s][r] = mfma16(ah[r][s % NB], bop(s));
+            };
+            auto step_d = [&](int s) {
+                if (s >= NS) return;
+                const int b = s % NB;
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
                     if (HP) {
-                        const v4i hh = mfma16(ah[b], bop);
-                        const int s128 = b == 0 ? ws[t].x : ws[t].y;
-                        const v4i ci = {(hh[0] << 8) + s128, (hh[1] << 8) + s128, (hh[2] << 8) + s128,
-                                        (hh[3] << 8) + s128};
-                        d[t] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)al[b], (long)bop, ci, 0, 0, 0);
+                        const int s128 = b == 0 ? ws[s / NB].x : ws[s / NB].y;
+                        const v4i ci = {(hh[s][r][0] << 8) + s128, (hh[s][r][1] << 8) + s128,
+                                        (hh[s][r][2] << 8) + s128, (hh[s][r][3] << 8) + s128};
+                        dd[s][r] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)al[r][b], (long)bop(s), ci, 0, 0, 0);
                     } else {
-                        d[t] = mfma16(ah[b], bop);
+                        dd[s][r] = mfma16(ah[r][b], bop(s));
                     }
                 }
+            };
+            auto step_e = [&](int s) {
+                const int ct = s / NB, b = s % NB;
 #pragma unroll
-                for (int t = 0; t < G; ++t) {
-                    const int ct = g0 + t;
-                    if (ct >= CT) continue;
+                for (int r = 0; r < 2; ++r)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        acc[ct][i] = __builtin_fmaf(sa[b][i], (float)d[t][i] * sb[t][b], acc[ct][i]);
-                }
+                        acc[r][ct][i] = __builtin_fmaf(sa[r][b][i], (float)dd[s][r][i] * sb[ct][b], acc[r][ct][i]);
+            };
+            load_tile(0);
+            load_tile(1);
+            load_tile(2);
+            step_h(0);
+            step_h(1);
+            step_d(0);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                if (s % NB == 0) load_tile(s / NB + 3);
+                step_h(s + 2);
+                step_d(s + 1);
+                step_e(s);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        // Every stage but the last holds kPfChunks full chunks, so the main
+        // loop body is straight-line and the accumulators stay in place.
+        static_assert(kPfChunks == 2, "stage loop");
+        constexpr std::integral_constant<int, 2> two{};
+        constexpr std::integral_constant<int, 1> one{};
+        issue_stage(0, 0);
+        for (int g = 0; g + 1 < nst; ++g) {
+            // Stage g's loads (issued one stage earlier) have landed; the
+            // barrier publishes them and retires stage g-1's buffer.
+            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+            lds_barrier();
+            issue_stage(g + 1, (g + 1) & 1);
+            if (active) {
+                const char* sp = pf_lds + (g & 1) * L::kStage;
+                compute(sp, two);
+                compute(sp + L::kChunk, two);
             }
         }
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        lds_barrier();
+        if (!active) return;
+        {
+            const char* sp = pf_lds + ((nst - 1) & 1) * L::kStage;
+            const int c0 = (nst - 1) * kPfChunks;
+            if (c0 + 1 < nch) {
+                compute(sp, two);
+                if (odd) compute(sp + L::kChunk, one);
+                else compute(sp + L::kChunk, two);
+            } else if (odd) {
+                compute(sp, one);
+            } else {
+                compute(sp, two);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int ct = 0; ct < CTW; ++ct) {
+                const int tile = t0 + toff + ct;
+                if (tile >= a.ntiles) continue;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int m = (rt0 + r) * 16 + 4 * grp + i;
+                    if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + col] = acc[r][ct][i];
+                }
+            }
     };
-
-#pragma unroll
-    for (int s = 0; s < kPfStages - 1; ++s)
-        if (s < nch) issue(s, s);
-    const bool odd = a.nblk & 1;
-    int st = 0;
-    for (int c = 0; c < nch; ++c) {
-        // This wave's loads of chunk c have landed once at most the loads of
-        // chunk c+1 (issued later) are outstanding.
-        if (c + 1 < nch) __builtin_amdgcn_s_waitcnt(vm_wait(L::kDma));
-        else __builtin_amdgcn_s_waitcnt(vm_wait(0));
-        lds_barrier();  // every wave's part of chunk c is in; chunk c-1 is consumed
-        if (c + kPfStages - 1 < nch) issue(c + kPfStages - 1, st == 0 ? kPfStages - 1 : st - 1);
-        if (active) {
-            const char* sp = pf_lds + st * L::kStage;
-            if (c + 1 < nch || !odd) compute(sp, std::integral_constant<int, 2>{});
-            else compute(sp, std::integral_constant<int, 1>{});
-        }
-        st = st == kPfStages - 1 ? 0 : st + 1;
-    }
-    if (!active) return;
-#pragma unroll
-    for (int ct = 0; ct < CT; ++ct) {
-        const int tile = t0 + ct;
-        if (tile >= a.ntiles) continue;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int m = rt * 16 + 4 * grp + i;
-            if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + col] = acc[ct][i];
-        }
-    }
+    if (half == 0) run(std::integral_constant<int, (CT + 1) / 2>{}, 0);
+    else run(std::integral_constant<int, CT / 2>{}, (CT + 1) / 2);
 }
 
 // Activation records for the prefill GEMM: 8 lanes per (row, block) over
