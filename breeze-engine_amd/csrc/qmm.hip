@@ -856,19 +856,23 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
     const char* rec0 = a.R + (size_t)rt0 * nch * kRecBytes + 16 * lane;
     const size_t rec_step = (size_t)nch * kRecBytes;  // next row tile
 
-    auto issue_chunk = [&](int c, uint32_t cbase) {
-        const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
-#pragma unroll
-        for (int k = 0; k < L::kPerWave; ++k)
-            dma16(src0[k] + (size_t)c * step[k] + g * gstep[k], cbase + x0s[k]);
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const char* rec = rec0 + r * rec_step + (size_t)c * kRecBytes;
-            const uint32_t abase = cbase + (uint32_t)(L::kA + (2 * rp + r) * kRecBytes);
-            dma16(rec, abase);
-            dma16(rec + 1024, abase + 1024);
-            dma16(rec + 1152, abase + 1152);
+    // Load d of this wave's kDmaChunk loads of chunk c into the chunk region
+    // at LDS address cbase: the shared slots, then 3 per activation record.
+    constexpr int kDmaChunk = L::kPerWave + 6;
+    auto dma_slot = [&](int c, uint32_t cbase, int d) {
+        if (d < L::kPerWave) {
+            const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
+            dma16(src0[d] + (size_t)c * step[d] + g * gstep[d], cbase + x0s[d]);
+        } else {
+            const int e = d - L::kPerWave, r = e / 3, part = e % 3;
+            const int off = part == 0 ? 0 : part == 1 ? 1024 : 1152;
+            dma16(rec0 + r * rec_step + (size_t)c * kRecBytes + off,
+                  cbase + (uint32_t)(L::kA + (2 * rp + r) * kRecBytes + off));
         }
+    };
+    auto issue_chunk = [&](int c, uint32_t cbase) {
+#pragma unroll
+        for (int d = 0; d < kDmaChunk; ++d) dma_slot(c, cbase, d);
     };
     auto issue_stage = [&](int g, int buf) {
         const uint32_t sbase = lds0 + (uint32_t)(buf * L::kStage);
@@ -907,10 +911,14 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
         // the shift-adds and l-byte MFMAs of step s+1 and the epilogue of
         // step s, so every step carries four MFMAs per 32 VALU instructions
         // and no instruction waits on the one just before it.  Tile
-        // operands are read from LDS three tiles ahead; both row tiles
-        // share each weight operand.
-        auto compute = [&](const char* cp, auto nb_tag) {
+        // operands are read from LDS kAhead tiles ahead; both row tiles
+        // share each weight operand.  With DMA, every other step also
+        // issues one of this wave's loads of chunk c_next into nbase, so
+        // the next stage streams in without a burst of loads.
+        auto compute = [&](const char* cp, auto nb_tag, auto dma_tag, int c_next, uint32_t nbase) {
             constexpr int NB = decltype(nb_tag)::value;
+            constexpr bool DMA = decltype(dma_tag)::value;
+            constexpr int kAhead = 5;
             constexpr int NS = CTW * NB;
             const char* ar = cp + L::kA + 2 * rp * kRecBytes;
             uint64_t ah[2][2], al[2][2];
@@ -979,19 +987,23 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
                     for (int i = 0; i < 4; ++i)
                         acc[r][ct][i] = __builtin_fmaf(sa[r][b][i], (float)dd[s][r][i] * sb[ct][b], acc[r][ct][i]);
             };
-            load_tile(0);
-            load_tile(1);
-            load_tile(2);
+#pragma unroll
+            for (int t = 0; t < kAhead; ++t) load_tile(t);
             step_h(0);
             step_h(1);
             step_d(0);
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                if (s % NB == 0) load_tile(s / NB + 3);
+                if (s % NB == 0) load_tile(s / NB + kAhead);
+                if (DMA && s % 2 == 0 && s / 2 < kDmaChunk) dma_slot(c_next, nbase, s / 2);
                 step_h(s + 2);
                 step_d(s + 1);
                 step_e(s);
                 __builtin_amdgcn_sched_barrier(0);
+            }
+            if (DMA) {
+#pragma unroll
+                for (int d = (NS + 1) / 2; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d);
             }
         };
 
@@ -1000,17 +1012,24 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
         static_assert(kPfChunks == 2, "stage loop");
         constexpr std::integral_constant<int, 2> two{};
         constexpr std::integral_constant<int, 1> one{};
+        constexpr std::true_type dma{};
+        constexpr std::false_type no_dma{};
         issue_stage(0, 0);
         for (int g = 0; g + 1 < nst; ++g) {
-            // Stage g's loads (issued one stage earlier) have landed; the
-            // barrier publishes them and retires stage g-1's buffer.
+            // Stage g's loads (issued during stage g-1) have landed; the
+            // barrier publishes them and retires stage g-1's buffer, which
+            // stage g+1's loads then fill.  A missing last chunk of stage
+            // g+1 reloads chunk nch-1 into a region that is never read.
             __builtin_amdgcn_s_waitcnt(vm_wait(0));
             lds_barrier();
-            issue_stage(g + 1, (g + 1) & 1);
+            const uint32_t nbase = lds0 + (uint32_t)(((g + 1) & 1) * L::kStage);
+            const int cn = (g + 1) * kPfChunks;
             if (active) {
                 const char* sp = pf_lds + (g & 1) * L::kStage;
-                compute(sp, two);
-                compute(sp + L::kChunk, two);
+                compute(sp, two, dma, cn, nbase);
+                compute(sp + L::kChunk, two, dma, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk);
+            } else {
+                issue_stage(g + 1, (g + 1) & 1);
             }
         }
         __builtin_amdgcn_s_waitcnt(vm_wait(0));
@@ -1020,13 +1039,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
             const char* sp = pf_lds + ((nst - 1) & 1) * L::kStage;
             const int c0 = (nst - 1) * kPfChunks;
             if (c0 + 1 < nch) {
-                compute(sp, two);
-                if (odd) compute(sp + L::kChunk, one);
-                else compute(sp + L::kChunk, two);
+                compute(sp, two, no_dma, 0, 0u);
+                if (odd) compute(sp + L::kChunk, one, no_dma, 0, 0u);
+                else compute(sp + L::kChunk, two, no_dma, 0, 0u);
             } else if (odd) {
-                compute(sp, one);
+                compute(sp, one, no_dma, 0, 0u);
             } else {
-                compute(sp, two);
+                compute(sp, two, no_dma, 0, 0u);
             }
         }
 #pragma unroll
