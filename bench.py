@@ -16,7 +16,10 @@ of breeze-engine, compiled from its own source into oracle/_ref) on this
 host's cores for the same workload; without it, the oracle's scalar C port.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
-                       [--no-cpu-baseline]
+                       [--no-cpu-baseline] [--workload NAME[:ROWS]]
+
+--workload times one workload alone and prints its own JSON line (for
+profiling one kernel); the default run prints the contract line above.
 """
 import argparse
 import json
@@ -141,6 +144,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", default=None,
+                    help="time only this workload (w8_gemv, w4_gemv, w4_decode:ROWS, w8_lmhead, w8_prefill)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 elementwise copy 5 times (counter calibration)")
     args = ap.parse_args()
@@ -169,6 +174,22 @@ def main():
     if not hb.device_available():
         raise SystemExit(f"bench.py: gfx950 path unavailable: {hb.last_error()}")
     hb.set_hi_prec(True)
+
+    if args.workload:
+        name, _, r = args.workload.partition(":")
+        if name not in workloads.LABELS:
+            raise SystemExit(f"bench.py: unknown workload {name!r}; one of {sorted(workloads.LABELS)}")
+        rows = int(r) if r else None
+        t, m = time_workload(hb, torch, name, rows, args.steps, args.warmup, argmax=name == "w8_lmhead")
+        entry = {"workload": workloads.LABELS[name].format(M=m), "steps": args.steps, "us": round(t * 1e6, 3)}
+        if name == "w8_prefill":
+            tops = workloads.algorithmic_ops(name, m) / t / 1e12
+            entry.update(tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
+        else:
+            g = workloads.algorithmic_bytes(name, m) / t / 1e9
+            entry.update(gbs=round(g, 1), frac_hbm_peak=round(g / HBM_PEAK_GBS, 4))
+        print(json.dumps(entry), flush=True)
+        return
 
     t_step, M = time_workload(hb, torch, HEADLINE, None, args.steps, args.warmup)
     nbytes = workloads.algorithmic_bytes(HEADLINE)
