@@ -341,7 +341,9 @@ struct GemvArgs {
     const int* Sq;         // [M][nblk4]
     float* C;              // [M][N]
     int32_t* Cs;           // [M][N][nblk] (block-dot export)
-    unsigned long long* part;  // [NG][M] argmax partials, or NULL
+    int64_t* idx;              // [M] argmax, or NULL
+    unsigned int* ticket;      // with idx: workgroups done (0 between calls)
+    unsigned long long* key;   // with idx: [8] merged argmax keys (0 between calls)
     int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
     int ntiles, NG, RG, pair_xcd;
     int lds_recs, lds_sa, lds_sq, lds_consts, lds_fbuf;
@@ -577,7 +579,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
                 if (grp < Mr) {
                     const int n = (t_begin + pr_t) * 16 + col;
                     a.C[(size_t)(m0 + grp) * a.N + n] = acc;
-                    if (a.part) {
+                    if (a.idx) {
                         const unsigned long long k = argmax_key(acc, n);
                         best = k > best ? k : best;
                     }
@@ -587,14 +589,30 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
                 ++pr_t;
             }
         }
-        if (a.part) {
+        if (a.idx) {
             // Row maximum over the lanes of each row (lanes 16r..16r+15).
 #pragma unroll
             for (int s = 1; s < 16; s <<= 1) {
                 const unsigned long long o = __shfl_xor(best, s, 16);
                 best = o > best ? o : best;
             }
-            if (col == 0 && grp < Mr) a.part[(size_t)g * a.M + m0 + grp] = best;
+            {
+                // Argmax without a second launch: each workgroup merges its
+                // row keys into idx_key with device-scope atomic max, waits
+                // for them, then takes a ticket; the workgroup holding the
+                // last ticket swaps the merged keys back to zero (re-arming
+                // them for the next call) and writes the indices.
+                if (col == 0 && grp < Mr) (void)atomicMax(a.key + m0 + grp, best);
+                __builtin_amdgcn_s_waitcnt(0);
+                unsigned int t = 0;
+                if (lane == 0) t = atomicAdd(a.ticket, 1u);
+                t = __shfl(t, 0);
+                if (t == gridDim.x - 1 && lane < a.M) {
+                    const unsigned long long k = atomicExch(a.key + lane, 0ull);
+                    a.idx[lane] = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+                    if (lane == 0) atomicExch(a.ticket, 0u);
+                }
+            }
         }
         return;
     }
@@ -1163,6 +1181,7 @@ struct Workspace {
     int* sq = nullptr;
     size_t rows_cap = 0, nblk4_cap = 0;
     unsigned long long* parts = nullptr;
+    unsigned int* ticket = nullptr;  // decode argmax: ticket counter, then 8 row keys; zero between calls
     size_t parts_cap = 0;
     uint8_t* rec = nullptr;  // prefill activation records
     size_t rec_cap = 0;
@@ -1570,7 +1589,6 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     }
 
     hipError_t e;
-    int nparts = 0;
     if (dec) {
         const int n_cu = device_cus(w, dev);
         a.RG = (M + 3) / 4;
@@ -1584,9 +1602,19 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
         }
         const int units = (a.ntiles + a.NG - 1) / a.NG * ((a.nbg + kProducers - 1) / kProducers);
         if (dIdx) {
-            if (!grow(&w.parts, &w.parts_cap, (size_t)a.NG * M, "argmax workspace")) return -4;
-            a.part = w.parts;
-            nparts = a.NG;
+            if (!w.ticket) {
+                // Allocated and zeroed once per device (not under graph capture);
+                // the kernel's last workgroup re-arms it to zero.
+                if (!hip_ok(hipMalloc(&w.ticket, 9 * sizeof(unsigned long long)), "argmax workspace")) return -4;
+                if (!hip_ok(hipMemset(w.ticket, 0, 9 * sizeof(unsigned long long)), "argmax workspace")) {
+                    (void)hipFree(w.ticket);
+                    w.ticket = nullptr;
+                    return -4;
+                }
+            }
+            a.ticket = w.ticket;
+            a.key = reinterpret_cast<unsigned long long*>(w.ticket) + 1;
+            a.idx = dIdx;
         }
         const int grid = a.NG * a.RG;
         const bool x = h->extra;
@@ -1622,12 +1650,11 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     }
     if (!hip_ok(e, "matmul launch")) return -5;
 
-    if (dIdx && !dots) {
-        if (!dec) {
-            nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
-            if (!grow(&w.parts, &w.parts_cap, (size_t)M * nparts, "argmax workspace")) return -4;
-            argmax_partial_kernel<<<dim3(nparts, M), 256, 0, st>>>(dC, h->N, w.parts);
-        }
+    if (dIdx && !dots && !dec) {
+        // The decode kernel merges its own argmax (last workgroup).
+        const int nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
+        if (!grow(&w.parts, &w.parts_cap, (size_t)M * nparts, "argmax workspace")) return -4;
+        argmax_partial_kernel<<<dim3(nparts, M), 256, 0, st>>>(dC, h->N, w.parts);
         argmax_final_kernel<<<M, 256, 0, st>>>(w.parts, nparts, M, dIdx);
         if (!hip_ok(hipGetLastError(), "argmax launch")) return -5;
     }

@@ -217,3 +217,35 @@ def test_prefill_gemm_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
                 assert bits_equal(got.cpu().numpy(), want), (hp, rows)
     finally:
         hb.free(h)
+
+
+def test_matmulnbits_operator_routes_to_the_gpu(gpu, hb, orc, hi_prec):
+    """breeze_amd.ops with the real backend: the session cache prepacks an
+    INT4 node with explicit zeros and an INT8 node, and the operator body
+    matches the oracle for a 3-D NumPy activation and a GPU tensor."""
+    import types
+
+    from breeze_amd import ops
+
+    rng = np.random.default_rng(12)
+    qw4, sc4, qz4 = rng_weights(rng, 64, 256, 4, np.float16, True)
+    qw8, sc8, _ = rng_weights(rng, 32, 320, 8)
+    inits = {"w4": qw4, "s4": sc4, "z4": qz4, "w8": qw8, "s8": sc8}
+    nodes = [types.SimpleNamespace(name="p4", op_type="MatMulNBits", inputs=["x", "w4", "s4", "z4"],
+                                   attrs=dict(K=256, N=64, bits=4, block_size=32)),
+             types.SimpleNamespace(name="p8", op_type="MatMulNBits", inputs=["x", "w8", "s8"],
+                                   attrs=dict(K=320, N=32, bits=8, block_size=32))]
+    cache = ops.prepack_nodes(nodes, inits)
+    try:
+        hb.set_hi_prec(True)
+        a4 = rng.normal(size=(2, 5, 256)).astype(np.float32)
+        out4 = ops.matmul_nbits(cache, "p4", a4)
+        assert out4.shape == (2, 5, 64)
+        assert bits_equal(out4.reshape(10, 64), orc.matmul(qw4, sc4, qz4, 64, 256, 4, a4.reshape(10, 256), True))
+        a8 = rng.normal(size=(3, 320)).astype(np.float32)
+        out8 = ops.matmul_nbits(cache, "p8", gpu.from_numpy(a8[None]).cuda())
+        gpu.cuda.synchronize()
+        assert tuple(out8.shape) == (1, 3, 32)
+        assert bits_equal(out8[0].cpu().numpy(), orc.matmul(qw8, sc8, None, 32, 320, 8, a8, True))
+    finally:
+        ops.free_cache(cache)
