@@ -34,6 +34,9 @@ FLAGS = [
     # MFMA results in ordinary VGPRs: the epilogues read every MFMA result
     # with VALU instructions, and the AGPR form adds a copy for each.
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # Leading scalar kernel arguments arrive in SGPRs at wave launch, so a
+    # kernel's first loads do not wait for a kernarg fetch.
+    "-mllvm", "-amdgpu-kernarg-preload-count=14",
     "-Wall",
 ]
 

@@ -346,7 +346,6 @@ struct GemvArgs {
     unsigned long long* key;   // with idx: [8] merged argmax keys (0 between calls)
     int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
     int ntiles, NG, RG, pair_xcd;
-    int lds_recs, lds_sa, lds_sq, lds_consts, lds_fbuf;
 };
 
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
@@ -384,8 +383,66 @@ __device__ inline void lds_barrier() {
 // padding that keeps the JG-wide stores and reads free of bank conflicts.
 __host__ __device__ constexpr int dec_pitch(int JG) { return kProducers * JG + (JG == 4 ? 8 : 4); }
 
+// LDS layout of the decode kernel for Mr_max activation rows per workgroup.
+// The host sizes the launch with it and the kernel rebuilds it from its
+// preloaded arguments.  With more than one row the row pitches are padded
+// so the rows read by one lane group fall on different banks: records 64 B
+// past a multiple of 256 B, block scales and sums 16 B past one.
+struct DecLds {
+    int rec_pitch;  // bytes per activation row of records
+    int sa_pitch;   // elements per row of block scales / sums
+    int recs, sa, sq, consts, fbuf, total;  // byte offsets, bytes used
+};
+
+__host__ __device__ inline int lds_take(int& off, int bytes) {
+    const int o = off;
+    off += (bytes + 15) / 16 * 16;
+    return o;
+}
+
+__host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG) {
+    DecLds l;
+    l.rec_pitch = nblk * 64;
+    l.sa_pitch = (nblk + 3) / 4 * 4;
+    if (Mr_max > 1) {
+        l.rec_pitch = (l.rec_pitch + 191) / 256 * 256 + 64;
+        l.sa_pitch = (l.sa_pitch + 59) / 64 * 64 + 4;
+    }
+    int off = 0;
+    l.recs = lds_take(off, Mr_max * l.rec_pitch);
+    l.sa = lds_take(off, Mr_max * l.sa_pitch * 4);
+    l.sq = lds_take(off, Mr_max * l.sa_pitch * 4);
+    l.consts = lds_take(off, 512);
+    l.fbuf = lds_take(off, 2 * 64 * dec_pitch(JG) * 4);
+    l.total = off;
+    return l;
+}
+
+// The leading scalar arguments are what the first activation and weight
+// loads need.  They are preloaded into SGPRs at wave launch (kernarg
+// preload, 14 SGPRs), so those loads do not wait for a kernarg fetch; the
+// rest of the arguments come from the struct as the code reaches them.
+// misc = sc_shift | RG << 8 | pair_xcd << 10.
 template <int BITS, bool HP, bool FUSED, bool EXTRA, int R>
-__global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
+__global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
+                                                             int pK, int pnblk, int pM, int pnbg, int pntiles,
+                                                             int pNG, int pngrp, int misc, GemvArgs args) {
+    GemvArgs a = args;
+    if (FUSED) a.A = static_cast<const float*>(act);
+    else a.Aq = static_cast<const uint8_t*>(act);
+    a.W = pW;
+    a.S = pS;
+    a.K = pK;
+    a.nblk = pnblk;
+    a.M = pM;
+    a.nbg = pnbg;
+    a.ntiles = pntiles;
+    a.NG = pNG;
+    a.ngrp = pngrp;
+    a.nblk4 = (pnblk + 3) / 4 * 4;
+    a.sc_shift = misc & 31;
+    a.RG = (misc >> 8) & 3;
+    a.pair_xcd = (misc >> 10) & 1;
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int PP = dec_pitch(JG);
     typedef float fvec __attribute__((ext_vector_type(JG)));
@@ -415,10 +472,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
     const int npw = (nbg + kProducers - 1) / kProducers;  // phases per tile
     const int U = nT * npw;                                // phases of this workgroup
 
-    uint8_t* recs = smem + a.lds_recs;
-    float* sa_l = reinterpret_cast<float*>(smem + a.lds_sa);
-    int* sq_l = reinterpret_cast<int*>(smem + a.lds_sq);
-    float* fbuf = reinterpret_cast<float*>(smem + a.lds_fbuf);  // [2][64][PP]
+    const DecLds lay = dec_lds(min(a.M, 4), a.nblk, JG);
+    uint8_t* recs = smem + lay.recs;
+    float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
+    int* sq_l = reinterpret_cast<int*>(smem + lay.sq);
+    float* fbuf = reinterpret_cast<float*>(smem + lay.fbuf);  // [2][64][PP]
 
     const int col = lane & 15, grp = lane >> 4;
     const int me = min(grp, Mr - 1);
@@ -505,32 +563,41 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
                            s, sum, p0, p1);
                 if (blk < nb_rows) {
                     const int m = blk / a.nblk, j = blk - m * a.nblk;
-                    uint8_t* rec = recs + ((size_t)m * a.nblk + j) * 64;
+                    uint8_t* rec = recs + m * lay.rec_pitch + j * 64;
                     *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
                     *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
                     if (e == 0) {
-                        sa_l[m * a.nblk4 + j] = s;
-                        sq_l[m * a.nblk4 + j] = sum;
+                        sa_l[m * lay.sa_pitch + j] = s;
+                        sq_l[m * lay.sa_pitch + j] = sum;
                     }
                 }
             }
         } else {
             // Unconditional stores: threads past the end rewrite the last
-            // element with the value they loaded from it.
+            // element with the value they loaded from it.  Rows land at the
+            // padded LDS pitches.
             uint4* dst = reinterpret_cast<uint4*>(recs);
             const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
-            dst[min(tid, nrec - 1)] = r0;
-            dst[min(1024 + tid, nrec - 1)] = r1;
-            dst[min(2048 + tid, nrec - 1)] = r2;
-            dst[min(3072 + tid, nrec - 1)] = r3;
-            dst[min(4096 + tid, nrec - 1)] = r4;
-            dst[min(5120 + tid, nrec - 1)] = r5;
+            const int L = a.nblk * 4, gap = (lay.rec_pitch >> 4) - L;
+            auto put = [&](int i, const uint4& v) {
+                i = min(i, nrec - 1);
+                const int m = (i >= L) + (i >= 2 * L) + (i >= 3 * L);
+                dst[i + m * gap] = v;
+            };
+            put(tid, r0);
+            put(1024 + tid, r1);
+            put(2048 + tid, r2);
+            put(3072 + tid, r3);
+            put(4096 + tid, r4);
+            put(5120 + tid, r5);
             const int mi = min(tid, nmeta - 1);
-            reinterpret_cast<uint4*>(sa_l)[mi] = rsa;
-            reinterpret_cast<uint4*>(sq_l)[mi] = rsq;
+            const int mm = (mi * 4) / a.nblk4;
+            const int md = mi + mm * ((lay.sa_pitch - a.nblk4) >> 2);
+            reinterpret_cast<uint4*>(sa_l)[md] = rsa;
+            reinterpret_cast<uint4*>(sq_l)[md] = rsq;
         }
         {
-            uint32_t* cst = reinterpret_cast<uint32_t*>(smem + a.lds_consts);
+            uint32_t* cst = reinterpret_cast<uint32_t*>(smem + lay.consts);
             if (tid < 128) cst[tid] = tid < 64 ? 0x01010101u : 0u;  // [0,256) ones, [256,512) zeros
         }
     };
@@ -541,7 +608,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
         store_acts();
         lds_barrier();
         // Lane (row me, column col) of the current tile.
-        const float* sa_row = sa_l + me * a.nblk4;
+        const float* sa_row = sa_l + me * lay.sa_pitch;
         const bool tail_pad = a.nblk != nbg * JG;  // the last chunk has padding blocks
         float acc = 0.0f;
         unsigned long long best = 0;
@@ -631,8 +698,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
     // k-octet kq.  Output lane (col, grp) holds row grp.
     const int arow = lane & 15, arg = arow >> 2, ars = arow & 3, kq = lane >> 4;
     const bool is_data = ars < 2 && arg < Mr;
-    const int data_base = a.lds_recs + arg * a.nblk * 64 + ars * 32 + kq * 8;
-    const int const_base = a.lds_consts + ((ars == 2 && arg < Mr) ? 0 : 256) + kq * 8;
+    const int data_base = lay.recs + arg * lay.rec_pitch + ars * 32 + kq * 8;
+    const int const_base = lay.consts + ((ars == 2 && arg < Mr) ? 0 : 256) + kq * 8;
 
     int pr_p = 0;  // phase of the unit being processed
     for (int u0 = 0; u0 < U; u0 += R) {
@@ -645,7 +712,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(GemvArgs a) {
                 const Unit<JG, EXTRA>& cur = ring[d];
                 const int abase = is_data ? data_base + c * JG * 64 : const_base;
                 int4 sqv = make_int4(0, 0, 0, 0);
-                if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * a.nblk4 + c * 4);
+                if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * lay.sa_pitch + c * 4);
                 fvec fo;
 #pragma unroll
                 for (int jb = 0; jb < JG; ++jb) {
@@ -1416,23 +1483,13 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 constexpr int kLdsMax = 160 * 1024;
 constexpr int kFusedMaxBlocks = 512;  // row-blocks the prologue quantizes (4 passes of 128)
 
-// LDS plan of the decode kernel; returns the bytes used, or 0 if the
-// activation records of a row group do not fit (in LDS, or in the
-// prologue's 6-uint4-per-thread record copy).
-int plan_dec_lds(GemvArgs& a, int Mr_max, int JG) {
+// LDS bytes of the decode kernel, or 0 if the activation records of a row
+// group do not fit (in LDS, or in the prologue's 6-uint4-per-thread record
+// copy).
+int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG) {
     if (Mr_max * a.nblk > kFusedMaxBlocks && Mr_max * a.nblk * 4 > 6 * kDecWaves * 64) return 0;
-    int off = 0;
-    auto take = [&](int bytes) {
-        const int o = off;
-        off += (bytes + 15) / 16 * 16;
-        return o;
-    };
-    a.lds_recs = take(Mr_max * a.nblk * 64);
-    a.lds_sa = take(Mr_max * a.nblk4 * 4);
-    a.lds_sq = take(Mr_max * a.nblk4 * 4);
-    a.lds_consts = take(512);
-    a.lds_fbuf = take(2 * 64 * dec_pitch(JG) * 4);
-    return off <= kLdsMax ? off : 0;
+    const int total = dec_lds(Mr_max, a.nblk, JG).total;
+    return total <= kLdsMax ? total : 0;
 }
 
 template <int BITS, bool HP, bool FUSED, bool EXTRA, int R>
@@ -1445,7 +1502,9 @@ hipError_t launch_dec_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipS
         if (e != hipSuccess) return e;
         w.attr_set[key] = true;
     }
-    kern<<<grid, kDecWaves * 64, lds, st>>>(a);
+    const void* act = FUSED ? static_cast<const void*>(a.A) : static_cast<const void*>(a.Aq);
+    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 10;
+    kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, a.K, a.nblk, a.M, a.nbg, a.ntiles, a.NG, a.ngrp, misc, a);
     return hipGetLastError();
 }
 
