@@ -568,7 +568,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
                     if (e == 0) {
                         sa_l[m * lay.sa_pitch + j] = s;
-                        sq_l[m * lay.sa_pitch + j] = sum;
+                        sq_l[m * lay.sa_pitch + j] = (EXTRA ? -1 : -8) * sum;
                     }
                 }
             }
@@ -594,11 +594,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             const int mm = (mi * 4) / a.nblk4;
             const int md = mi + mm * ((lay.sa_pitch - a.nblk4) >> 2);
             reinterpret_cast<uint4*>(sa_l)[md] = rsa;
-            reinterpret_cast<uint4*>(sq_l)[md] = rsq;
+            const uint32_t f = EXTRA ? 0xFFFFFFFFu : 0xFFFFFFF8u;  // -1 or -8
+            reinterpret_cast<uint4*>(sq_l)[md] = make_uint4(f * rsq.x, f * rsq.y, f * rsq.z, f * rsq.w);
         }
         {
             uint32_t* cst = reinterpret_cast<uint32_t*>(smem + lay.consts);
-            if (tid < 128) cst[tid] = tid < 64 ? 0x01010101u : 0u;  // [0,256) ones, [256,512) zeros
+            if (tid < 128) cst[tid] = tid < 64 ? 0x40404040u : 0u;  // [0,256) bytes of 64, [256,512) zeros
         }
     };
 
@@ -694,12 +695,15 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     store_acts();
     lds_barrier();
 
-    // A operand: lane row arow = 4 * group + slot (slots h, l, ones, zero),
-    // k-octet kq.  Output lane (col, grp) holds row grp.
+    // A operand: lane row arow = 4 * group + slot, k-octet kq.  Slots 0 and
+    // 1 are the h and l bytes; slots 2 and 3 are rows of 64, so their two
+    // results add up to the 128 * sum(b) term.  Output lane (col, grp) holds
+    // row grp.  The LDS sums of q hold the zero-point term's factor: -sum(q)
+    // for explicit zero points, -8 * sum(q) for the default zero point 8.
     const int arow = lane & 15, arg = arow >> 2, ars = arow & 3, kq = lane >> 4;
     const bool is_data = ars < 2 && arg < Mr;
     const int data_base = lay.recs + arg * lay.rec_pitch + ars * 32 + kq * 8;
-    const int const_base = lay.consts + ((ars == 2 && arg < Mr) ? 0 : 256) + kq * 8;
+    const int const_base = lay.consts + ((ars >= 2 && arg < Mr) ? 0 : 256) + kq * 8;
 
     int pr_p = 0;  // phase of the unit being processed
     for (int u0 = 0; u0 < U; u0 += R) {
@@ -721,11 +725,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     const uint64_t bop = unpack_b(cur.w, jb, BITS);
                     const uint64_t aop = *reinterpret_cast<const uint64_t*>(smem + abase + jb * 64);
                     const v4i dd = mfma16(aop, bop);
-                    int cs = HP ? dd[0] * 256 + dd[1] + dd[2] * 128 : dd[0];
+                    int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
                     if (BITS == 4) {
-                        const int zp = EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) : 8;
-                        const int sq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
-                        cs -= zp * sq;
+                        const int nsq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
+                        cs += EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) * nsq : nsq;
                     }
                     if (EXTRA) cs += (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
                     fo[jb] = (float)cs * cur.sc[EXTRA ? jb : 0];

@@ -83,6 +83,30 @@ def test_projection_widths(gpu, hb, orc, hi_prec, K, N, bits):
     assert bits_equal(got, orc.matmul(qw, scales, None, N, K, bits, a, True))
 
 
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
+def test_decode_with_staged_activation_records(gpu, hb, orc, hi_prec, bits, explicit_zeros):
+    """Decode shapes whose activation records come from the stand-alone
+    quantizer (more than 512 row-blocks per row group: K = 4608 with 4 or
+    more rows; K = 17408 with one row), beside a shape quantized inside the
+    decode kernel (2 rows), in both activation modes, bit-exact."""
+    rng = np.random.default_rng(11 + bits)
+    for K, rows_list in ((4608, (2, 4, 5, 8)), (17408, (1,))):
+        N = 64
+        qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
+        h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+        try:
+            for hp in (False, True):
+                hb.set_hi_prec(hp)
+                for rows in rows_list:
+                    A = rng.normal(size=(rows, K)).astype(np.float32)
+                    want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
+                    c_host, c_dev = _run_both(hb, gpu, h, A, N)
+                    assert bits_equal(c_host, want), (K, hp, rows)
+                    assert bits_equal(c_dev, want), (K, hp, rows)
+        finally:
+            hb.free(h)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_legacy_layout_entry_point(gpu, hb, orc, hi_prec, bits):
     """i4_prepack of the NumPy-built legacy layout == i4_prepack_onnx."""
