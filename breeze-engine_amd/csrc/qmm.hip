@@ -605,6 +605,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
 
     if (wave == kChainWave) {
         // ================= chain wave
+        // Its fold is one dependent FMA chain per output and paces the
+        // phases: first pick of the SIMD's issue slots over the producers.
+        __builtin_amdgcn_s_setprio(3);
         load_acts();
         store_acts();
         lds_barrier();
