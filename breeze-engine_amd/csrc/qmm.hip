@@ -357,6 +357,7 @@ struct Unit {
     float sc[EXTRA ? JG : 1];
     int dl[EXTRA ? JG : 1];
     uint32_t zp;  // INT4 zero points, one byte per block
+    int c;        // chunk to compute; nbg or more: none (past the end)
 };
 
 __device__ inline unsigned long long argmax_key(float v, int idx) {
@@ -481,17 +482,22 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int col = lane & 15, grp = lane >> 4;
     const int me = min(grp, Mr - 1);
 
-    // Load cursor: unit (ld_t, ld_p) is chunk wave + 15 * ld_p of local tile
-    // ld_t (clamped to the tile's last chunk).  Units past the end read one
-    // line at the start of each array.
-    int ld_t = 0, ld_p = 0;
+    // Load cursor, kept incrementally: one scalar unit serves the CU's
+    // sixteen waves, which reach their scalar work together after each
+    // barrier, so every scalar instruction per unit lengthens every phase.
+    // The next unit is chunk ld_c (clamped to the tile's last chunk) of local
+    // tile ld_t, ld_rem units before the tile ends; ld_w, ld_s and ld_m index
+    // the tile's weights, scales and per-block metadata.  Past the end ld_c
+    // is out of range (no work) and the loads re-read the last tile.
+    int ld_c = wave, ld_rem = npw, ld_t = 0;
+    uint32_t ld_w = (uint32_t)t_begin * nbg * 64;
+    uint32_t ld_s = (uint32_t)t_begin * a.ngrp * 16;
+    uint32_t ld_m = (uint32_t)t_begin * nbg * 16;
     auto load_unit = [&](Unit<JG, EXTRA>& p) {
-        const int c = min(wave + kProducers * ld_p, nbg - 1);
-        const int tc = (t_begin + ld_t) * nbg + c;  // chunk index in the tile-major arrays
-        uint32_t wi = (uint32_t)tc * 64 + lane;     // weight uint4 index
-        uint32_t mi = (uint32_t)tc * 16 + col;      // per-block metadata index (EXTRA)
-        uint32_t si = (uint32_t)((t_begin + ld_t) * a.ngrp + ((c * JG) >> a.sc_shift)) * 16 + col;
-        if (ld_t >= nT) wi = mi = si = 0;
+        const int c = min(ld_c, nbg - 1);
+        uint32_t wi = ld_w + c * 64 + lane;                                // weight uint4 index
+        uint32_t mi = ld_m + c * 16 + col;                                 // per-block metadata (EXTRA)
+        uint32_t si = ld_s + (uint32_t)((c * JG) >> a.sc_shift) * 16 + col;  // scale index
         // Opaque to the optimizer, so the loads are not split into
         // uniform-address copies on branches of their own.
         asm("" : "+v"(wi), "+v"(mi), "+v"(si));
@@ -508,9 +514,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         } else {
             p.sc[0] = a.S[si];
         }
-        if (++ld_p == npw) {
-            ld_p = 0;
-            ++ld_t;
+        p.c = ld_c;
+        ld_c += kProducers;
+        if (--ld_rem == 0) {
+            ld_rem = npw;
+            if (++ld_t < nT) {
+                ld_c = wave;
+                ld_w += nbg * 64;
+                ld_s += a.ngrp * 16;
+                ld_m += nbg * 16;
+            } else {
+                ld_c = 1 << 24;
+            }
         }
     };
 
@@ -708,14 +723,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int data_base = lay.recs + arg * lay.rec_pitch + ars * 32 + kq * 8;
     const int const_base = lay.consts + ((ars >= 2 && arg < Mr) ? 0 : 256) + kq * 8;
 
-    int pr_p = 0;  // phase of the unit being processed
     for (int u0 = 0; u0 < U; u0 += R) {
 #pragma unroll
         for (int d = 0; d < R; ++d) {
             const bool live = u0 + d < U;  // uniform over the workgroup
-            const int c = wave + kProducers * pr_p;
+            const int c = ring[d].c;
             const int buf = (u0 + d) & 1;
-            if (live && c < nbg) {
+            if (c < nbg) {
                 const Unit<JG, EXTRA>& cur = ring[d];
                 const int abase = is_data ? data_base + c * JG * 64 : const_base;
                 int4 sqv = make_int4(0, 0, 0, 0);
@@ -741,7 +755,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             load_unit(ring[d]);
             __builtin_amdgcn_sched_barrier(0);
             if (live) lds_barrier();
-            if (++pr_p == npw) pr_p = 0;
         }
     }
 }

@@ -107,6 +107,32 @@ def test_decode_with_staged_activation_records(gpu, hb, orc, hi_prec, bits, expl
             hb.free(h)
 
 
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
+@pytest.mark.parametrize("K", [224, 672, 2080])
+def test_single_row_decode_several_tiles_per_workgroup(gpu, hb, orc, hi_prec, bits, explicit_zeros, K):
+    """One activation row with 4 or 5 tiles per decode workgroup
+    (N = 16 * 1029, uneven split), K with short last phases and padded last
+    chunks.  Outputs bit-exact, argmax first-max across workgroups."""
+    rng = np.random.default_rng(K + bits)
+    N = 16 * 1029
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        for hp in (False, True):
+            hb.set_hi_prec(hp)
+            A = rng.normal(size=(1, K)).astype(np.float32)
+            want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
+            c_host, c_dev = _run_both(hb, gpu, h, A, N)
+            assert bits_equal(c_host, want), (K, hp)
+            assert bits_equal(c_dev, want), (K, hp)
+            c_arg, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+            gpu.cuda.synchronize()
+            assert bits_equal(c_arg.cpu().numpy(), want), (K, hp)
+            assert idx.cpu().tolist() == np.argmax(want, axis=1).tolist(), (K, hp)
+    finally:
+        hb.free(h)
+
+
 @pytest.mark.parametrize("bits", [4, 8])
 def test_legacy_layout_entry_point(gpu, hb, orc, hi_prec, bits):
     """i4_prepack of the NumPy-built legacy layout == i4_prepack_onnx."""
