@@ -237,11 +237,15 @@ def main():
 
     if not args.headline_only:
         rows = []
-        steps2 = max(10, args.steps // 4)
+        # The decode workloads take about 10 us a call: same steps and warmup
+        # as the headline.  The LM head and the prefill GEMM take 140-250 us:
+        # fewer steps keep the run short.
         for name, r in (("w8_gemv", None), ("w4_gemv", None), ("w4_decode", 1), ("w4_decode", 2),
                         ("w4_decode", 4), ("w4_decode", 8), ("w8_lmhead", None), ("w8_prefill", None)):
-            t, m = time_workload(hb, torch, name, r, steps2 if name != "w8_lmhead" else 20,
-                                 max(3, args.warmup // 4), argmax=name == "w8_lmhead")
+            long_call = name in ("w8_lmhead", "w8_prefill")
+            t, m = time_workload(hb, torch, name, r, max(10, args.steps // 4) if long_call else args.steps,
+                                 max(3, args.warmup // 4) if long_call else args.warmup,
+                                 argmax=name == "w8_lmhead")
             entry = {"workload": workloads.LABELS[name].format(M=m), "us": round(t * 1e6, 2)}
             if name == "w8_prefill":
                 tops = workloads.algorithmic_ops(name, m) / t / 1e12
