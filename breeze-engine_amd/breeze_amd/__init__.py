@@ -6,11 +6,13 @@ Modules mirror the reference's public surface for this path:
 - ``quant`` for breeze/quant.py;
 - ``linear`` for breeze/linear.py (imported on demand since it pulls in torch);
 - ``ops`` for the MatMulNBits operator and weight cache of breeze/ops.py and
-  breeze/graph_session.py.
+  breeze/graph_session.py;
+- ``loader`` for the external-data mapping of breeze/loader.py (weights go
+  from the mapped file to the GPU without a host copy).
 
 The compute lives in ``libbreeze_qmm.so``, hand-written HIP behind a C ABI
 (include/breeze_qmm.h).
 """
-from . import hip_backend, ops, quant  # noqa: F401
+from . import hip_backend, loader, ops, quant  # noqa: F401
 
-__all__ = ["hip_backend", "ops", "quant", "linear"]
+__all__ = ["hip_backend", "loader", "ops", "quant", "linear"]
