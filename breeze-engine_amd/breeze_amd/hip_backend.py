@@ -76,6 +76,8 @@ try:
     _lib.i4_matmul_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
     _lib.i4_matmul_argmax_dev.restype = _i
     _lib.i4_matmul_argmax_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
+    _lib.i4_matmul_silu_mul_dev.restype = _i
+    _lib.i4_matmul_silu_mul_dev.argtypes = [_vp, _vp, _vp, _i, _vp, _vp]
     _lib.i4_block_dots_dev.restype = _i
     _lib.i4_block_dots_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
     _lib.i4_handle_info.restype = _i
@@ -269,6 +271,20 @@ def matmul(handle, a2d, N):
     err = last_error()
     if err:
         raise RuntimeError(f"i4_matmul failed: {err}")
+    return out
+
+
+def matmul_silu_mul(gate, up, a2d, N):
+    """GPU torch tensor [M, K] -> silu(a @ Wgate) * (a @ Wup), fp32 [M, N]: the
+    decoder MLP's gate/up step (kernel/qwen35_decoder.cpp:406-408) in one
+    call, asynchronous on the current stream."""
+    _require_lib()
+    import torch
+    a = a2d.to(torch.float32).contiguous()
+    M = a.shape[0]
+    out = torch.empty((M, N), dtype=torch.float32, device=a.device)
+    _check_rc(_lib.i4_matmul_silu_mul_dev(_vp(gate), _vp(up), _vp(a.data_ptr()), int(M), _vp(out.data_ptr()),
+                                          _torch_stream(a)), "i4_matmul_silu_mul_dev")
     return out
 
 

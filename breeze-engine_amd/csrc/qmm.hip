@@ -322,7 +322,7 @@ __global__ __launch_bounds__(256) void wsum_kernel(const uint4* __restrict__ W, 
 // R units go out at kernel start, behind only the activation loads, and
 // stream in while the activations are quantized into LDS (FUSED) or their
 // records, made by the stand-alone quantizer, are copied there.  Every load
-// is unconditional (units past the end read one line) and the ring is
+// is unconditional (units past the end re-read the last tile) and the ring is
 // unrolled, so the compiler's load waits stay exact across the loop back
 // edge.
 
@@ -344,6 +344,12 @@ struct GemvArgs {
     int64_t* idx;              // [M] argmax, or NULL
     unsigned int* ticket;      // with idx: workgroups done (0 between calls)
     unsigned long long* key;   // with idx: [8] merged argmax keys (0 between calls)
+    // Second weight set for the gate/up pairing, in the same layout as W, S,
+    // Z, D (same N, K, bits and scale grouping).
+    const uint4* W2;
+    const float* S2;
+    const int8_t* Z2;
+    const int32_t* D2;
     int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
     int ntiles, NG, RG, pair_xcd;
 };
@@ -423,8 +429,10 @@ __host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG) {
 // loads need.  They are preloaded into SGPRs at wave launch (kernarg
 // preload, 14 SGPRs), so those loads do not wait for a kernarg fetch; the
 // rest of the arguments come from the struct as the code reaches them.
-// misc = sc_shift | RG << 8 | pair_xcd << 10.
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R>
+// misc = sc_shift | RG << 8 | pair_xcd << 10.  PAIR: gate and up projections
+// in one launch; each output tile is the gate tile then the up tile of the
+// same columns, and C = silu(gate) * up.
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR>
 __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
                                                              int pK, int pnblk, int pM, int pnbg, int pntiles,
                                                              int pNG, int pngrp, int misc, GemvArgs args) {
@@ -471,7 +479,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int nT = base_t + (g < rem_t ? 1 : 0);
     const int nbg = a.nbg;
     const int npw = (nbg + kProducers - 1) / kProducers;  // phases per tile
-    const int U = nT * npw;                                // phases of this workgroup
+    const int U = nT * npw * (PAIR ? 2 : 1);               // phases of this workgroup
 
     const DecLds lay = dec_lds(min(a.M, 4), a.nblk, JG);
     uint8_t* recs = smem + lay.recs;
@@ -489,7 +497,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // tile ld_t, ld_rem units before the tile ends; ld_w, ld_s and ld_m index
     // the tile's weights, scales and per-block metadata.  Past the end ld_c
     // is out of range (no work) and the loads re-read the last tile.
-    int ld_c = wave, ld_rem = npw, ld_t = 0;
+    int ld_c = wave, ld_rem = npw, ld_t = 0, ld_sel = 0;  // ld_sel: up tile of a pair
     uint32_t ld_w = (uint32_t)t_begin * nbg * 64;
     uint32_t ld_s = (uint32_t)t_begin * a.ngrp * 16;
     uint32_t ld_m = (uint32_t)t_begin * nbg * 16;
@@ -501,30 +509,37 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         // Opaque to the optimizer, so the loads are not split into
         // uniform-address copies on branches of their own.
         asm("" : "+v"(wi), "+v"(mi), "+v"(si));
-        p.w = a.W[wi];
+        const bool up = PAIR && ld_sel;
+        p.w = (up ? a.W2 : a.W)[wi];
         if (EXTRA) {
-            const fvec sv = *reinterpret_cast<const fvec*>(a.S + (size_t)mi * JG);
-            const ivec dv = *reinterpret_cast<const ivec*>(a.D + (size_t)mi * JG);
+            const fvec sv = *reinterpret_cast<const fvec*>((up ? a.S2 : a.S) + (size_t)mi * JG);
+            const ivec dv = *reinterpret_cast<const ivec*>((up ? a.D2 : a.D) + (size_t)mi * JG);
 #pragma unroll
             for (int jb = 0; jb < JG; ++jb) {
                 p.sc[EXTRA ? jb : 0] = sv[jb];
                 p.dl[EXTRA ? jb : 0] = dv[jb];
             }
-            if (JG == 4) p.zp = *reinterpret_cast<const uint32_t*>(a.Z + (size_t)mi * 4);
+            if (JG == 4) p.zp = *reinterpret_cast<const uint32_t*>((up ? a.Z2 : a.Z) + (size_t)mi * 4);
         } else {
-            p.sc[0] = a.S[si];
+            p.sc[0] = (up ? a.S2 : a.S)[si];
         }
         p.c = ld_c;
         ld_c += kProducers;
         if (--ld_rem == 0) {
             ld_rem = npw;
-            if (++ld_t < nT) {
+            if (PAIR && ld_sel == 0 && ld_t < nT) {
+                ld_sel = 1;  // the same tile's up projection
                 ld_c = wave;
-                ld_w += nbg * 64;
-                ld_s += a.ngrp * 16;
-                ld_m += nbg * 16;
             } else {
-                ld_c = 1 << 24;
+                if (PAIR) ld_sel = 0;
+                if (++ld_t < nT) {
+                    ld_c = wave;
+                    ld_w += nbg * 64;
+                    ld_s += a.ngrp * 16;
+                    ld_m += nbg * 16;
+                } else {
+                    ld_c = 1 << 24;
+                }
             }
         }
     };
@@ -629,9 +644,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         // Lane (row me, column col) of the current tile.
         const float* sa_row = sa_l + me * lay.sa_pitch;
         const bool tail_pad = a.nblk != nbg * JG;  // the last chunk has padding blocks
-        float acc = 0.0f;
+        float acc = 0.0f, gate = 0.0f;
         unsigned long long best = 0;
-        int pr_t = 0, pr_p = 0;
+        int pr_t = 0, pr_p = 0, pr_sel = 0;
         for (int u = 0; u < U; ++u) {
             lds_barrier();
             const float* fp = fbuf + ((u & 1) * 64 + lane) * PP;
@@ -662,20 +677,29 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
             }
             if (++pr_p == npw) {
-                if (grp < Mr) {
-                    const int n = (t_begin + pr_t) * 16 + col;
-                    a.C[(size_t)(m0 + grp) * a.N + n] = acc;
-                    if (a.idx) {
-                        const unsigned long long k = argmax_key(acc, n);
-                        best = k > best ? k : best;
+                if (PAIR && pr_sel == 0) {
+                    gate = acc;  // the up tile of the same columns follows
+                    pr_sel = 1;
+                } else {
+                    // silu(g) = g / (1 + exp(-g)) (qwen35_decoder.cpp:129),
+                    // times the up projection (qwen35_decoder.cpp:408).
+                    const float v = PAIR ? gate / (1.0f + expf(-gate)) * acc : acc;
+                    if (grp < Mr) {
+                        const int n = (t_begin + pr_t) * 16 + col;
+                        a.C[(size_t)(m0 + grp) * a.N + n] = v;
+                        if (!PAIR && a.idx) {
+                            const unsigned long long k = argmax_key(acc, n);
+                            best = k > best ? k : best;
+                        }
                     }
+                    if (PAIR) pr_sel = 0;
+                    ++pr_t;
                 }
                 acc = 0.0f;
                 pr_p = 0;
-                ++pr_t;
             }
         }
-        if (a.idx) {
+        if (!PAIR && a.idx) {
             // Row maximum over the lanes of each row (lanes 16r..16r+15).
 #pragma unroll
             for (int s = 1; s < 16; s <<= 1) {
@@ -1249,6 +1273,18 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
 }
 
 // part [nparts][M] -> out[m].
+// u = silu(g) * u elementwise, silu(x) = x / (1 + exp(-x)) as in
+// kernel/qwen35_decoder.cpp:129 and 408; the same expression as the paired
+// decode kernel's epilogue, so both paths give the same bits.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ g, float* __restrict__ u,
+                                                       size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) {
+        const float x = g[i];
+        u[i] = x / (1.0f + expf(-x)) * u[i];
+    }
+}
+
 __global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long long* __restrict__ part,
                                                            int nparts, int M, int64_t* __restrict__ out) {
     const int m = blockIdx.x;
@@ -1272,6 +1308,8 @@ struct Workspace {
     uint8_t* rec = nullptr;  // prefill activation records
     size_t rec_cap = 0;
     bool pf_attr[64] = {};
+    float* gate = nullptr;  // gate projection of the unpaired gate/up path
+    size_t gate_cap = 0;
     float* hA = nullptr;  // device staging for the host-pointer entry points
     float* hC = nullptr;
     size_t hA_cap = 0, hC_cap = 0;
@@ -1511,10 +1549,11 @@ int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG) {
     return total <= kLdsMax ? total : 0;
 }
 
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R>
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR>
 hipError_t launch_dec_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipStream_t st) {
-    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R>;
-    const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (EXTRA ? 8 : 0) | ((R / 2 - 1) << 4);
+    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, PAIR>;
+    const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (EXTRA ? 8 : 0) | ((R / 2 - 1) << 4) |
+                    (PAIR ? 32 : 0);
     if (!w.attr_set[key]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
@@ -1533,17 +1572,18 @@ hipError_t launch_dec_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipS
 constexpr int kDecRing = 2;
 
 template <int BITS, bool HP, bool FUSED, bool EXTRA>
-hipError_t launch_dec_r(Workspace& w, const GemvArgs& a, int grid, int lds, int, hipStream_t st) {
-    return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing>(w, a, grid, lds, st);
+hipError_t launch_dec_r(Workspace& w, const GemvArgs& a, int grid, int lds, bool pair, hipStream_t st) {
+    return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true>(w, a, grid, lds, st)
+                : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false>(w, a, grid, lds, st);
 }
 
 template <int BITS, bool HP>
-hipError_t launch_dec_bits(Workspace& w, const GemvArgs& a, int grid, int lds, int units, bool fused,
+hipError_t launch_dec_bits(Workspace& w, const GemvArgs& a, int grid, int lds, bool pair, bool fused,
                            bool extra, hipStream_t st) {
-    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(w, a, grid, lds, units, st)
-                            : launch_dec_r<BITS, HP, false, true>(w, a, grid, lds, units, st);
-    return fused ? launch_dec_r<BITS, HP, true, false>(w, a, grid, lds, units, st)
-                 : launch_dec_r<BITS, HP, false, false>(w, a, grid, lds, units, st);
+    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(w, a, grid, lds, pair, st)
+                            : launch_dec_r<BITS, HP, false, true>(w, a, grid, lds, pair, st);
+    return fused ? launch_dec_r<BITS, HP, true, false>(w, a, grid, lds, pair, st)
+                 : launch_dec_r<BITS, HP, false, false>(w, a, grid, lds, pair, st);
 }
 
 template <int BITS, bool HP>
@@ -1599,7 +1639,21 @@ int device_cus(Workspace& w, int dev) {
 
 // Quantize + block dots + epilogue for M rows on `st`.  Exactly one of
 // dC / dCs is non-null; dIdx (optional) receives the per-row argmax.
-int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dIdx, hipStream_t st) {
+constexpr int kNotPairable = -100;  // run() with h2: the decode kernel does not take this call
+
+// Gate and up handles the paired decode kernel can stream together: the same
+// device, shape and device layout.
+bool same_layout(const Handle* a, const Handle* b) {
+    return a->device == b->device && a->N == b->N && a->K == b->K && a->bits == b->bits && a->nbg == b->nbg &&
+           a->sc_shift == b->sc_shift && a->ngrp == b->ngrp && a->sc_blk == b->sc_blk && a->extra == b->extra &&
+           (a->Z == nullptr) == (b->Z == nullptr) && (a->D == nullptr) == (b->D == nullptr);
+}
+
+// h2 (gate/up pairing): a second handle with the same layout (same_layout).
+// Returns kNotPairable, having launched nothing, when the decode kernel does
+// not take the call.
+int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dIdx, hipStream_t st,
+        const Handle* h2 = nullptr) {
     if (M < 0) {
         set_err("M must be >= 0 (got %d)", M);
         return -2;
@@ -1642,6 +1696,7 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     const int Mr_max = std::min(M, 4);
     const int lds = (M <= 8 && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     const bool dec = lds > 0;
+    if (h2 && !dec) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
     // Prefill GEMM: more than 8 rows of INT8 weights without a legacy corr.
     const bool pre = !dec && !dots && M > 8 && h->bits == 8 && h->WS && !h->has_dl;
@@ -1678,7 +1733,13 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
             a.pair_xcd = ng % 8 == 0 ? 1 : 0;
             a.NG = ng;
         }
-        const int units = (a.ntiles + a.NG - 1) / a.NG * ((a.nbg + kProducers - 1) / kProducers);
+        const bool pair = h2 != nullptr;
+        if (pair) {
+            a.W2 = h2->W;
+            a.S2 = h2->S;
+            a.Z2 = h2->Z;
+            a.D2 = h2->D;
+        }
         if (dIdx) {
             if (!w.ticket) {
                 // Allocated and zeroed once per device (not under graph capture);
@@ -1696,10 +1757,10 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
         }
         const int grid = a.NG * a.RG;
         const bool x = h->extra;
-        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w, a, grid, lds, units, fused, x, st)
-                                 : launch_dec_bits<8, false>(w, a, grid, lds, units, fused, x, st);
-        else e = hp ? launch_dec_bits<4, true>(w, a, grid, lds, units, fused, x, st)
-                    : launch_dec_bits<4, false>(w, a, grid, lds, units, fused, x, st);
+        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w, a, grid, lds, pair, fused, x, st)
+                                 : launch_dec_bits<8, false>(w, a, grid, lds, pair, fused, x, st);
+        else e = hp ? launch_dec_bits<4, true>(w, a, grid, lds, pair, fused, x, st)
+                    : launch_dec_bits<4, false>(w, a, grid, lds, pair, fused, x, st);
     } else if (pre) {
         PfArgs p{};
         p.W = reinterpret_cast<const char*>(h->W);
@@ -1778,7 +1839,7 @@ int i4_device_ok(void) {
         return 0;
     }
     hipFuncAttributes attr;
-    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&dec_kernel<8, true, true, false, kDecRing>)) !=
+    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&dec_kernel<8, true, true, false, kDecRing, false>)) !=
         hipSuccess) {
         set_err("gfx950 kernels not loadable");
         return 0;
@@ -1929,6 +1990,37 @@ int i4_matmul_dev(void* handle, const float* dA, int M, float* dC, void* stream)
     Handle* h = as_handle(handle);
     if (!h) return -1;
     return run(h, dA, M, dC, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* dC, void* stream) {
+    Handle* hg = as_handle(gate);
+    Handle* hu = as_handle(up);
+    if (!hg || !hu) return -1;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (hg->N != hu->N || hg->K != hu->K) {
+        set_err("gate and up projections differ in shape (N %d/%d, K %d/%d)", hg->N, hu->N, hg->K, hu->K);
+        return -2;
+    }
+    if (same_layout(hg, hu)) {
+        const int rc = run(hg, dA, M, dC, nullptr, nullptr, st, hu);
+        if (rc != kNotPairable) return rc;
+    }
+    // Two projections, then the elementwise epilogue.
+    if (M <= 0 || !dC) return run(hu, dA, M, dC, nullptr, nullptr, st);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev != hg->device) {
+        set_err("handle lives on device %d but device %d is current", hg->device, dev);
+        return -3;
+    }
+    Workspace& w = g_ws[dev];
+    const size_t n = (size_t)M * hg->N;
+    if (!grow(&w.gate, &w.gate_cap, n, "workspace alloc")) return -4;
+    int rc = run(hg, dA, M, w.gate, nullptr, nullptr, st);
+    if (rc == 0) rc = run(hu, dA, M, dC, nullptr, nullptr, st);
+    if (rc) return rc;
+    silu_mul_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(w.gate, dC, n);
+    return hip_ok(hipGetLastError(), "silu-mul launch") ? 0 : -5;
 }
 
 int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream) {

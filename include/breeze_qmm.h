@@ -91,6 +91,15 @@ int i4_matmul_dev(void* handle, const float* dA, int M, float* dC, void* stream)
 int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC,
                          int64_t* dIdx, void* stream);
 
+/* Fused gate/up projection of a decoder MLP, replacing the two i4_matmul calls
+ * and the SiLU loop of kernel/qwen35_decoder.cpp:406-408:
+ *   dC[M,N] = silu(dA * Wgate) * (dA * Wup),  silu(x) = x / (1 + exp(-x)).
+ * Both projections are bit-identical to i4_matmul_dev's; the SiLU uses the
+ * device expf.  With M <= 8 and handles of the same layout it is one decode
+ * launch (SiLU and product in the epilogue); otherwise two launches and an
+ * elementwise kernel with the same arithmetic.  Returns as i4_matmul_dev. */
+int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* dC, void* stream);
+
 /* Handle facts: out[0..7] = N, K, bits, scale group (blocks per distinct
  * scale, 0 = one per column), has_zero_points, has_corr_delta,
  * device bytes held, device ordinal.  Returns 0 or -1. */
