@@ -207,6 +207,16 @@ __device__ inline v4i mfma16(uint64_t a, uint64_t b) {
     return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, v4i{0, 0, 0, 0}, 0, 0, 0);
 }
 
+// v_mfma_i32_16x16x64_i8: A byte i of lane l multiplies B byte i of lane
+// (column + 16 * (l >> 4)) (checked on the device for all 1024 positions),
+// so a lane's first 8 bytes pair with the first block of a decode chunk's
+// block pair and its last 8 bytes with the second.
+__device__ inline v4i mfma64(const uint4& a, const uint4& b) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{(int)a.x, (int)a.y, (int)a.z, (int)a.w},
+                                                   v4i{(int)b.x, (int)b.y, (int)b.z, (int)b.w},
+                                                   v4i{0, 0, 0, 0}, 0, 0, 0);
+}
+
 // ------------------------------------------------------------------ repack
 
 // MatMulNBits bytes (or signed bytes, raw_signed) -> device chunk layout.
@@ -407,12 +417,17 @@ __host__ __device__ inline int lds_take(int& off, int bytes) {
     return o;
 }
 
-__host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG) {
+// P64 (one or two rows, block pairs per MFMA): each 8-byte k-octet of a
+// record sits in a 16-byte slot behind 8 zero bytes, 128 B per block plus
+// one zero slot at the row end, so one 16-byte read yields [octet | zeros]
+// or [zeros | octet]; the row pitch of the second row is 32 B past a
+// multiple of 256 B.
+__host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG, bool p64 = false) {
     DecLds l;
-    l.rec_pitch = nblk * 64;
+    l.rec_pitch = p64 ? nblk * 128 + 16 : nblk * 64;
     l.sa_pitch = (nblk + 3) / 4 * 4;
     if (Mr_max > 1) {
-        l.rec_pitch = (l.rec_pitch + 191) / 256 * 256 + 64;
+        l.rec_pitch = p64 ? (l.rec_pitch + 223) / 256 * 256 + 32 : (l.rec_pitch + 191) / 256 * 256 + 64;
         l.sa_pitch = (l.sa_pitch + 59) / 64 * 64 + 4;
     }
     int off = 0;
@@ -432,7 +447,7 @@ __host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG) {
 // misc = sc_shift | RG << 8 | pair_xcd << 10.  PAIR: gate and up projections
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR>
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR, bool P64>
 __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
                                                              int pK, int pnblk, int pM, int pnbg, int pntiles,
                                                              int pNG, int pngrp, int misc, GemvArgs args) {
@@ -481,7 +496,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int npw = (nbg + kProducers - 1) / kProducers;  // phases per tile
     const int U = nT * npw * (PAIR ? 2 : 1);               // phases of this workgroup
 
-    const DecLds lay = dec_lds(min(a.M, 4), a.nblk, JG);
+    const DecLds lay = dec_lds(min(a.M, 4), a.nblk, JG, P64);
     uint8_t* recs = smem + lay.recs;
     float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
     int* sq_l = reinterpret_cast<int*>(smem + lay.sq);
@@ -593,9 +608,20 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                            s, sum, p0, p1);
                 if (blk < nb_rows) {
                     const int m = blk / a.nblk, j = blk - m * a.nblk;
-                    uint8_t* rec = recs + m * lay.rec_pitch + j * 64;
-                    *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
-                    *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
+                    if (P64) {
+                        // Lane e holds bytes 4(e&1).. of k-octet e>>1: the
+                        // slot's zero half, then the octet.
+                        uint32_t* sh = reinterpret_cast<uint32_t*>(recs + m * lay.rec_pitch + j * 128 +
+                                                                   (e >> 1) * 16) + (e & 1);
+                        sh[0] = 0u;
+                        sh[2] = p0;
+                        sh[16] = 0u;  // l octets, 64 B further
+                        sh[18] = p1;
+                    } else {
+                        uint8_t* rec = recs + m * lay.rec_pitch + j * 64;
+                        *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
+                        *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
+                    }
                     if (e == 0) {
                         sa_l[m * lay.sa_pitch + j] = s;
                         sq_l[m * lay.sa_pitch + j] = (EXTRA ? -1 : -8) * sum;
@@ -612,7 +638,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             auto put = [&](int i, const uint4& v) {
                 i = min(i, nrec - 1);
                 const int m = (i >= L) + (i >= 2 * L) + (i >= 3 * L);
-                dst[i + m * gap] = v;
+                if (P64) {
+                    // Source uint4 q of a block: h or l (q >> 1) octets
+                    // 2(q & 1) and 2(q & 1) + 1, each into its slot.
+                    const int r = i - m * L, j = r >> 2, q = r & 3;
+                    uint4* slot = reinterpret_cast<uint4*>(recs + m * lay.rec_pitch + j * 128 + (q >> 1) * 64 +
+                                                           (q & 1) * 32);
+                    slot[0] = make_uint4(0u, 0u, v.x, v.y);
+                    slot[1] = make_uint4(0u, 0u, v.z, v.w);
+                } else {
+                    dst[i + m * gap] = v;
+                }
             };
             put(tid, r0);
             put(1024 + tid, r1);
@@ -629,7 +665,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         }
         {
             uint32_t* cst = reinterpret_cast<uint32_t*>(smem + lay.consts);
-            if (tid < 128) cst[tid] = tid < 64 ? 0x40404040u : 0u;  // [0,256) bytes of 64, [256,512) zeros
+            if (P64) {
+                // [8 zeros][8 bytes of 64], then zeros; and each record row's
+                // closing zero slot.
+                if (tid < 128) cst[tid] = (tid == 2 || tid == 3) ? 0x40404040u : 0u;
+                if (tid < 4 * Mr) {
+                    uint32_t* z = reinterpret_cast<uint32_t*>(recs + (tid >> 2) * lay.rec_pitch + a.nblk * 128);
+                    z[tid & 3] = 0u;
+                }
+            } else if (tid < 128) {
+                cst[tid] = tid < 64 ? 0x40404040u : 0u;  // [0,256) bytes of 64, [256,512) zeros
+            }
         }
     };
 
@@ -746,6 +792,16 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const bool is_data = ars < 2 && arg < Mr;
     const int data_base = lay.recs + arg * lay.rec_pitch + ars * 32 + kq * 8;
     const int const_base = lay.consts + ((ars >= 2 && arg < Mr) ? 0 : 256) + kq * 8;
+    // P64: A row r = 8 * activation row + 4 * (block of the pair) + slot,
+    // read as 16 bytes from the zero-padded octet slots ([octet | zeros] for
+    // the pair's first block, [zeros | octet] for its second).  Output lane
+    // (col, grp): activation row grp >> 1, block 2 * mi + (grp & 1).
+    const int p_row = arow >> 3, p_sel = (arow >> 2) & 1;
+    const bool p_data = ars < 2 && p_row < Mr;
+    const int p_data_base = lay.recs + p_row * lay.rec_pitch + ars * 64 + kq * 16 + p_sel * 128 + 8 - 8 * p_sel;
+    const int p_const_base = lay.consts + ((ars >= 2 && p_row < Mr) ? 8 - 8 * p_sel : 16);
+    const int o_row = min(grp >> 1, Mr - 1), o_sel = grp & 1;
+    float* const p_fout = fbuf + (col + 16 * (grp >> 1)) * PP + wave * JG + o_sel;
 
     for (int u0 = 0; u0 < U; u0 += R) {
 #pragma unroll
@@ -753,7 +809,46 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             const bool live = u0 + d < U;  // uniform over the workgroup
             const int c = ring[d].c;
             const int buf = (u0 + d) & 1;
-            if (c < nbg) {
+            if (P64 && c < nbg) {
+                const Unit<JG, EXTRA>& cur = ring[d];
+                const int abase = p_data ? p_data_base + c * JG * 128 : p_const_base;
+                int2 nsq2 = make_int2(0, 0);  // this lane's block in each pair
+                if (BITS == 4) {
+                    const int* q = sq_l + o_row * lay.sa_pitch + c * 4 + o_sel;
+                    nsq2 = make_int2(q[0], q[2]);
+                }
+#pragma unroll
+                for (int mi = 0; mi < JG / 2; ++mi) {
+                    // Blocks past nblk (last chunk) read padding; the chain
+                    // never folds them.
+                    uint4 bop = cur.w;
+                    if (BITS == 4) {
+                        const uint64_t b0 = unpack_b(cur.w, 2 * mi, 4), b1 = unpack_b(cur.w, 2 * mi + 1, 4);
+                        bop = make_uint4((uint32_t)b0, (uint32_t)(b0 >> 32), (uint32_t)b1, (uint32_t)(b1 >> 32));
+                    }
+                    const uint8_t* ap = smem + abase + (p_data ? mi * 256 : 0);
+                    const uint2 alo = *reinterpret_cast<const uint2*>(ap);
+                    const uint2 ahi = *reinterpret_cast<const uint2*>(ap + 8);
+                    const v4i dd = mfma64(make_uint4(alo.x, alo.y, ahi.x, ahi.y), bop);
+                    const int jb = 2 * mi + o_sel;
+                    int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
+                    if (BITS == 4) {
+                        const int nsq = mi == 0 ? nsq2.x : nsq2.y;
+                        cs += EXTRA ? (int)(int8_t)((o_sel ? cur.zp >> 8 : cur.zp) >> (16 * mi)) * nsq : nsq;
+                    }
+                    float sc = cur.sc[0];
+                    if (EXTRA) {
+                        // Values first, then the lane's pick: a select
+                        // between array elements would index the unit in
+                        // memory.
+                        const int dl0 = cur.dl[EXTRA ? 2 * mi : 0], dl1 = cur.dl[EXTRA ? 2 * mi + 1 : 0];
+                        const float sc0 = cur.sc[EXTRA ? 2 * mi : 0], sc1 = cur.sc[EXTRA ? 2 * mi + 1 : 0];
+                        cs += (HP ? 256 : 1) * (o_sel ? dl1 : dl0);
+                        sc = o_sel ? sc1 : sc0;
+                    }
+                    p_fout[buf * 64 * PP + 2 * mi] = (float)cs * sc;
+                }
+            } else if (!P64 && c < nbg) {
                 const Unit<JG, EXTRA>& cur = ring[d];
                 const int abase = is_data ? data_base + c * JG * 64 : const_base;
                 int4 sqv = make_int4(0, 0, 0, 0);
@@ -1315,7 +1410,7 @@ struct Workspace {
     size_t hA_cap = 0, hC_cap = 0;
     hipStream_t stream = nullptr;
     int n_cu = 0;
-    bool attr_set[64] = {};
+    bool attr_set[128] = {};
 };
 
 constexpr int kMaxDevices = 64;
@@ -1543,17 +1638,17 @@ constexpr int kFusedMaxBlocks = 512;  // row-blocks the prologue quantizes (4 pa
 // LDS bytes of the decode kernel, or 0 if the activation records of a row
 // group do not fit (in LDS, or in the prologue's 6-uint4-per-thread record
 // copy).
-int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG) {
+int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG, bool p64 = false) {
     if (Mr_max * a.nblk > kFusedMaxBlocks && Mr_max * a.nblk * 4 > 6 * kDecWaves * 64) return 0;
-    const int total = dec_lds(Mr_max, a.nblk, JG).total;
+    const int total = dec_lds(Mr_max, a.nblk, JG, p64).total;
     return total <= kLdsMax ? total : 0;
 }
 
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR>
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR, bool P64>
 hipError_t launch_dec_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipStream_t st) {
-    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, PAIR>;
+    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, PAIR, P64>;
     const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (EXTRA ? 8 : 0) | ((R / 2 - 1) << 4) |
-                    (PAIR ? 32 : 0);
+                    (PAIR ? 32 : 0) | (P64 ? 64 : 0);
     if (!w.attr_set[key]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
@@ -1572,18 +1667,21 @@ hipError_t launch_dec_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipS
 constexpr int kDecRing = 2;
 
 template <int BITS, bool HP, bool FUSED, bool EXTRA>
-hipError_t launch_dec_r(Workspace& w, const GemvArgs& a, int grid, int lds, bool pair, hipStream_t st) {
-    return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true>(w, a, grid, lds, st)
-                : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false>(w, a, grid, lds, st);
+hipError_t launch_dec_r(Workspace& w, const GemvArgs& a, int grid, int lds, bool pair, bool p64,
+                        hipStream_t st) {
+    if (p64) return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true, true>(w, a, grid, lds, st)
+                         : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false, true>(w, a, grid, lds, st);
+    return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true, false>(w, a, grid, lds, st)
+                : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false, false>(w, a, grid, lds, st);
 }
 
 template <int BITS, bool HP>
-hipError_t launch_dec_bits(Workspace& w, const GemvArgs& a, int grid, int lds, bool pair, bool fused,
+hipError_t launch_dec_bits(Workspace& w, const GemvArgs& a, int grid, int lds, bool pair, bool p64, bool fused,
                            bool extra, hipStream_t st) {
-    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(w, a, grid, lds, pair, st)
-                            : launch_dec_r<BITS, HP, false, true>(w, a, grid, lds, pair, st);
-    return fused ? launch_dec_r<BITS, HP, true, false>(w, a, grid, lds, pair, st)
-                 : launch_dec_r<BITS, HP, false, false>(w, a, grid, lds, pair, st);
+    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(w, a, grid, lds, pair, p64, st)
+                            : launch_dec_r<BITS, HP, false, true>(w, a, grid, lds, pair, p64, st);
+    return fused ? launch_dec_r<BITS, HP, true, false>(w, a, grid, lds, pair, p64, st)
+                 : launch_dec_r<BITS, HP, false, false>(w, a, grid, lds, pair, p64, st);
 }
 
 template <int BITS, bool HP>
@@ -1694,7 +1792,11 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     // activations itself; larger ones go through the stand-alone quantizer
     // once instead of once per workgroup.
     const int Mr_max = std::min(M, 4);
-    const int lds = (M <= 8 && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
+    // One or two rows: block pairs per MFMA (P64) when its larger record
+    // layout fits in LDS.
+    const int lds_p64 = (M <= 2 && !dots) ? plan_dec_lds(a, Mr_max, JG, true) : 0;
+    const bool p64 = lds_p64 > 0;
+    const int lds = p64 ? lds_p64 : (M <= 8 && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     const bool dec = lds > 0;
     if (h2 && !dec) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
@@ -1757,10 +1859,10 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
         }
         const int grid = a.NG * a.RG;
         const bool x = h->extra;
-        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w, a, grid, lds, pair, fused, x, st)
-                                 : launch_dec_bits<8, false>(w, a, grid, lds, pair, fused, x, st);
-        else e = hp ? launch_dec_bits<4, true>(w, a, grid, lds, pair, fused, x, st)
-                    : launch_dec_bits<4, false>(w, a, grid, lds, pair, fused, x, st);
+        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w, a, grid, lds, pair, p64, fused, x, st)
+                                 : launch_dec_bits<8, false>(w, a, grid, lds, pair, p64, fused, x, st);
+        else e = hp ? launch_dec_bits<4, true>(w, a, grid, lds, pair, p64, fused, x, st)
+                    : launch_dec_bits<4, false>(w, a, grid, lds, pair, p64, fused, x, st);
     } else if (pre) {
         PfArgs p{};
         p.W = reinterpret_cast<const char*>(h->W);
@@ -1839,7 +1941,7 @@ int i4_device_ok(void) {
         return 0;
     }
     hipFuncAttributes attr;
-    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&dec_kernel<8, true, true, false, kDecRing, false>)) !=
+    if (hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&dec_kernel<8, true, true, false, kDecRing, false, false>)) !=
         hipSuccess) {
         set_err("gfx950 kernels not loadable");
         return 0;
