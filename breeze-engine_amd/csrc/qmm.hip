@@ -208,9 +208,10 @@ __device__ inline v4i mfma16(uint64_t a, uint64_t b) {
 }
 
 // v_mfma_i32_16x16x64_i8: A byte i of lane l multiplies B byte i of lane
-// (column + 16 * (l >> 4)) (checked on the device for all 1024 positions),
-// so a lane's first 8 bytes pair with the first block of a decode chunk's
-// block pair and its last 8 bytes with the second.
+// (column + 16 * (l >> 4)), so a lane's first 8 bytes pair with the first
+// block of a decode chunk's block pair and its last 8 bytes with the second
+// (the decode parity tests with one and two rows pin this pairing: any other
+// would change the exact block sums).
 __device__ inline v4i mfma64(const uint4& a, const uint4& b) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{(int)a.x, (int)a.y, (int)a.z, (int)a.w},
                                                    v4i{(int)b.x, (int)b.y, (int)b.z, (int)b.w},
