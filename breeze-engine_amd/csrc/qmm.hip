@@ -490,6 +490,41 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     }
     const int m0 = rg * 4;
     const int Mr = min(4, a.M - m0);
+
+    // Activation loads, ahead of all other set-up in program order: at kernel
+    // start the prologue's instructions are fetched cold, and timestamps put
+    // the load ~1.4 us after wave start when it sat behind the set-up code.
+    // Row m of a block index follows by comparison (at most four rows).
+    const int nb_rows = Mr * a.nblk;
+    uint4 av[4];
+    uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
+    if (FUSED) {
+        const int npass_ld = (nb_rows + 127) >> 7;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            if (p >= npass_ld) break;
+            const int blk = min(p * 128 + (tid >> 3), nb_rows - 1);
+            const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk), j = blk - m * a.nblk;
+            av[p] = *reinterpret_cast<const uint4*>(a.A + (size_t)(m0 + m) * a.K + 32 * j + 4 * (tid & 7));
+        }
+    } else {
+        // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
+        // scale and sum(q) rows as uint4 (Mr * nblk4 / 4 each).
+        const uint4* rsrc = reinterpret_cast<const uint4*>(a.Aq + (size_t)m0 * a.nblk * 64);
+        const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+        r0 = rsrc[min(tid, nrec - 1)];
+        r1 = rsrc[min(1024 + tid, nrec - 1)];
+        r2 = rsrc[min(2048 + tid, nrec - 1)];
+        r3 = rsrc[min(3072 + tid, nrec - 1)];
+        r4 = rsrc[min(4096 + tid, nrec - 1)];
+        r5 = rsrc[min(5120 + tid, nrec - 1)];
+        const int mi = min(tid, nmeta - 1);
+        const int mm = (mi * 4) / a.nblk4, mj = mi * 4 - mm * a.nblk4;
+        rsa = *reinterpret_cast<const uint4*>(a.Sa + (size_t)(m0 + mm) * a.nblk4 + mj);
+        rsq = *reinterpret_cast<const uint4*>(a.Sq + (size_t)(m0 + mm) * a.nblk4 + mj);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
     const int t_begin = g * base_t + min(g, rem_t);
     const int nT = base_t + (g < rem_t ? 1 : 0);
@@ -561,39 +596,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     };
 
     // ---------------- prologue
-    // Activation loads first, then the first R weight units, then the
-    // activations are quantized (or their records copied) into LDS while the
-    // weights stream in.  The scheduling barriers keep this issue order.
-    const int nb_rows = Mr * a.nblk;
-    uint4 av[4];
-    uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
-    auto load_acts = [&]() {
-        if (FUSED) {
-            const int npass_ld = (nb_rows + 127) >> 7;
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                if (p >= npass_ld) break;
-                const int blk = min(p * 128 + (tid >> 3), nb_rows - 1);
-                const int m = blk / a.nblk, j = blk - m * a.nblk;
-                av[p] = *reinterpret_cast<const uint4*>(a.A + (size_t)(m0 + m) * a.K + 32 * j + 4 * (tid & 7));
-            }
-        } else {
-            // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
-            // scale and sum(q) rows as uint4 (Mr * nblk4 / 4 each).
-            const uint4* rsrc = reinterpret_cast<const uint4*>(a.Aq + (size_t)m0 * a.nblk * 64);
-            const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
-            r0 = rsrc[min(tid, nrec - 1)];
-            r1 = rsrc[min(1024 + tid, nrec - 1)];
-            r2 = rsrc[min(2048 + tid, nrec - 1)];
-            r3 = rsrc[min(3072 + tid, nrec - 1)];
-            r4 = rsrc[min(4096 + tid, nrec - 1)];
-            r5 = rsrc[min(5120 + tid, nrec - 1)];
-            const int mi = min(tid, nmeta - 1);
-            const int mm = (mi * 4) / a.nblk4, mj = mi * 4 - mm * a.nblk4;
-            rsa = *reinterpret_cast<const uint4*>(a.Sa + (size_t)(m0 + mm) * a.nblk4 + mj);
-            rsq = *reinterpret_cast<const uint4*>(a.Sq + (size_t)(m0 + mm) * a.nblk4 + mj);
-        }
-    };
+    // The activation loads went out first (above); the first R weight units
+    // follow, then the activations are quantized (or their records copied)
+    // into LDS while the weights stream in.  The scheduling barriers keep
+    // this issue order.
     auto store_acts = [&]() {
         if (FUSED) {
             const int npass = (nb_rows + 127) >> 7;
@@ -685,7 +691,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         // Its fold is one dependent FMA chain per output and paces the
         // phases: first pick of the SIMD's issue slots over the producers.
         __builtin_amdgcn_s_setprio(3);
-        load_acts();
         store_acts();
         lds_barrier();
         // Lane (row me, column col) of the current tile.
@@ -776,8 +781,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
 
     // ================= producers (waves 0..14)
     Unit<JG, EXTRA> ring[R];
-    load_acts();
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int d = 0; d < R; ++d) load_unit(ring[d]);
     __builtin_amdgcn_sched_barrier(0);
