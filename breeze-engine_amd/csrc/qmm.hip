@@ -614,7 +614,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                                        __uint_as_float(av[p].z), __uint_as_float(av[p].w)),
                            s, sum, p0, p1);
                 if (blk < nb_rows) {
-                    const int m = blk / a.nblk, j = blk - m * a.nblk;
+                    const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk), j = blk - m * a.nblk;
                     if (P64) {
                         // Lane e holds bytes 4(e&1).. of k-octet e>>1: the
                         // slot's zero half, then the octet.
