@@ -55,7 +55,7 @@ def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, bits, expl
             u = orc.matmul(qu, su, zu, N, K, bits, A, hp)
             want = _silu_mul(g, u)
             fused = {}
-            for rows in (1, 3, 5, 8):
+            for rows in (1, 2, 3, 5, 8):
                 got = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A[:rows]).cuda(), N).cpu().numpy()
                 np.testing.assert_allclose(got, want[:rows], rtol=1e-6, atol=1e-30, err_msg=f"{rows} rows")
                 fused[rows] = got

@@ -37,7 +37,7 @@ def test_matmul_bit_exact(gpu, hb, orc, hi_prec, N, K, bits, dtype, explicit_zer
     try:
         for hp in (False, True):
             hb.set_hi_prec(hp)
-            for rows in (1, 3, 8, 9, 17):
+            for rows in (1, 2, 3, 8, 9, 17):
                 A = rng.normal(size=(rows, K)).astype(np.float32)
                 want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
                 c_host, c_dev = _run_both(hb, gpu, h, A, N)
