@@ -494,18 +494,20 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // Activation loads, ahead of all other set-up in program order: at kernel
     // start the prologue's instructions are fetched cold, and timestamps put
     // the load ~1.4 us after wave start when it sat behind the set-up code.
-    // Row m of a block index follows by comparison (at most four rows).
+    // K is a multiple of 32, so the rows m0.. of A are nb_rows contiguous
+    // 32-float blocks, and the staged scale and sum rows (pitch nblk4) are
+    // contiguous too: a block index is an offset, with no row/column split.
     const int nb_rows = Mr * a.nblk;
     uint4 av[4];
     uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
     if (FUSED) {
+        const float* arow = a.A + (size_t)m0 * a.K + 4 * (tid & 7);
         const int npass_ld = (nb_rows + 127) >> 7;
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             if (p >= npass_ld) break;
             const int blk = min(p * 128 + (tid >> 3), nb_rows - 1);
-            const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk), j = blk - m * a.nblk;
-            av[p] = *reinterpret_cast<const uint4*>(a.A + (size_t)(m0 + m) * a.K + 32 * j + 4 * (tid & 7));
+            av[p] = *reinterpret_cast<const uint4*>(arow + 32 * blk);
         }
     } else {
         // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
@@ -519,9 +521,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         r4 = rsrc[min(4096 + tid, nrec - 1)];
         r5 = rsrc[min(5120 + tid, nrec - 1)];
         const int mi = min(tid, nmeta - 1);
-        const int mm = (mi * 4) / a.nblk4, mj = mi * 4 - mm * a.nblk4;
-        rsa = *reinterpret_cast<const uint4*>(a.Sa + (size_t)(m0 + mm) * a.nblk4 + mj);
-        rsq = *reinterpret_cast<const uint4*>(a.Sq + (size_t)(m0 + mm) * a.nblk4 + mj);
+        rsa = *reinterpret_cast<const uint4*>(a.Sa + (size_t)m0 * a.nblk4 + 4 * mi);
+        rsq = *reinterpret_cast<const uint4*>(a.Sq + (size_t)m0 * a.nblk4 + 4 * mi);
     }
     __builtin_amdgcn_sched_barrier(0);
 
@@ -548,13 +549,26 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // tile ld_t, ld_rem units before the tile ends; ld_w, ld_s and ld_m index
     // the tile's weights, scales and per-block metadata.  Past the end ld_c
     // is out of range (no work) and the loads re-read the last tile.
+    //
+    // A producer with no chunk in a tile's short last phase still fills its
+    // ring slot.  That load's data is never used, so its weight address is
+    // the chunk this producer loads next in the following tile (chunk
+    // wave + 15, requested two phases later): the slot warms L2 for it.  The
+    // tiles of a workgroup are contiguous, so that is chunk nbg + wave + 15
+    // from the current tile.  On the last tile (and for gate/up pairs, whose
+    // next tile lies in the other array) the load re-reads the tile's last
+    // chunk instead, so every address stays inside the workgroup's tiles.
     int ld_c = wave, ld_rem = npw, ld_t = 0, ld_sel = 0;  // ld_sel: up tile of a pair
     uint32_t ld_w = (uint32_t)t_begin * nbg * 64;
     uint32_t ld_s = (uint32_t)t_begin * a.ngrp * 16;
     uint32_t ld_m = (uint32_t)t_begin * nbg * 16;
+    const int pf_c = nbg + kProducers + wave;
+    const bool pf = !PAIR && npw >= 2 && wave + kProducers < nbg;
+    int ld_idle = (pf && nT > 1) ? pf_c : nbg - 1;  // weight chunk of a load with no work
     auto load_unit = [&](Unit<JG, EXTRA>& p) {
         const int c = min(ld_c, nbg - 1);
-        uint32_t wi = ld_w + c * 64 + lane;                                // weight uint4 index
+        const int cw = ld_c < nbg ? ld_c : ld_idle;
+        uint32_t wi = ld_w + cw * 64 + lane;                               // weight uint4 index
         uint32_t mi = ld_m + c * 16 + col;                                 // per-block metadata (EXTRA)
         uint32_t si = ld_s + (uint32_t)((c * JG) >> a.sc_shift) * 16 + col;  // scale index
         // Opaque to the optimizer, so the loads are not split into
@@ -588,6 +602,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     ld_w += nbg * 64;
                     ld_s += a.ngrp * 16;
                     ld_m += nbg * 16;
+                    if (ld_t + 1 == nT) ld_idle = nbg - 1;
                 } else {
                     ld_c = 1 << 24;
                 }
@@ -664,7 +679,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             put(4096 + tid, r4);
             put(5120 + tid, r5);
             const int mi = min(tid, nmeta - 1);
-            const int mm = (mi * 4) / a.nblk4;
+            const int mm = (4 * mi >= a.nblk4) + (4 * mi >= 2 * a.nblk4) + (4 * mi >= 3 * a.nblk4);
             const int md = mi + mm * ((lay.sa_pitch - a.nblk4) >> 2);
             reinterpret_cast<uint4*>(sa_l)[md] = rsa;
             const uint32_t f = EXTRA ? 0xFFFFFFFFu : 0xFFFFFFF8u;  // -1 or -8
@@ -705,28 +720,44 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             const int c0 = kProducers * pr_p;
             const float* sp = sa_row + c0 * JG;
             if (c0 + kProducers < nbg || (c0 + kProducers == nbg && !tail_pad)) {
-                // Full phase: every block is real.  Groups of chunks: all
-                // reads of a group, then its FMAs.
-                constexpr int G = JG == 4 ? 4 : 8;
+                // Full phase: every block is real.  All fifteen chunks'
+                // reads, then the FMAs: right after the barrier the reads
+                // queue behind the producers' operand reads (~0.3 us), so
+                // one wait instead of one per group of chunks.
+                fvec fv[kProducers], sv[kProducers];
 #pragma unroll
-                for (int h = 0; h < kProducers; h += G) {
-                    fvec fv[G], sv[G];
+                for (int i = 0; i < kProducers; ++i) {
+                    fv[i] = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    sv[i] = *reinterpret_cast<const fvec*>(sp + i * JG);
+                }
 #pragma unroll
-                    for (int i = 0; i < G; ++i) {
-                        if (h + i >= kProducers) break;
-                        fv[i] = *reinterpret_cast<const fvec*>(fp + (h + i) * JG);
-                        sv[i] = *reinterpret_cast<const fvec*>(sp + (h + i) * JG);
-                    }
+                for (int i = 0; i < kProducers; ++i) {
 #pragma unroll
-                    for (int i = 0; i < G; ++i) {
-                        if (h + i >= kProducers) break;
-#pragma unroll
-                        for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[i][jb], fv[i][jb], acc);
-                    }
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[i][jb], fv[i][jb], acc);
                 }
             } else {
-                const int nb = a.nblk - c0 * JG;
-                for (int b = 0; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
+                // The tile's last phase: whole chunks two at a time with
+                // wide reads, then the blocks of a padded last chunk.
+                const int nb = a.nblk - c0 * JG, nwc = nb / JG;
+                int i = 0;
+                for (; i + 2 <= nwc; i += 2) {
+                    const fvec f0 = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    const fvec s0 = *reinterpret_cast<const fvec*>(sp + i * JG);
+                    const fvec f1 = *reinterpret_cast<const fvec*>(fp + (i + 1) * JG);
+                    const fvec s1 = *reinterpret_cast<const fvec*>(sp + (i + 1) * JG);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s0[jb], f0[jb], acc);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s1[jb], f1[jb], acc);
+                }
+                if (i < nwc) {
+                    const fvec f0 = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    const fvec s0 = *reinterpret_cast<const fvec*>(sp + i * JG);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s0[jb], f0[jb], acc);
+                    ++i;
+                }
+                for (int b = i * JG; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
             }
             if (++pr_p == npw) {
                 if (PAIR && pr_sel == 0) {
