@@ -445,23 +445,24 @@ __host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG, bool p64
 // loads need.  They are preloaded into SGPRs at wave launch (kernarg
 // preload, 14 SGPRs), so those loads do not wait for a kernarg fetch; the
 // rest of the arguments come from the struct as the code reaches them.
-// misc = sc_shift | RG << 8 | pair_xcd << 10.  PAIR: gate and up projections
+// Tiles per workgroup group: the first rem_t groups own base_t + 1 tiles, the
+// rest base_t (ntiles = base_t * NG + rem_t).  misc = sc_shift | RG << 8 |
+// pair_xcd << 10 | phases per tile << 16.  PAIR: gate and up projections
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
 template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR, bool P64>
 __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
-                                                             int pK, int pnblk, int pM, int pnbg, int pntiles,
+                                                             int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
                                                              int pNG, int pngrp, int misc, GemvArgs args) {
     GemvArgs a = args;
     if (FUSED) a.A = static_cast<const float*>(act);
     else a.Aq = static_cast<const uint8_t*>(act);
     a.W = pW;
     a.S = pS;
-    a.K = pK;
+    a.K = 32 * pnblk;
     a.nblk = pnblk;
     a.M = pM;
     a.nbg = pnbg;
-    a.ntiles = pntiles;
     a.NG = pNG;
     a.ngrp = pngrp;
     a.nblk4 = (pnblk + 3) / 4 * 4;
@@ -526,12 +527,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
+    const int base_t = pbase_t, rem_t = prem_t;
     const int t_begin = g * base_t + min(g, rem_t);
     const int nT = base_t + (g < rem_t ? 1 : 0);
     const int nbg = a.nbg;
-    const int npw = (nbg + kProducers - 1) / kProducers;  // phases per tile
-    const int U = nT * npw * (PAIR ? 2 : 1);               // phases of this workgroup
+    const int npw = misc >> 16;                // phases per tile: ceil(nbg / 15)
+    const int U = nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
 
     const DecLds lay = dec_lds(min(a.M, 4), a.nblk, JG, P64);
     uint8_t* recs = smem + lay.recs;
@@ -1699,8 +1700,10 @@ hipError_t launch_dec_t(Workspace& w, const GemvArgs& a, int grid, int lds, hipS
         w.attr_set[key] = true;
     }
     const void* act = FUSED ? static_cast<const void*>(a.A) : static_cast<const void*>(a.Aq);
-    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 10;
-    kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, a.K, a.nblk, a.M, a.nbg, a.ntiles, a.NG, a.ngrp, misc, a);
+    const int npw = (a.nbg + kProducers - 1) / kProducers;
+    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 10 | npw << 16;
+    const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
+    kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, base_t, a.nblk, a.M, a.nbg, rem_t, a.NG, a.ngrp, misc, a);
     return hipGetLastError();
 }
 
