@@ -340,6 +340,12 @@ __global__ __launch_bounds__(256) void wsum_kernel(const uint4* __restrict__ W, 
 constexpr int kDecWaves = 16;
 constexpr int kChainWave = kDecWaves - 1;
 constexpr int kProducers = kDecWaves - 1;
+// The quantizing prologue (8 lanes per 32-block) runs on the first eight
+// waves when two passes of 64 blocks cover the activations: the last waves
+// of a workgroup start up to ~0.3 us after the first, and the prologue
+// barrier waits for the slowest quantizer.  More blocks take all sixteen
+// waves (at most kQuantPasses passes of 128).
+constexpr int kQuantEarlyBlocks = 128, kQuantPasses = 4;
 
 struct GemvArgs {
     const uint4* W;
@@ -499,16 +505,20 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // 32-float blocks, and the staged scale and sum rows (pitch nblk4) are
     // contiguous too: a block index is an offset, with no row/column split.
     const int nb_rows = Mr * a.nblk;
-    uint4 av[4];
+    uint4 av[kQuantPasses];
     uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
     if (FUSED) {
-        const float* arow = a.A + (size_t)m0 * a.K + 4 * (tid & 7);
-        const int npass_ld = (nb_rows + 127) >> 7;
+        if (nb_rows > kQuantEarlyBlocks || wave < 8) {
+            const float* arow = a.A + (size_t)m0 * a.K + 4 * (tid & 7);
+            const bool all = nb_rows > kQuantEarlyBlocks;
+            const int qb = all ? 128 : 64;  // blocks per pass
+            const int npass_ld = all ? (nb_rows + 127) >> 7 : (nb_rows + 63) >> 6;
 #pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            if (p >= npass_ld) break;
-            const int blk = min(p * 128 + (tid >> 3), nb_rows - 1);
-            av[p] = *reinterpret_cast<const uint4*>(arow + 32 * blk);
+            for (int p = 0; p < kQuantPasses; ++p) {
+                if (p >= npass_ld) break;
+                const int blk = min(p * qb + (tid >> 3), nb_rows - 1);
+                av[p] = *reinterpret_cast<const uint4*>(arow + 32 * blk);
+            }
         }
     } else {
         // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
@@ -618,11 +628,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // this issue order.
     auto store_acts = [&]() {
         if (FUSED) {
-            const int npass = (nb_rows + 127) >> 7;
+            const bool all = nb_rows > kQuantEarlyBlocks;
+            const int qb = all ? 128 : 64;  // blocks per pass
+            const int npass = all ? (nb_rows + 127) >> 7 : wave < 8 ? (nb_rows + 63) >> 6 : 0;
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
+            for (int p = 0; p < kQuantPasses; ++p) {
                 if (p >= npass) break;
-                const int blk = p * 128 + (tid >> 3), e = tid & 7;
+                const int blk = p * qb + (tid >> 3), e = tid & 7;
                 float s;
                 int sum;
                 uint32_t p0, p1;
@@ -1677,7 +1689,7 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 }
 
 constexpr int kLdsMax = 160 * 1024;
-constexpr int kFusedMaxBlocks = 512;  // row-blocks the prologue quantizes (4 passes of 128)
+constexpr int kFusedMaxBlocks = 512;  // row-blocks the prologue quantizes (kQuantPasses passes of 128)
 
 // LDS bytes of the decode kernel, or 0 if the activation records of a row
 // group do not fit (in LDS, or in the prologue's 6-uint4-per-thread record
