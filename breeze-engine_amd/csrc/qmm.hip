@@ -128,14 +128,13 @@ __device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v,
 __device__ inline int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
 __device__ inline int dpp_mirror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
 
-// max over the 8 lanes of an aligned lane octet; inputs are never NaN.
-__device__ inline float max8(float x) {
-    float y = __int_as_float(dpp_xor1(__float_as_int(x)));
-    x = y > x ? y : x;
-    y = __int_as_float(dpp_xor2(__float_as_int(x)));
-    x = y > x ? y : x;
-    y = __int_as_float(dpp_mirror8(__float_as_int(x)));
-    return y > x ? y : x;
+// max over the 8 lanes of an aligned lane octet.  Inputs are +0 or more and
+// never NaN, so their bit patterns order as the floats do.
+__device__ inline float max8(float xf) {
+    int x = __float_as_int(xf);
+    x = max(x, dpp_xor1(x));
+    x = max(x, dpp_xor2(x));
+    return __int_as_float(max(x, dpp_mirror8(x)));
 }
 
 // min over each 16-lane row (row rotates by 1, 2, 4, 8).
@@ -159,12 +158,13 @@ __device__ inline int sum8(int x) {
 template <bool HP>
 __device__ inline void quant8(float4 v, float& s_out, int& sum_out, uint32_t& p0, uint32_t& p1) {
     const float x[4] = {v.x, v.y, v.z, v.w};
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float a = fabsf(x[i]);
-        amax = a > amax ? a : amax;
-    }
+    // amax over the block from +0 with NaNs skipped, as the reference's
+    // `a > amax ? a : amax` does.  fmaxf returns the other operand of a quiet
+    // NaN; canonicalizing first makes every NaN quiet, and the +0 operand
+    // keeps a lane whose values are all NaN at 0.
+    const float a0 = fabsf(__builtin_canonicalizef(x[0])), a1 = fabsf(__builtin_canonicalizef(x[1]));
+    const float a2 = fabsf(__builtin_canonicalizef(x[2])), a3 = fabsf(__builtin_canonicalizef(x[3]));
+    float amax = fmaxf(fmaxf(fmaxf(a0, a1), 0.0f), fmaxf(a2, a3));
     amax = max8(amax);
     constexpr int qmax = HP ? 32767 : 127;
     const float s = amax / (float)qmax;

@@ -299,3 +299,64 @@ def test_matmulnbits_operator_routes_to_the_gpu(gpu, hb, orc, hi_prec):
         assert bits_equal(out8[0].cpu().numpy(), orc.matmul(qw8, sc8, None, 32, 320, 8, a8, True))
     finally:
         ops.free_cache(cache)
+
+
+def _nan_aware_equal(a, b):
+    """NaN at the same places, bit-identical elsewhere.  A NaN output comes
+    from inf * 0 in the fold, and its sign and payload are the machine's:
+    x86 makes the negative default NaN, the GPU the positive one."""
+    a, b = np.asarray(a), np.asarray(b)
+    na, nb = np.isnan(a), np.isnan(b)
+    return a.shape == b.shape and np.array_equal(na, nb) and np.array_equal(a[~na].view(np.uint32), b[~nb].view(np.uint32))
+
+
+def _special_rows(rng, K):
+    """One N(0,1) row per pattern, the pattern planted in block 1 (k 32..63):
+    a quiet NaN, signaling NaNs, an all-NaN block, +inf, -inf, a block of
+    denormals, signed zeros only, values near the float maximum, and tiny
+    normals whose block scale is denormal (its reciprocal overflows)."""
+    snan = np.array([0x7F800001, 0xFFA00000, 0x7FBFFFFF], np.uint32).view(np.float32)
+    rows = []
+
+    def row():
+        return rng.normal(size=K).astype(np.float32)
+
+    r = row(); r[40] = np.nan; rows.append(r)
+    r = row(); r[33], r[50], r[63] = snan; rows.append(r)
+    r = row(); r[32:64] = np.nan; r[36:39] = snan; rows.append(r)
+    r = row(); r[45] = np.inf; rows.append(r)
+    r = row(); r[45] = -np.inf; rows.append(r)
+    r = row(); r[32:64] = (rng.uniform(-1, 1, 32) * 1e-39).astype(np.float32); rows.append(r)
+    r = row(); r[32:64] = 0.0; r[32:64:3] = -0.0; rows.append(r)
+    r = row(); r[32:64] = (rng.uniform(-1, 1, 32) * 3.4e38).astype(np.float32); rows.append(r)
+    r = row(); r[32:64] = (rng.uniform(-1, 1, 32) * 1e-34).astype(np.float32); rows.append(r)
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
+def test_non_finite_and_extreme_activations(gpu, hb, orc, hi_prec, bits, explicit_zeros):
+    """Activation blocks with NaNs (quiet and signaling: skipped by the block
+    max), infinities (the row becomes NaN), denormals, signed zeros, values
+    near the float maximum and tiny normals, through every quantizer: the
+    decode kernel's own (one row; 16 and 256 row-blocks), the stand-alone
+    decode quantizer (4 rows of K = 4608) and the records for M > 8 (all
+    nine rows at once).  Outputs match the oracle bit for bit outside NaNs."""
+    rng = np.random.default_rng(91 + bits)
+    N = 48
+    for K, groups in ((512, "single"), (8192, "single"), (4608, "four"), (512, "all")):
+        qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
+        h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+        try:
+            A = _special_rows(rng, K)
+            batches = {"single": [A[i:i + 1] for i in range(len(A))],
+                       "four": [A[0:4], A[4:8]],
+                       "all": [A]}[groups]
+            for hp in (False, True):
+                hb.set_hi_prec(hp)
+                for x in batches:
+                    want = orc.matmul(qw, sc, qz, N, K, bits, x, hp)
+                    c_host, c_dev = _run_both(hb, gpu, h, x, N)
+                    assert _nan_aware_equal(c_host, want), (K, groups, hp, x.shape)
+                    assert _nan_aware_equal(c_dev, want), (K, groups, hp, x.shape)
+        finally:
+            hb.free(h)
