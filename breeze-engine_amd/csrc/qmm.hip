@@ -212,6 +212,15 @@ __device__ inline v4i mfma16(uint64_t a, uint64_t b) {
 // block of a decode chunk's block pair and its last 8 bytes with the second
 // (the decode parity tests with one and two rows pin this pairing: any other
 // would change the exact block sums).
+// v_mfma_i32_32x32x32_i8 (full INT8 rate, one 32-block of k): A byte i of
+// lane l is row l & 31, k 16 * (l >> 5) + i; B byte i of lane l is k
+// 16 * (l >> 5) + i, column l & 31; result j of lane l is row
+// (j & 3) + 8 * (j >> 2) + 4 * (l >> 5), column l & 31.
+typedef int v16i __attribute__((ext_vector_type(16)));
+__device__ inline v16i mfma32(const v4i& a, const v4i& b, const v16i& c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
 __device__ inline v4i mfma64(const uint4& a, const uint4& b) {
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{(int)a.x, (int)a.y, (int)a.z, (int)a.w},
                                                    v4i{(int)b.x, (int)b.y, (int)b.z, (int)b.w},
@@ -1017,12 +1026,14 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
 
 // ------------------------------------------------------------------ prefill GEMM (M > 8, INT8 weights)
 //
-// One workgroup of 8 waves computes 128 rows x 16*CT columns over all of K;
-// wave w owns the 16-row tile w of the group and all CT column tiles.  Per
-// 32-block and tile, H = sum(h*b) comes from one v_mfma_i32_16x16x32_i8,
-// (H << 8) + 128*S is the accumulator input of the l-byte MFMA, which then
-// holds the exact block integer cs, and the lane folds
-// acc = fma(s_a, f32(cs) * s_b, acc) in block order.
+// One workgroup of 8 waves computes 128 rows x 16*CT columns over all of K.
+// Wave w owns rows 32 (w & 3) .. +31 and column half w >> 2 (the first
+// (CT+1)/2 tiles or the other CT/2), so each SIMD holds one wave of each
+// half.  Per 32-block, H = sum(h*b) comes from one MFMA, (H << 8) + 128*S is
+// the accumulator input of the l-byte MFMA, which then holds the exact block
+// integer cs, and the lane folds acc = fma(s_a, f32(cs) * s_b, acc) in block
+// order.  Pairs of tiles run on v_mfma_i32_32x32x32_i8, an odd last tile on
+// v_mfma_i32_16x16x32_i8.
 //
 // Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4,
 // 16 bytes per lane to LDS address M0 + 16*lane) through a ring of
@@ -1162,132 +1173,222 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
         }
     };
 
-    // The whole K loop of one column half: CTW tiles starting at WG tile toff.
-    auto run = [&](auto ctw_tag, int toff) {
+    // The whole K loop of one column half (CTW tiles from WG tile toff) on
+    // v_mfma_i32_32x32x32_i8: the wave's two 16-row records are its 32 rows
+    // and pairs of its tiles are 32-column groups, one MFMA per (group,
+    // 32-block) at the full INT8 rate (twice the 16x16x32 rate).  An odd
+    // last tile of the half takes 16x16x32 MFMAs on the 16-row records.
+    // Per (group, block) the h-byte MFMA's result, shifted left by 8 plus
+    // 128 * sum(b), is the l-byte MFMA's accumulator input, so that MFMA
+    // holds the exact block integer cs, and the lane folds
+    // acc = fma(s_a, f32(cs) * s_b, acc) in block order.
+    // Lane l: A row / output column c32 = l & 31, k half kh = l >> 5.  The
+    // operands come from the same LDS layout: a record's lane r + 16 * o
+    // holds k-octet o of row r, and a weight chunk's lane c + 16 * o holds
+    // k-octet o of column c for both blocks, so octets 2 kh and 2 kh + 1 are
+    // two 16-byte reads 256 bytes apart.
+    auto run32 = [&](auto ctw_tag, int toff) {
         constexpr int CTW = decltype(ctw_tag)::value;
-        // Per-column scales (SCM 0) are loaded and waited for before the
-        // first direct load, so no compiler wait inside the loop counts them.
-        float sbc[CTW];
+        constexpr int NG = CTW / 2;
+        constexpr bool ODD = (CTW & 1) != 0;
+        const int c32 = lane & 31, kh = lane >> 5;
+        float sbg[NG], sbo = 0.0f;
 #pragma unroll
-        for (int ct = 0; ct < CTW; ++ct) {
-            sbc[ct] = 0.0f;
+        for (int g = 0; g < NG; ++g) {
+            sbg[g] = 0.0f;
             if (SCM == 0) {
-                sbc[ct] = reinterpret_cast<const float*>(a.S)[(size_t)min(t0 + toff + ct, a.ntiles - 1) * a.ngrp * 16 + col];
-                asm volatile("" ::"v"(sbc[ct]));
+                const int t = min(t0 + toff + 2 * g + (c32 >> 4), a.ntiles - 1);
+                sbg[g] = reinterpret_cast<const float*>(a.S)[(size_t)t * a.ngrp * 16 + (c32 & 15)];
+                asm volatile("" ::"v"(sbg[g]));
             }
         }
-        float acc[2][CTW][4];
+        if (ODD && SCM == 0) {
+            sbo = reinterpret_cast<const float*>(a.S)[(size_t)min(t0 + toff + CTW - 1, a.ntiles - 1) * a.ngrp * 16 + col];
+            asm volatile("" ::"v"(sbo));
+        }
+        float acc[NG][16], acco[2][4];
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int ct = 0; ct < CTW; ++ct)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[r][ct][i] = 0.0f;
+            for (int i = 0; i < 4; ++i) acco[r][i] = 0.0f;
 
-        // One chunk (NB = 2 blocks, or 1 for the last chunk of an odd block
-        // count) from LDS region cp, software-pipelined over the CTW*NB
-        // (tile, block) steps: step s issues the h-byte MFMAs of step s+2,
-        // the shift-adds and l-byte MFMAs of step s+1 and the epilogue of
-        // step s, so every step carries four MFMAs per 32 VALU instructions
-        // and no instruction waits on the one just before it.  Tile
-        // operands are read from LDS kAhead tiles ahead; both row tiles
-        // share each weight operand.  With DMA, every other step also
-        // issues one of this wave's loads of chunk c_next into nbase, so
-        // the next stage streams in without a burst of loads.
         auto compute = [&](const char* cp, auto nb_tag, auto dma_tag, int c_next, uint32_t nbase) {
             constexpr int NB = decltype(nb_tag)::value;
             constexpr bool DMA = decltype(dma_tag)::value;
-            constexpr int kAhead = 5;
-            constexpr int NS = CTW * NB;
+            constexpr int kAhead = 1;            // groups read ahead
+            constexpr int NGB = NG * NB;         // group steps
+            constexpr int NS = NGB + (ODD ? NB : 0);
             const char* ar = cp + L::kA + 2 * rp * kRecBytes;
-            uint64_t ah[2][2], al[2][2];
-            float sa[2][2][4];
+            v4i a_h[2], a_l[2];
+            float sa[2][16];
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
+            for (int b = 0; b < NB; ++b) {
+                // Two 8-byte halves 256 bytes apart: one ds_read2_b64 into
+                // the operand's four registers.
+                const char* rb = ar + (c32 >> 4) * kRecBytes + b * 1024 + 16 * ((c32 & 15) + 32 * kh);
+                const uint2 h0 = *reinterpret_cast<const uint2*>(rb), h1 = *reinterpret_cast<const uint2*>(rb + 256);
+                const uint2 l0 = *reinterpret_cast<const uint2*>(rb + 8), l1 = *reinterpret_cast<const uint2*>(rb + 264);
+                a_h[b] = v4i{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y};
+                a_l[b] = v4i{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
 #pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    const uint4 q = *reinterpret_cast<const uint4*>(ar + r * kRecBytes + b * 1024 + 16 * lane);
-                    ah[r][b] = (uint64_t)q.y << 32 | q.x;
-                    al[r][b] = (uint64_t)q.w << 32 | q.z;
-                    const float4 s4 = *reinterpret_cast<const float4*>(ar + r * kRecBytes + kRecA + b * 64 + 16 * grp);
-                    sa[r][b][0] = s4.x;
-                    sa[r][b][1] = s4.y;
-                    sa[r][b][2] = s4.z;
-                    sa[r][b][3] = s4.w;
+                for (int q = 0; q < 4; ++q) {
+                    // rows 8q + 4kh .. +3: record (q >> 1), row 8 (q & 1) + 4 kh
+                    const float4 s4 = *reinterpret_cast<const float4*>(ar + (q >> 1) * kRecBytes + kRecA + b * 64 +
+                                                                       4 * (8 * (q & 1) + 4 * kh));
+                    sa[b][4 * q] = s4.x;
+                    sa[b][4 * q + 1] = s4.y;
+                    sa[b][4 * q + 2] = s4.z;
+                    sa[b][4 * q + 3] = s4.w;
                 }
-            uint4 bw[CTW];
-            int2 ws[CTW];
-            float sb[CTW][2];
-            auto load_tile = [&](int ct) {
-                if (ct >= CTW) return;
-                const int t = toff + ct;
-                bw[ct] = *reinterpret_cast<const uint4*>(cp + t * 1024 + 16 * lane);
-                if (HP) ws[ct] = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * col);
+            }
+            // The odd tile: 16x16x32 operands, as in the path above, read at
+            // the last group step (its registers are free by then).
+            uint64_t ah[2][2], al[2][2];
+            float so[2][2][4];
+            uint4 bwo = make_uint4(0, 0, 0, 0);
+            int2 wso = make_int2(0, 0);
+            float sbo2[2] = {0.0f, 0.0f};
+            auto load_odd = [&]() {
+                if (!ODD) return;
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const uint4 q = *reinterpret_cast<const uint4*>(ar + r * kRecBytes + b * 1024 + 16 * lane);
+                        ah[r][b] = (uint64_t)q.y << 32 | q.x;
+                        al[r][b] = (uint64_t)q.w << 32 | q.z;
+                        const float4 s4 = *reinterpret_cast<const float4*>(ar + r * kRecBytes + kRecA + b * 64 + 16 * grp);
+                        so[r][b][0] = s4.x;
+                        so[r][b][1] = s4.y;
+                        so[r][b][2] = s4.z;
+                        so[r][b][3] = s4.w;
+                    }
+                const int t = toff + CTW - 1;
+                bwo = *reinterpret_cast<const uint4*>(cp + t * 1024 + 16 * lane);
+                if (HP) wso = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * col);
                 if (SCM == 2) {
                     const float2 f = *reinterpret_cast<const float2*>(cp + L::kSB + t * 128 + 8 * col);
-                    sb[ct][0] = f.x;
-                    sb[ct][1] = f.y;
+                    sbo2[0] = f.x;
+                    sbo2[1] = f.y;
                 } else if (SCM == 1) {
-                    sb[ct][0] = sb[ct][1] = *reinterpret_cast<const float*>(cp + L::kSB + t * 64 + 4 * col);
+                    sbo2[0] = sbo2[1] = *reinterpret_cast<const float*>(cp + L::kSB + t * 64 + 4 * col);
                 } else {
-                    sb[ct][0] = sb[ct][1] = sbc[ct];
+                    sbo2[0] = sbo2[1] = sbo;
                 }
             };
-            auto bop = [&](int s) -> uint64_t {
-                const uint4& w4 = bw[s / NB];
-                return s % NB == 0 ? ((uint64_t)w4.y << 32 | w4.x) : ((uint64_t)w4.w << 32 | w4.z);
+            v4i bq[NG][2];  // B operand per group and block
+            int2 wsg[NG];
+            float sbv[NG][2];
+            auto load_group = [&](int g) {
+                if (g >= NG) return;
+                const int t = toff + 2 * g + (c32 >> 4);
+                const char* bp = cp + t * 1024 + 16 * ((c32 & 15) + 32 * kh);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const uint2 lo = *reinterpret_cast<const uint2*>(bp + 8 * b);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(bp + 256 + 8 * b);
+                    bq[g][b] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+                }
+                if (HP) wsg[g] = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * (c32 & 15));
+                if (SCM == 2) {
+                    const float2 f = *reinterpret_cast<const float2*>(cp + L::kSB + t * 128 + 8 * (c32 & 15));
+                    sbv[g][0] = f.x;
+                    sbv[g][1] = f.y;
+                } else if (SCM == 1) {
+                    sbv[g][0] = sbv[g][1] = *reinterpret_cast<const float*>(cp + L::kSB + t * 64 + 4 * (c32 & 15));
+                } else {
+                    sbv[g][0] = sbv[g][1] = sbg[g];
+                }
             };
-            v4i hh[NS][2], dd[NS][2];
+            auto bop32 = [&](int g, int b) -> v4i { return bq[g][b]; };
+            auto bopo = [&](int b) -> uint64_t {
+                return b == 0 ? ((uint64_t)bwo.y << 32 | bwo.x) : ((uint64_t)bwo.w << 32 | bwo.z);
+            };
+            v16i h32[NGB], d32[NGB];
+            v4i ho[2][2], dov[2][2];
+            const v16i z16 = {};
             auto step_h = [&](int s) {
                 if (!HP || s >= NS) return;
+                if (s < NGB) {
+                    h32[s] = mfma32(a_h[s % NB], bop32(s / NB, s % NB), z16);
+                } else {
+                    const int b = s - NGB;
 #pragma unroll
-                for (int r = 0; r < 2; ++r) hh[s][r] = mfma16(ah[r][s % NB], bop(s));
+                    for (int r = 0; r < 2; ++r) ho[b][r] = mfma16(ah[r][b], bopo(b));
+                }
             };
             auto step_d = [&](int s) {
                 if (s >= NS) return;
-                const int b = s % NB;
-#pragma unroll
-                for (int r = 0; r < 2; ++r) {
+                if (s < NGB) {
+                    const int g = s / NB, b = s % NB;
                     if (HP) {
-                        const int s128 = b == 0 ? ws[s / NB].x : ws[s / NB].y;
-                        const v4i ci = {(hh[s][r][0] << 8) + s128, (hh[s][r][1] << 8) + s128,
-                                        (hh[s][r][2] << 8) + s128, (hh[s][r][3] << 8) + s128};
-                        dd[s][r] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)al[r][b], (long)bop(s), ci, 0, 0, 0);
+                        const int s128 = b == 0 ? wsg[g].x : wsg[g].y;
+                        v16i ci;
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) ci[j] = (h32[s][j] << 8) + s128;
+                        d32[s] = mfma32(a_l[b], bop32(g, b), ci);
                     } else {
-                        dd[s][r] = mfma16(ah[r][b], bop(s));
+                        d32[s] = mfma32(a_h[b], bop32(g, b), z16);
+                    }
+                } else {
+                    const int b = s - NGB;
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        if (HP) {
+                            const int s128 = b == 0 ? wso.x : wso.y;
+                            const v4i ci = {(ho[b][r][0] << 8) + s128, (ho[b][r][1] << 8) + s128,
+                                            (ho[b][r][2] << 8) + s128, (ho[b][r][3] << 8) + s128};
+                            dov[b][r] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)al[r][b], (long)bopo(b), ci, 0, 0, 0);
+                        } else {
+                            dov[b][r] = mfma16(ah[r][b], bopo(b));
+                        }
                     }
                 }
             };
             auto step_e = [&](int s) {
-                const int ct = s / NB, b = s % NB;
+                if (s < NGB) {
+                    const int g = s / NB, b = s % NB;
 #pragma unroll
-                for (int r = 0; r < 2; ++r)
+                    for (int j = 0; j < 16; ++j)
+                        acc[g][j] = __builtin_fmaf(sa[b][j], (float)d32[s][j] * sbv[g][b], acc[g][j]);
+                } else {
+                    const int b = s - NGB;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[r][ct][i] = __builtin_fmaf(sa[r][b][i], (float)dd[s][r][i] * sb[ct][b], acc[r][ct][i]);
+                    for (int r = 0; r < 2; ++r)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acco[r][i] = __builtin_fmaf(so[r][b][i], (float)dov[b][r][i] * sbo2[b], acco[r][i]);
+                }
             };
+            // Depth-1 pipeline (registers: 16 accumulators per group): step
+            // s issues step s+1's h-byte MFMA, runs its own epilogue, which
+            // covers that MFMA's latency, then step s+1's shift-add and
+            // l-byte MFMA.
 #pragma unroll
-            for (int t = 0; t < kAhead; ++t) load_tile(t);
+            for (int g = 0; g < kAhead; ++g) load_group(g);
+            if (NGB == 0) load_odd();
             step_h(0);
-            step_h(1);
             step_d(0);
 #pragma unroll
             for (int s = 0; s < NS; ++s) {
-                if (s % NB == 0) load_tile(s / NB + kAhead);
-                if (DMA && s % 2 == 0 && s / 2 < kDmaChunk) dma_slot(c_next, nbase, s / 2);
-                step_h(s + 2);
-                step_d(s + 1);
+                if (s < NGB && s % NB == 0) load_group(s / NB + kAhead);
+                if (s == NGB - 1) load_odd();
+                if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s);
+                step_h(s + 1);
                 step_e(s);
+                step_d(s + 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (DMA) {
 #pragma unroll
-                for (int d = (NS + 1) / 2; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d);
+                for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d);
             }
         };
 
-        // Every stage but the last holds kPfChunks full chunks, so the main
-        // loop body is straight-line and the accumulators stay in place.
         static_assert(kPfChunks == 2, "stage loop");
         constexpr std::integral_constant<int, 2> two{};
         constexpr std::integral_constant<int, 1> one{};
@@ -1295,10 +1396,6 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
         constexpr std::false_type no_dma{};
         issue_stage(0, 0);
         for (int g = 0; g + 1 < nst; ++g) {
-            // Stage g's loads (issued during stage g-1) have landed; the
-            // barrier publishes them and retires stage g-1's buffer, which
-            // stage g+1's loads then fill.  A missing last chunk of stage
-            // g+1 reloads chunk nch-1 into a region that is never read.
             __builtin_amdgcn_s_waitcnt(vm_wait(0));
             lds_barrier();
             const uint32_t nbase = lds0 + (uint32_t)(((g + 1) & 1) * L::kStage);
@@ -1328,20 +1425,30 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
             }
         }
 #pragma unroll
-        for (int r = 0; r < 2; ++r)
+        for (int g = 0; g < NG; ++g) {
+            const int tile = t0 + toff + 2 * g + (c32 >> 4);
+            if (tile >= a.ntiles) continue;
 #pragma unroll
-            for (int ct = 0; ct < CTW; ++ct) {
-                const int tile = t0 + toff + ct;
-                if (tile >= a.ntiles) continue;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int m = (rt0 + r) * 16 + 4 * grp + i;
-                    if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + col] = acc[r][ct][i];
-                }
+            for (int j = 0; j < 16; ++j) {
+                const int m = rt0 * 16 + (j & 3) + 8 * (j >> 2) + 4 * kh;
+                if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + (c32 & 15)] = acc[g][j];
             }
+        }
+        if (ODD) {
+            const int tile = t0 + toff + CTW - 1;
+            if (tile < a.ntiles) {
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int m = (rt0 + r) * 16 + 4 * grp + i;
+                        if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + col] = acco[r][i];
+                    }
+            }
+        }
     };
-    if (half == 0) run(std::integral_constant<int, (CT + 1) / 2>{}, 0);
-    else run(std::integral_constant<int, CT / 2>{}, (CT + 1) / 2);
+    if (half == 0) run32(std::integral_constant<int, (CT + 1) / 2>{}, 0);
+    else run32(std::integral_constant<int, CT / 2>{}, (CT + 1) / 2);
 }
 
 // Activation records for the prefill GEMM: 8 lanes per (row, block) over
@@ -1689,7 +1796,7 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 }
 
 constexpr int kLdsMax = 160 * 1024;
-constexpr int kFusedMaxBlocks = 512;  // row-blocks the prologue quantizes (kQuantPasses passes of 128)
+constexpr int kFusedMaxBlocks = kQuantPasses * 128;  // row-blocks the prologue quantizes
 
 // LDS bytes of the decode kernel, or 0 if the activation records of a row
 // group do not fit (in LDS, or in the prologue's 6-uint4-per-thread record
