@@ -137,14 +137,6 @@ __device__ inline float max8(float xf) {
     return __int_as_float(max(x, dpp_mirror8(x)));
 }
 
-// min over each 16-lane row (row rotates by 1, 2, 4, 8).
-__device__ inline int min16(int x) {
-    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x121, 0xF, 0xF, false));
-    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x122, 0xF, 0xF, false));
-    x = min(x, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
-    return min(x, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
-}
-
 __device__ inline int sum8(int x) {
     x += dpp_xor1(x);
     x += dpp_xor2(x);
@@ -895,7 +887,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     const uint2 alo = *reinterpret_cast<const uint2*>(ap);
                     const uint2 ahi = *reinterpret_cast<const uint2*>(ap + 8);
                     const v4i dd = mfma64(make_uint4(alo.x, alo.y, ahi.x, ahi.y), bop);
-                    const int jb = 2 * mi + o_sel;
                     int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
                     if (BITS == 4) {
                         const int nsq = mi == 0 ? nsq2.x : nsq2.y;
