@@ -874,6 +874,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     const int* q = sq_l + o_row * lay.sa_pitch + c * 4 + o_sel;
                     nsq2 = make_int2(q[0], q[2]);
                 }
+                float fo[JG / 2];
 #pragma unroll
                 for (int mi = 0; mi < JG / 2; ++mi) {
                     // Blocks past nblk (last chunk) read padding; the chain
@@ -902,8 +903,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                         cs += (HP ? 256 : 1) * (o_sel ? dl1 : dl0);
                         sc = o_sel ? sc1 : sc0;
                     }
-                    p_fout[buf * 64 * PP + 2 * mi] = (float)cs * sc;
+                    fo[mi] = (float)cs * sc;
                 }
+                // Both results in one LDS instruction (ds_write2_b32): the
+                // phase is bounded by LDS instruction issue, ~8 CU cycles each.
+#pragma unroll
+                for (int mi = 0; mi < JG / 2; ++mi) p_fout[buf * 64 * PP + 2 * mi] = fo[mi];
             } else if (!P64 && c < nbg) {
                 const Unit<JG, EXTRA>& cur = ring[d];
                 const int abase = is_data ? data_base + c * JG * 64 : const_base;
