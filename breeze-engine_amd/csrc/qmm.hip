@@ -432,7 +432,9 @@ __host__ __device__ inline int lds_take(int& off, int bytes) {
 // multiple of 256 B.
 __host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG, bool p64 = false) {
     DecLds l;
-    l.rec_pitch = p64 ? nblk * 128 + 16 : nblk * 64;
+    // The 16x16x32 layout stores whole chunks ([h, l][k-octet][block]), so a
+    // row spans every chunk, padding blocks included.
+    l.rec_pitch = p64 ? nblk * 128 + 16 : (nblk + JG - 1) / JG * JG * 64;
     l.sa_pitch = (nblk + 3) / 4 * 4;
     if (Mr_max > 1) {
         l.rec_pitch = p64 ? (l.rec_pitch + 223) / 256 * 256 + 32 : (l.rec_pitch + 191) / 256 * 256 + 64;
@@ -654,9 +656,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                         sh[16] = 0u;  // l octets, 64 B further
                         sh[18] = p1;
                     } else {
-                        uint8_t* rec = recs + m * lay.rec_pitch + j * 64;
-                        *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
-                        *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
+                        // [chunk][h, l][k-octet][block of the chunk] of 8
+                        // bytes: a lane's A operands for a chunk are 8 JG
+                        // contiguous bytes.
+                        uint8_t* rec = recs + m * lay.rec_pitch + (j / JG) * (JG * 64) + (e >> 1) * (JG * 8) +
+                                       (j % JG) * 8 + 4 * (e & 1);
+                        *reinterpret_cast<uint32_t*>(rec) = p0;
+                        *reinterpret_cast<uint32_t*>(rec + JG * 32) = p1;
                     }
                     if (e == 0) {
                         sa_l[m * lay.sa_pitch + j] = s;
@@ -668,9 +674,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             // Unconditional stores: threads past the end rewrite the last
             // element with the value they loaded from it.  Rows land at the
             // padded LDS pitches.
-            uint4* dst = reinterpret_cast<uint4*>(recs);
             const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
-            const int L = a.nblk * 4, gap = (lay.rec_pitch >> 4) - L;
+            const int L = a.nblk * 4;
             auto put = [&](int i, const uint4& v) {
                 i = min(i, nrec - 1);
                 const int m = (i >= L) + (i >= 2 * L) + (i >= 3 * L);
@@ -683,7 +688,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     slot[0] = make_uint4(0u, 0u, v.x, v.y);
                     slot[1] = make_uint4(0u, 0u, v.z, v.w);
                 } else {
-                    dst[i + m * gap] = v;
+                    // Source uint4 q of a block: h or l (q >> 1) octets
+                    // 2(q & 1) and 2(q & 1) + 1, each to its place in the
+                    // [chunk][h, l][k-octet][block] layout.
+                    const int r = i - m * L, j = r >> 2, q = r & 3;
+                    uint8_t* o = recs + m * lay.rec_pitch + (j / JG) * (JG * 64) + (q >> 1) * (JG * 32) +
+                                 2 * (q & 1) * (JG * 8) + (j % JG) * 8;
+                    *reinterpret_cast<uint2*>(o) = make_uint2(v.x, v.y);
+                    *reinterpret_cast<uint2*>(o + JG * 8) = make_uint2(v.z, v.w);
                 }
             };
             put(tid, r0);
@@ -847,8 +859,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // for explicit zero points, -8 * sum(q) for the default zero point 8.
     const int arow = lane & 15, arg = arow >> 2, ars = arow & 3, kq = lane >> 4;
     const bool is_data = ars < 2 && arg < Mr;
-    const int data_base = lay.recs + arg * lay.rec_pitch + ars * 32 + kq * 8;
-    const int const_base = lay.consts + ((ars >= 2 && arg < Mr) ? 0 : 256) + kq * 8;
+    const int data_base = lay.recs + arg * lay.rec_pitch + ars * (JG * 32) + kq * (JG * 8);
+    const int const_base = lay.consts + ((ars >= 2 && arg < Mr) ? 0 : 256) + kq * (JG * 8);
     // P64: A row r = 8 * activation row + 4 * (block of the pair) + slot,
     // read as 16 bytes from the zero-padded octet slots ([octet | zeros] for
     // the pair's first block, [zeros | octet] for its second).  Output lane
@@ -912,6 +924,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             } else if (!P64 && c < nbg) {
                 const Unit<JG, EXTRA>& cur = ring[d];
                 const int abase = is_data ? data_base + c * JG * 64 : const_base;
+                // The chunk's JG A operands of this lane: 8 JG contiguous bytes.
+                uint4 av4[JG / 2];
+#pragma unroll
+                for (int h = 0; h < JG / 2; ++h) av4[h] = *reinterpret_cast<const uint4*>(smem + abase + 16 * h);
                 int4 sqv = make_int4(0, 0, 0, 0);
                 if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * lay.sa_pitch + c * 4);
                 fvec fo;
@@ -920,7 +936,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     // Blocks past nblk (last chunk) read padding; the chain
                     // never folds them.
                     const uint64_t bop = unpack_b(cur.w, jb, BITS);
-                    const uint64_t aop = *reinterpret_cast<const uint64_t*>(smem + abase + jb * 64);
+                    const uint4& a2 = av4[jb >> 1];
+                    const uint64_t aop = (jb & 1) ? ((uint64_t)a2.w << 32 | a2.z) : ((uint64_t)a2.y << 32 | a2.x);
                     const v4i dd = mfma16(aop, bop);
                     int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
                     if (BITS == 4) {
