@@ -90,7 +90,9 @@ def test_decode_with_staged_activation_records(gpu, hb, orc, hi_prec, bits, expl
     more rows; K = 17408 with one row), beside a shape quantized inside the
     decode kernel (2 rows), in both activation modes, bit-exact."""
     rng = np.random.default_rng(11 + bits)
-    for K, rows_list in ((4608, (2, 4, 5, 8)), (17408, (1,))):
+    # K = 4640: 145 blocks, a partial last chunk of the records (1 of 4 or
+    # 1 of 2 blocks); 3 rows quantize inside the kernel, 4 and 8 stage.
+    for K, rows_list in ((4608, (2, 4, 5, 8)), (4640, (3, 4, 8)), (17408, (1,))):
         N = 64
         qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
         h = hb.prepack(qw, sc, qz, K, N, bits=bits)
