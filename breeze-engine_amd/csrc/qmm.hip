@@ -528,12 +528,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         // scale and sum(q) rows as uint4 (Mr * nblk4 / 4 each).
         const uint4* rsrc = reinterpret_cast<const uint4*>(a.Aq + (size_t)m0 * a.nblk * 64);
         const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+        // With one or two rows (block pairs) only the groups of 1024
+        // records that hold work are loaded; with more rows every group is
+        // (branches there cost more than the clamped loads).
         r0 = rsrc[min(tid, nrec - 1)];
         r1 = rsrc[min(1024 + tid, nrec - 1)];
         r2 = rsrc[min(2048 + tid, nrec - 1)];
-        r3 = rsrc[min(3072 + tid, nrec - 1)];
-        r4 = rsrc[min(4096 + tid, nrec - 1)];
-        r5 = rsrc[min(5120 + tid, nrec - 1)];
+        if (!P64 || nrec > 3072) {
+            r3 = rsrc[min(3072 + tid, nrec - 1)];
+            r4 = rsrc[min(4096 + tid, nrec - 1)];
+            r5 = rsrc[min(5120 + tid, nrec - 1)];
+        }
         const int mi = min(tid, nmeta - 1);
         rsa = *reinterpret_cast<const uint4*>(a.Sa + (size_t)m0 * a.nblk4 + 4 * mi);
         rsq = *reinterpret_cast<const uint4*>(a.Sq + (size_t)m0 * a.nblk4 + 4 * mi);
@@ -671,9 +676,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 }
             }
         } else {
-            // Unconditional stores: threads past the end rewrite the last
-            // element with the value they loaded from it.  Rows land at the
-            // padded LDS pitches.
+            // Rows land at the padded LDS pitches.
             const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
             const int L = a.nblk * 4;
             auto put = [&](int i, const uint4& v) {
@@ -698,12 +701,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     *reinterpret_cast<uint2*>(o + JG * 8) = make_uint2(v.z, v.w);
                 }
             };
+            // Threads past the end rewrite the last element with the value
+            // they loaded from it; with block pairs, groups of 1024 records
+            // without work are skipped (up to 3072 such stores to one LDS
+            // address otherwise).
             put(tid, r0);
             put(1024 + tid, r1);
             put(2048 + tid, r2);
-            put(3072 + tid, r3);
-            put(4096 + tid, r4);
-            put(5120 + tid, r5);
+            if (!P64 || nrec > 3072) {
+                put(3072 + tid, r3);
+                put(4096 + tid, r4);
+                put(5120 + tid, r5);
+            }
             const int mi = min(tid, nmeta - 1);
             const int mm = (4 * mi >= a.nblk4) + (4 * mi >= 2 * a.nblk4) + (4 * mi >= 3 * a.nblk4);
             const int md = mi + mm * ((lay.sa_pitch - a.nblk4) >> 2);
