@@ -145,7 +145,8 @@ def main():
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", default=None,
-                    help="time only this workload (w8_gemv, w4_gemv, w4_decode:ROWS, w8_lmhead, w8_prefill)")
+                    help="time only this workload (w8_gemv, w4_gemv, w4_decode:ROWS, w8_lmhead, w8_prefill, "
+                         "w4_prefill)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 elementwise copy 5 times (counter calibration)")
     args = ap.parse_args()
@@ -182,7 +183,7 @@ def main():
         rows = int(r) if r else None
         t, m = time_workload(hb, torch, name, rows, args.steps, args.warmup, argmax=name == "w8_lmhead")
         entry = {"workload": workloads.LABELS[name].format(M=m), "steps": args.steps, "us": round(t * 1e6, 3)}
-        if name == "w8_prefill":
+        if name.endswith("prefill"):
             tops = workloads.algorithmic_ops(name, m) / t / 1e12
             entry.update(tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
         else:
@@ -238,16 +239,17 @@ def main():
     if not args.headline_only:
         rows = []
         # The decode workloads take about 10 us a call: same steps and warmup
-        # as the headline.  The LM head and the prefill GEMM take 140-250 us:
+        # as the headline.  The LM head and the prefill GEMMs take 140-300 us:
         # fewer steps keep the run short.
         for name, r in (("w8_gemv", None), ("w4_gemv", None), ("w4_decode", 1), ("w4_decode", 2),
-                        ("w4_decode", 4), ("w4_decode", 8), ("w8_lmhead", None), ("w8_prefill", None)):
-            long_call = name in ("w8_lmhead", "w8_prefill")
+                        ("w4_decode", 4), ("w4_decode", 8), ("w8_lmhead", None), ("w8_prefill", None),
+                        ("w4_prefill", None)):
+            long_call = name in ("w8_lmhead", "w8_prefill", "w4_prefill")
             t, m = time_workload(hb, torch, name, r, max(10, args.steps // 4) if long_call else args.steps,
                                  max(3, args.warmup // 4) if long_call else args.warmup,
                                  argmax=name == "w8_lmhead")
             entry = {"workload": workloads.LABELS[name].format(M=m), "us": round(t * 1e6, 2)}
-            if name == "w8_prefill":
+            if name.endswith("prefill"):
                 tops = workloads.algorithmic_ops(name, m) / t / 1e12
                 entry.update(tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
             else:

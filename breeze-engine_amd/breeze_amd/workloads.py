@@ -1,4 +1,5 @@
-"""Seeded synthetic inputs of the five benchmark workloads.
+"""Seeded synthetic inputs of the five benchmark workloads (and a W4
+prefill of the same shape as the W8 one).
 
 MatMulNBits weights and activations drawn exactly as the benchmark
 specification prescribes (one ``numpy.random.default_rng(seed)`` stream per
@@ -15,6 +16,8 @@ CONFIGS = {
     "w4_decode": (4, 8, 12288, 4096, 4, 3, True),
     "w8_prefill": (8, 512, 5120, 17408, None, 4, False),
     "w8_lmhead": (8, 1, 5120, 151936, None, 5, False),
+    # Not a benchmark workload: the W4 counterpart of the prefill GEMM.
+    "w4_prefill": (4, 512, 5120, 17408, 4, 6, False),
 }
 
 LABELS = {
@@ -23,6 +26,7 @@ LABELS = {
     "w4_decode": "W4 decode M={M} K=12288 N=4096, group-128 scales, 1% x20 outliers",
     "w8_prefill": "W8 prefill M=512 K=5120 N=17408, per-channel scales",
     "w8_lmhead": "W8 LM head M=1 K=5120 N=151936 + argmax, per-channel scales",
+    "w4_prefill": "W4 prefill M=512 K=5120 N=17408, group-128 scales",
 }
 
 

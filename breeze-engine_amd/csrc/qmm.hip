@@ -1046,7 +1046,7 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
     if (!DOTS && cm < Mc) a.C[(size_t)(m0 + cm) * a.N + t * 16 + ccol] = acc;
 }
 
-// ------------------------------------------------------------------ prefill GEMM (M > 8, INT8 weights)
+// ------------------------------------------------------------------ prefill GEMM (M > 8)
 //
 // One workgroup of 8 waves computes 128 rows x 16*CT columns over all of K.
 // Wave w owns rows 32 (w & 3) .. +31 and column half w >> 2 (the first
@@ -1065,6 +1065,15 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
 // wave's activation record.  The compiler does not see these loads: every
 // wave waits for its own with an explicit vmcnt, then the workgroup barrier
 // publishes the stage.
+//
+// INT4 weights (BITS 4) take the same core.  A stage is one INT4 chunk (four
+// blocks, 1 KB per tile), loaded raw into chunk 0's weight area; its scales
+// and zero points go to one raw area shared by both stages.  After the
+// stage barrier all 512 threads expand it in place: per byte, b = nibble -
+// zp as a signed byte ((n | 0x80) - zp) ^ 0x80, chunk 0 getting blocks 0-1
+// and chunk 1 blocks 2-3 in the INT8 chunk layout, plus 128 * sum(b) per
+// (column, block) for the two-pass product and the scales in the INT8
+// chunk layout.  A second barrier publishes the expanded stage.
 
 constexpr int kPfWaves = 8, kPfRows = 16 * kPfWaves;
 // Ring of kPfStages stages of kPfChunks chunks each.
@@ -1075,18 +1084,22 @@ constexpr int kPfStages = 2, kPfChunks = 2;
 constexpr int kRecA = 2048, kRecBytes = kRecA + 128;
 
 struct PfArgs {
-    const char* W;   // [ntiles][nch][64 lanes][16 B]
-    const char* WS;  // [ntiles][nch][16][2] int32
+    const char* W;   // INT8: [ntiles][nch][64 lanes][16 B]; INT4: [ntiles][nbg][64][16 B]
+    const char* WS;  // INT8: [ntiles][nch][16][2] int32
     const char* S;   // scales (grp_index / blk_index layouts)
+    const char* Z;   // INT4 per-block zero points [ntiles][nbg][16][4] (SCM 2 only)
     const char* R;   // activation records [Mpad/16][nch][kRecBytes]
     float* C;        // [M][N]
     int M, N, nblk, nch, ngrp, sc_shift, ntiles;
+    int nbg;         // INT4: 4-block chunks per tile
 };
 
 // SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
 // One chunk's LDS region: [CT weight tiles, 1 KB each][weight sums, 128 B
-// per tile][block or group scales][8 activation records].
-template <int CT, int SCM>
+// per tile][block or group scales][8 activation records].  INT4 adds the raw
+// area after the two stages: group scales (SCM 1, 64 B per tile) or block
+// scales then zero points (SCM 2, 256 + 64 B per tile), in whole KB.
+template <int CT, int SCM, int BITS>
 struct PfLayout {
     static constexpr int kWS = CT * 1024;
     static constexpr int kSB = kWS + CT * 128;
@@ -1094,9 +1107,15 @@ struct PfLayout {
     static constexpr int kA = kShared;
     static constexpr int kChunk = kA + kPfWaves * kRecBytes;
     static constexpr int kStage = kPfChunks * kChunk;
-    static constexpr int kUnits = (kShared + 1023) / 1024;
+    static constexpr int kRawZ = CT * 256;  // SCM 2: zero points after the block scales
+    static constexpr int kRawUsed = BITS == 8 ? 0 : SCM == 2 ? CT * 320 : SCM == 1 ? CT * 64 : 0;
+    static constexpr int kRaw = (kRawUsed + 1023) / 1024 * 1024;
+    static constexpr int kRawOff = kPfStages * kStage;
+    // DMA units of 1 KB per stage (INT8: per chunk): INT8 the chunk's shared
+    // part, INT4 the CT raw tiles and the raw area.
+    static constexpr int kUnits = BITS == 8 ? (kShared + 1023) / 1024 : CT + kRaw / 1024;
     static constexpr int kPerWave = (kUnits + kPfWaves - 1) / kPfWaves;
-    static constexpr int kBytes = kPfStages * kStage;
+    static constexpr int kBytes = kRawOff + kRaw;
     static_assert(kShared % 64 == 0 && kBytes <= 160 * 1024, "layout");
 };
 
@@ -1112,9 +1131,9 @@ __device__ inline void dma16(const void* src, uint32_t lds) {
 // s_waitcnt immediate: vmcnt(n), no wait on the other counters.
 __host__ __device__ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
 
-template <bool HP, int SCM, int CT>
-__global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
-    using L = PfLayout<CT, SCM>;
+template <int BITS, bool HP, int SCM, int CT>
+__global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
+    using L = PfLayout<CT, SCM, BITS>;
     extern __shared__ __align__(16) char pf_lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1130,11 +1149,14 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
     const int nst = (nch + kPfChunks - 1) / kPfChunks;
     const bool odd = a.nblk & 1;
 
-    // Shared part of a chunk: slot k of this wave loads the 1 KB at
-    // x0 = min(u * 1024, kShared - 1024), u = k * kPfWaves + wave (clamped),
-    // lane bytes x0 + 16*lane.  Overlapping slots write equal bytes.
+    // Shared part of a chunk (INT8) or stage (INT4): slot k of this wave
+    // loads the 1 KB at x0, u = k * kPfWaves + wave (clamped), lane bytes
+    // x0 + 16*lane.  INT8: x0 = min(u * 1024, kShared - 1024) in the chunk
+    // (overlapping slots write equal bytes).  INT4: raw tile u of the stage
+    // into chunk 0's weight area, or KB u - CT of the raw area.
     const char* src0[L::kPerWave];
     uint32_t step[L::kPerWave], gstep[L::kPerWave], x0s[L::kPerWave];
+    bool to_raw[L::kPerWave];
 #pragma unroll
     for (int k = 0; k < L::kPerWave; ++k) {
         const int u = min(k * kPfWaves + wave, L::kUnits - 1);
@@ -1142,7 +1164,35 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
         const int x = x0 + 16 * lane;
         x0s[k] = (uint32_t)x0;
         gstep[k] = 0;
-        if (x < L::kWS) {
+        to_raw[k] = false;
+        if (BITS == 4) {
+            if (u < CT) {
+                const int tc = min(t0 + u, a.ntiles - 1);
+                src0[k] = a.W + (size_t)tc * a.nbg * 1024 + 16 * lane;
+                step[k] = 1024;
+                x0s[k] = (uint32_t)(u * 1024);
+            } else {
+                const int y = (u - CT) * 1024 + 16 * lane;
+                to_raw[k] = true;
+                x0s[k] = (uint32_t)(L::kRawOff + (u - CT) * 1024);
+                src0[k] = a.S;  // padding lanes: any valid source
+                step[k] = 0;
+                if (SCM == 2 && y < L::kRawZ) {
+                    const int tc = min(t0 + (y >> 8), a.ntiles - 1);
+                    src0[k] = a.S + (size_t)tc * a.nbg * 256 + (y & 255);
+                    step[k] = 256;
+                } else if (SCM == 2 && y < L::kRawUsed) {
+                    const int yz = y - L::kRawZ;
+                    const int tc = min(t0 + (yz >> 6), a.ntiles - 1);
+                    src0[k] = a.Z + (size_t)tc * a.nbg * 64 + (yz & 63);
+                    step[k] = 64;
+                } else if (SCM == 1 && y < L::kRawUsed) {
+                    const int tc = min(t0 + (y >> 6), a.ntiles - 1);
+                    src0[k] = a.S + (size_t)tc * a.ngrp * 64 + (y & 63);
+                    gstep[k] = 64;
+                }
+            }
+        } else if (x < L::kWS) {
             const int tc = min(t0 + (x >> 10), a.ntiles - 1);
             src0[k] = a.W + (size_t)tc * nch * 1024 + (x & 1023);
             step[k] = 1024;
@@ -1171,10 +1221,17 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
     // Load d of this wave's kDmaChunk loads of chunk c into the chunk region
     // at LDS address cbase: the shared slots, then 3 per activation record.
     constexpr int kDmaChunk = L::kPerWave + 6;
-    auto dma_slot = [&](int c, uint32_t cbase, int d) {
+    // INT4: only chunk 0 of a stage (first) carries the stage's shared loads.
+    auto dma_slot = [&](int c, uint32_t cbase, int d, bool first) {
         if (d < L::kPerWave) {
-            const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
-            dma16(src0[d] + (size_t)c * step[d] + g * gstep[d], cbase + x0s[d]);
+            if (BITS == 8) {
+                const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
+                dma16(src0[d] + (size_t)c * step[d] + g * gstep[d], cbase + x0s[d]);
+            } else if (first) {
+                const int sg = c >> 1;
+                const size_t g = SCM == 1 ? (size_t)((4 * sg) >> a.sc_shift) : 0;
+                dma16(src0[d] + (size_t)sg * step[d] + g * gstep[d], (to_raw[d] ? lds0 : cbase) + x0s[d]);
+            }
         } else {
             const int e = d - L::kPerWave, r = e / 3, part = e % 3;
             const int off = part == 0 ? 0 : part == 1 ? 1024 : 1152;
@@ -1182,16 +1239,71 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
                   cbase + (uint32_t)(L::kA + (2 * rp + r) * kRecBytes + off));
         }
     };
-    auto issue_chunk = [&](int c, uint32_t cbase) {
+    auto issue_chunk = [&](int c, uint32_t cbase, bool first) {
 #pragma unroll
-        for (int d = 0; d < kDmaChunk; ++d) dma_slot(c, cbase, d);
+        for (int d = 0; d < kDmaChunk; ++d) dma_slot(c, cbase, d, first);
     };
     auto issue_stage = [&](int g, int buf) {
         const uint32_t sbase = lds0 + (uint32_t)(buf * L::kStage);
 #pragma unroll
         for (int cc = 0; cc < kPfChunks; ++cc) {
             const int c = g * kPfChunks + cc;
-            if (c < nch) issue_chunk(c, sbase + (uint32_t)(cc * L::kChunk));
+            if (c < nch) issue_chunk(c, sbase + (uint32_t)(cc * L::kChunk), cc == 0);
+        }
+    };
+
+    // INT4: expands stage buffer buf in place (all threads; a workgroup
+    // barrier must follow).  Wave w takes tiles w, w + 8, ...; lane l holds
+    // weight lane l of the tile (column l & 15, k-octet l >> 4), so the LDS
+    // reads and writes are linear.  The nibble sums of a column's four
+    // octets (one per 16-lane row) meet by row swaps.
+    auto expand = [&](int buf) {
+        if constexpr (BITS == 4) {
+            char* sb = pf_lds + buf * L::kStage;
+            const char* raw = pf_lds + L::kRawOff;
+            const int c = lane & 15, o = lane >> 4, cc = o & 1;
+            for (int t = wave; t < CT; t += kPfWaves) {
+                const int wl = t * 1024 + 16 * lane;
+                const uint4 w = *reinterpret_cast<const uint4*>(sb + wl);
+                const uint32_t z = SCM == 2 ? *reinterpret_cast<const uint32_t*>(raw + L::kRawZ + t * 64 + 4 * c)
+                                            : 0x08080808u;
+                const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+                uint32_t lo[4], hi[4], nsum[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t zr = SCM == 2 ? ((z >> (8 * b)) & 0xFFu) * 0x01010101u : 0x08080808u;
+                    lo[b] = (((wv[b] & 0x0F0F0F0Fu) | 0x80808080u) - zr) ^ 0x80808080u;
+                    hi[b] = ((((wv[b] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - zr) ^ 0x80808080u;
+                    nsum[b] = __builtin_amdgcn_udot8(wv[b], 0x11111111u, 0u, false);  // <= 120
+                }
+                *reinterpret_cast<uint4*>(sb + wl) = make_uint4(lo[0], hi[0], lo[1], hi[1]);
+                *reinterpret_cast<uint4*>(sb + L::kChunk + wl) = make_uint4(lo[2], hi[2], lo[3], hi[3]);
+                // Per-column nibble sums of blocks (0, 1) and (2, 3), two per
+                // dword, summed over the four rows (octets).
+                uint32_t ps[2] = {nsum[0] | nsum[1] << 16, nsum[2] | nsum[3] << 16};
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const auto s32 = __builtin_amdgcn_permlane32_swap(ps[q], ps[q], false, false);
+                    const uint32_t y = s32[0] + s32[1];
+                    const auto s16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
+                    ps[q] = s16[0] + s16[1];
+                }
+                char* cb = sb + cc * L::kChunk;
+                if (o < 2) {
+                    // Row o: 128 * sum(n - zp) of chunk o's two blocks.
+                    const uint32_t p2 = cc ? ps[1] : ps[0];
+                    const uint32_t zz = SCM == 2 ? z >> (16 * cc) : 0x0808u;
+                    const int s0 = (int)(p2 & 0xFFFFu) - 32 * (int)(zz & 0xFFu);
+                    const int s1 = (int)(p2 >> 16) - 32 * (int)((zz >> 8) & 0xFFu);
+                    *reinterpret_cast<int2*>(cb + L::kWS + t * 128 + 8 * c) = make_int2(128 * s0, 128 * s1);
+                } else if (SCM == 2) {
+                    *reinterpret_cast<float2*>(cb + L::kSB + t * 128 + 8 * c) =
+                        *reinterpret_cast<const float2*>(raw + t * 256 + 16 * c + 8 * cc);
+                } else if (SCM == 1) {
+                    *reinterpret_cast<float*>(cb + L::kSB + t * 64 + 4 * c) =
+                        *reinterpret_cast<const float*>(raw + t * 64 + 4 * c);
+                }
+            }
         }
     };
 
@@ -1238,9 +1350,12 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acco[r][i] = 0.0f;
 
+        // dma_tag: 0 no loads, 1 or 2 the loads of chunk 0 or 1 of the next
+        // stage (c_next, at LDS nbase).
         auto compute = [&](const char* cp, auto nb_tag, auto dma_tag, int c_next, uint32_t nbase) {
             constexpr int NB = decltype(nb_tag)::value;
-            constexpr bool DMA = decltype(dma_tag)::value;
+            constexpr bool DMA = decltype(dma_tag)::value != 0;
+            constexpr bool FIRST = decltype(dma_tag)::value == 1;
             constexpr int kAhead = 1;            // groups read ahead
             constexpr int NGB = NG * NB;         // group steps
             constexpr int NS = NGB + (ODD ? NB : 0);
@@ -1399,7 +1514,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
             for (int s = 0; s < NS; ++s) {
                 if (s < NGB && s % NB == 0) load_group(s / NB + kAhead);
                 if (s == NGB - 1) load_odd();
-                if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s);
+                if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s, FIRST);
                 step_h(s + 1);
                 step_e(s);
                 step_d(s + 1);
@@ -1407,31 +1522,40 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_w8_kernel(PfArgs a) {
             }
             if (DMA) {
 #pragma unroll
-                for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d);
+                for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d, FIRST);
             }
         };
 
         static_assert(kPfChunks == 2, "stage loop");
         constexpr std::integral_constant<int, 2> two{};
         constexpr std::integral_constant<int, 1> one{};
-        constexpr std::true_type dma{};
-        constexpr std::false_type no_dma{};
+        constexpr std::integral_constant<int, 1> dma0{};
+        constexpr std::integral_constant<int, 2> dma1{};
+        constexpr std::integral_constant<int, 0> no_dma{};
         issue_stage(0, 0);
         for (int g = 0; g + 1 < nst; ++g) {
             __builtin_amdgcn_s_waitcnt(vm_wait(0));
             lds_barrier();
+            if (BITS == 4) {
+                expand(g & 1);
+                lds_barrier();
+            }
             const uint32_t nbase = lds0 + (uint32_t)(((g + 1) & 1) * L::kStage);
             const int cn = (g + 1) * kPfChunks;
             if (active) {
                 const char* sp = pf_lds + (g & 1) * L::kStage;
-                compute(sp, two, dma, cn, nbase);
-                compute(sp + L::kChunk, two, dma, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk);
+                compute(sp, two, dma0, cn, nbase);
+                compute(sp + L::kChunk, two, dma1, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk);
             } else {
                 issue_stage(g + 1, (g + 1) & 1);
             }
         }
         __builtin_amdgcn_s_waitcnt(vm_wait(0));
         lds_barrier();
+        if (BITS == 4) {
+            expand((nst - 1) & 1);
+            lds_barrier();
+        }
         if (!active) return;
         {
             const char* sp = pf_lds + ((nst - 1) & 1) * L::kStage;
@@ -1878,13 +2002,13 @@ hipError_t launch_rows_bits(const GemvArgs& a, dim3 grid, bool dots, hipStream_t
     return hipGetLastError();
 }
 
-template <bool HP, int SCM, int CT>
+template <int BITS, bool HP, int SCM, int CT>
 hipError_t launch_pf_t(Workspace& w, const PfArgs& p, dim3 grid, hipStream_t st) {
-    using L = PfLayout<CT, SCM>;
-    auto kern = prefill_w8_kernel<HP, SCM, CT>;
+    using L = PfLayout<CT, SCM, BITS>;
+    auto kern = prefill_kernel<BITS, HP, SCM, CT>;
     int slot = 0;
     while (kPfCts[slot] != CT) ++slot;
-    const int key = (HP ? 1 : 0) | SCM << 1 | slot << 3;
+    const int key = (HP ? 1 : 0) | SCM << 1 | slot << 3 | (BITS == 4 ? 32 : 0);
     if (!w.pf_attr[key]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
@@ -1895,21 +2019,21 @@ hipError_t launch_pf_t(Workspace& w, const PfArgs& p, dim3 grid, hipStream_t st)
     return hipGetLastError();
 }
 
-template <bool HP, int SCM>
+template <int BITS, bool HP, int SCM>
 hipError_t launch_pf_scm(Workspace& w, const PfArgs& p, int ct, dim3 grid, hipStream_t st) {
     switch (ct) {
-        case 17: return launch_pf_t<HP, SCM, 17>(w, p, grid, st);
-        case 16: return launch_pf_t<HP, SCM, 16>(w, p, grid, st);
-        case 8: return launch_pf_t<HP, SCM, 8>(w, p, grid, st);
-        default: return launch_pf_t<HP, SCM, 4>(w, p, grid, st);
+        case 17: return launch_pf_t<BITS, HP, SCM, 17>(w, p, grid, st);
+        case 16: return launch_pf_t<BITS, HP, SCM, 16>(w, p, grid, st);
+        case 8: return launch_pf_t<BITS, HP, SCM, 8>(w, p, grid, st);
+        default: return launch_pf_t<BITS, HP, SCM, 4>(w, p, grid, st);
     }
 }
 
-template <bool HP>
+template <int BITS, bool HP>
 hipError_t launch_pf(Workspace& w, const PfArgs& p, int scm, int ct, dim3 grid, hipStream_t st) {
-    if (scm == 2) return launch_pf_scm<HP, 2>(w, p, ct, grid, st);
-    if (scm == 1) return launch_pf_scm<HP, 1>(w, p, ct, grid, st);
-    return launch_pf_scm<HP, 0>(w, p, ct, grid, st);
+    if (scm == 2) return launch_pf_scm<BITS, HP, 2>(w, p, ct, grid, st);
+    if (scm == 1) return launch_pf_scm<BITS, HP, 1>(w, p, ct, grid, st);
+    return launch_pf_scm<BITS, HP, 0>(w, p, ct, grid, st);
 }
 
 int device_cus(Workspace& w, int dev) {
@@ -1987,16 +2111,17 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
     const bool dec = lds > 0;
     if (h2 && !dec) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
-    // Prefill GEMM: more than 8 rows of INT8 weights without a legacy corr.
-    const bool pre = !dec && !dots && M > 8 && h->bits == 8 && h->WS && !h->has_dl;
+    // Prefill GEMM: more than 8 rows without a legacy corr.
+    const bool pre = !dec && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
     const int Mpad = (M + kPfRows - 1) / kPfRows * kPfRows;
+    const int nch_rec = (h->nblk + 1) / 2;  // record chunks of two blocks
     if (pre) {
         // Records in MFMA operand order for the prefill GEMM.
-        if (!grow(&w.rec, &w.rec_cap, (size_t)(Mpad / 16) * h->nbg * kRecBytes, "workspace alloc")) return -4;
-        const size_t threads = (size_t)Mpad * h->nbg * 2 * 8;
+        if (!grow(&w.rec, &w.rec_cap, (size_t)(Mpad / 16) * nch_rec * kRecBytes, "workspace alloc")) return -4;
+        const size_t threads = (size_t)Mpad * nch_rec * 2 * 8;
         const unsigned qb = (unsigned)((threads + 255) / 256);
-        if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nbg, Mpad, w.rec);
-        else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nbg, Mpad, w.rec);
+        if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, w.rec);
+        else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, w.rec);
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
     } else if (!fused) {
         if (!ensure_quant(w, M, h->nblk4)) return -4;
@@ -2055,20 +2180,27 @@ int run(Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dId
         p.W = reinterpret_cast<const char*>(h->W);
         p.WS = reinterpret_cast<const char*>(h->WS);
         p.S = reinterpret_cast<const char*>(h->S);
+        p.Z = reinterpret_cast<const char*>(h->Z);
         p.R = reinterpret_cast<const char*>(w.rec);
         p.C = dC;
         p.M = M;
         p.N = h->N;
         p.nblk = h->nblk;
-        p.nch = h->nbg;
+        p.nch = nch_rec;
         p.ngrp = h->ngrp;
         p.sc_shift = h->sc_shift;
         p.ntiles = h->N / 16;
+        p.nbg = h->nbg;
         const int scm = h->sc_blk ? 2 : (h->sc_shift == 31 ? 0 : 1);
+        if (h->bits == 4 && scm == 2 && !h->Z) {
+            set_err("internal: INT4 handle with per-block scales has no zero points");
+            return -5;
+        }
         const int gy = Mpad / kPfRows;
         const int ct = pick_pf_ct(p.ntiles, gy, device_cus(w, dev), std::getenv("BREEZE_HIP_PREFILL_CT"));
         const dim3 grid((unsigned)((p.ntiles + ct - 1) / ct), (unsigned)gy);
-        e = hp ? launch_pf<true>(w, p, scm, ct, grid, st) : launch_pf<false>(w, p, scm, ct, grid, st);
+        if (h->bits == 8) e = hp ? launch_pf<8, true>(w, p, scm, ct, grid, st) : launch_pf<8, false>(w, p, scm, ct, grid, st);
+        else e = hp ? launch_pf<4, true>(w, p, scm, ct, grid, st) : launch_pf<4, false>(w, p, scm, ct, grid, st);
         e = hipGetLastError();
     } else {
         const dim3 grid(a.ntiles, (M + kRowsPerWG - 1) / kRowsPerWG);

@@ -271,6 +271,45 @@ def test_prefill_gemm_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
         hb.free(h)
 
 
+@pytest.mark.parametrize("scales", ["channel", "group4", "group8", "block", "zeros"])
+@pytest.mark.parametrize("ct", ["auto", "17", "16", "8", "4"])
+def test_prefill_gemm_int4_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
+    """The M > 8 GEMM on INT4 weights (nibbles expanded to signed bytes
+    n - zp in LDS) against the oracle: per-column scales, groups of one and
+    two 4-block chunks, per-block scales (default zero point 8) and explicit
+    zero points 0..15; every column-tile width with a partial last column
+    group (19 tiles); 33 and 35 blocks, so the last 4-block chunk holds one
+    or three blocks."""
+    if ct != "auto":
+        monkeypatch.setenv("BREEZE_HIP_PREFILL_CT", ct)
+    N = 304
+    rng = np.random.default_rng(12)
+    for K in (1056, 1120):
+        qw, sc, qz = rng_weights(rng, N, K, 4, explicit_zeros=scales == "zeros")
+        nblk = K // 32
+        if scales == "channel":
+            sc = np.repeat(sc[:, :1], nblk, axis=1)
+        elif scales.startswith("group"):
+            g = int(scales[5:])
+            sc = np.repeat(sc[:, ::g], g, axis=1)[:, :nblk]
+        sc = np.ascontiguousarray(sc)
+        h = hb.prepack(qw, sc, qz, K, N, bits=4)
+        try:
+            info = hb.handle_info(h)
+            assert info["scale_group"] == {"channel": 0, "group4": 4, "group8": 8, "block": 1, "zeros": 1}[scales], info
+            for hp in (True, False):
+                hb.set_hi_prec(hp)
+                for rows in (9, 130, 300):
+                    A = rng.normal(size=(rows, K)).astype(np.float32)
+                    A[rng.random(A.shape) < 0.01] *= 20.0
+                    want = orc.matmul(qw, sc, qz, N, K, 4, A, hp)
+                    got = hb.matmul(h, gpu.from_numpy(A).cuda(), N)
+                    gpu.cuda.synchronize()
+                    assert bits_equal(got.cpu().numpy(), want), (K, hp, rows)
+        finally:
+            hb.free(h)
+
+
 def test_matmulnbits_operator_routes_to_the_gpu(gpu, hb, orc, hi_prec):
     """breeze_amd.ops with the real backend: the session cache prepacks an
     INT4 node with explicit zeros and an INT8 node, and the operator body

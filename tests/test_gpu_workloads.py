@@ -64,16 +64,17 @@ def test_lm_head_logits_and_argmax(gpu, hb, orc, hi_prec):
     assert idx.tolist() == np.argmax(want, axis=1).tolist()
 
 
-def test_prefill_rows_bit_exact(gpu, hb, orc, hi_prec):
+@pytest.mark.parametrize("name", ["w8_prefill", "w4_prefill"])
+def test_prefill_rows_bit_exact(gpu, hb, orc, hi_prec, name):
     from oracle import oracle
-    d = oracle.make_config("w8_prefill")
-    N, K = d["N"], d["K"]
+    d = oracle.make_config(name)
+    N, K, bits = d["N"], d["K"], d["bits"]
     hb.set_hi_prec(True)
-    h = hb.prepack(d["qweight"], d["scales"], None, K, N, bits=8)
+    h = hb.prepack(d["qweight"], d["scales"], None, K, N, bits=bits)
     try:
         got = _device_matmul(hb, gpu, h, d["A"], N)
     finally:
         hb.free(h)
     rows = [0, 1, 127, 128, 300, 511]
-    want = orc.matmul(d["qweight"], d["scales"], None, N, K, 8, d["A"][rows], True)
+    want = orc.matmul(d["qweight"], d["scales"], None, N, K, bits, d["A"][rows], True)
     assert bits_equal(got[rows], want)
