@@ -84,6 +84,8 @@ try:
     _lib.i4_handle_info.argtypes = [_vp, _vp]
     _lib.i4_unpack.restype = _i
     _lib.i4_unpack.argtypes = [_vp, _vp, _vp, _vp, _vp]
+    _lib.i4_rmsnorm_dev.restype = _i
+    _lib.i4_rmsnorm_dev.argtypes = [_vp, _vp, _i, _i, ctypes.c_float, _vp, _vp]
 except (OSError, AttributeError):
     _lib = None
 
@@ -285,6 +287,28 @@ def matmul_silu_mul(gate, up, a2d, N):
     out = torch.empty((M, N), dtype=torch.float32, device=a.device)
     _check_rc(_lib.i4_matmul_silu_mul_dev(_vp(gate), _vp(up), _vp(a.data_ptr()), int(M), _vp(out.data_ptr()),
                                           _torch_stream(a)), "i4_matmul_silu_mul_dev")
+    return out
+
+
+def rmsnorm(x2d, w, eps):
+    """GPU torch tensors x [s, H], w [H] -> fp32 [s, H]: the decoder's RMSNorm
+    (kernel/qwen35_decoder.cpp:134-140) bit for bit, asynchronous on the
+    current stream.  Its output is the activation of the projections that
+    follow (input_ln / post_ln ahead of qkv, gate/up)."""
+    _require_lib()
+    import torch
+    x = x2d.to(torch.float32).contiguous()
+    if x.dim() != 2:
+        raise ValueError(f"x must be 2-D [s, H], got shape {tuple(x.shape)}")
+    s, H = x.shape
+    wv = w.to(device=x.device, dtype=torch.float32).contiguous()
+    if wv.numel() != H:
+        raise ValueError(f"w has {wv.numel()} elements, x rows have {H}")
+    out = torch.empty_like(x)
+    if s == 0:
+        return out
+    _check_rc(_lib.i4_rmsnorm_dev(_vp(x.data_ptr()), _vp(wv.data_ptr()), int(s), int(H), float(eps),
+                                  _vp(out.data_ptr()), _torch_stream(x)), "i4_rmsnorm_dev")
     return out
 
 

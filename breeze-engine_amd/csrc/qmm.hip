@@ -1649,6 +1649,225 @@ int pick_pf_ct(int ntiles, int gy, int n_cu, const char* force) {
     return best;
 }
 
+// ------------------------------------------------------------------ RMSNorm
+//
+// The decoder's RMSNorm (kernel/qwen35_decoder.cpp:134-140), bit-identical:
+// ss = sum of (double)x*x in element order, inv = 1/sqrtf((float)(ss/H) +
+// eps), out = (x*inv)*w.  The sum is rebuilt exactly in parallel.  While the
+// running sum s stays in one binade [2^e, 2^(e+1)), every partial sum is a
+// multiple of u = 2^(e-52) and fl(s + t) = s + u*round(t/u), so such an
+// element adds the integer k = round(t/u) whatever s is.  An element is
+// "special" when that does not hold or is not certain: the first nonzero term
+// (s = 0), a step that leaves the binade, an estimated partial sum within a
+// relative 2^-20 of a power of two (exact specials), or an exact tie
+// (t/u = n + 1/2, rounded to the even neighbour of s/u).  The estimates are a
+// parallel prefix sum, within ~H*2^-53 (relative) of the true partial sums.
+// A tie leaves s/u even, so a tie whose previous special is a tie adds
+// X + (X & 1), X = (the k since that tie) + floor(t/u), whatever s is.  Only
+// the "anchors" -- exact specials and the first tie after each -- need the
+// running sum: one wave walks them in order, with everything between two
+// anchors summed in parallel beforehand.  Rows with more than kNormMaxSpecial
+// specials are summed by one thread in element order.
+constexpr int kNormThreads = 256;
+constexpr int kNormMaxSpecial = 1024;
+constexpr int kNormStage = 8192;  // rows up to this width are staged in LDS
+constexpr double kNormBand = 0x1p-20;
+
+__device__ inline int ilogb_pos(double v) { return __builtin_amdgcn_frexp_exp(v) - 1; }
+
+// v > 0 within a relative kNormBand of a power of two (either side).
+__device__ inline bool near_pow2(double v) {
+    const double m = __builtin_amdgcn_frexp_mant(v);  // [0.5, 1)
+    return m < 0.5 * (1.0 + kNormBand) || m > 1.0 - kNormBand;
+}
+
+__device__ inline long long readlane64(long long v, int l) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)v, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)((unsigned long long)v >> 32), l);
+    return (long long)((unsigned long long)hi << 32 | lo);
+}
+
+template <typename T>
+__device__ inline T block_exclusive_scan(T v, T* wsum, T* total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    T inc = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const T o = __shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) wsum[wave] = inc;
+    __syncthreads();
+    T base = 0, all = 0;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) {
+        if (i < wave) base += wsum[i];
+        all += wsum[i];
+    }
+    *total = all;
+    __syncthreads();
+    return base + inc - v;
+}
+
+// 0 simple (k set), 1 exact special, 2 tie (k = floor(t/u)).
+__device__ inline int norm_classify(double P, double t, unsigned long long* k) {
+    *k = 0;
+    if (t == 0.0) return 0;
+    const double Q = P + t;
+    if (P == 0.0 || near_pow2(P) || near_pow2(Q)) return 1;
+    const int e = ilogb_pos(P);
+    if (ilogb_pos(Q) != e) return 1;
+    const double f = __builtin_ldexp(t, 52 - e);  // < 2^53: t < 2^(e+1)
+    const double fl = __builtin_floor(f);
+    *k = (unsigned long long)fl;
+    const double fr = f - fl;
+    if (fr == 0.5) return 2;
+    if (fr > 0.5) *k += 1;
+    return 0;
+}
+
+template <bool STAGED>
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ X, const float* __restrict__ Wt,
+                                                                int H, float eps, float* __restrict__ Out) {
+    extern __shared__ float norm_row[];                      // STAGED: the row
+    __shared__ double spec[kNormMaxSpecial];                 // t, or -(floor(t/u) + 1) for a tie
+    __shared__ unsigned long long seg[kNormMaxSpecial + 1];  // sum of k with q specials before
+    __shared__ unsigned long long gap[kNormMaxSpecial];      // non-anchor ties after anchor a
+    __shared__ int alist[kNormMaxSpecial];                   // special index of anchor a
+    __shared__ double wsum_d[kNormThreads / 64];
+    __shared__ int wsum_i[kNormThreads / 64];
+    __shared__ double ss_s;
+    const float* xg = X + (size_t)blockIdx.x * H;
+    float* o = Out + (size_t)blockIdx.x * H;
+    const int tid = threadIdx.x;
+    if (STAGED) {
+#pragma unroll 4
+        for (int j = tid; j < H; j += kNormThreads) norm_row[j] = xg[j];
+        __syncthreads();
+    }
+    const float* x = STAGED ? norm_row : xg;
+    const int per = (H + kNormThreads - 1) / kNormThreads;
+    const int j0 = min(tid * per, H), j1 = min(j0 + per, H);
+
+    double loc = 0.0;
+    int nan = 0, inf = 0;
+    for (int j = j0; j < j1; ++j) {
+        const double t = (double)x[j] * (double)x[j];
+        nan |= t != t;
+        inf |= t == __builtin_inf();
+        loc += t;
+    }
+    const int any_nan = __syncthreads_or(nan), any_inf = __syncthreads_or(inf);
+    if (any_nan || any_inf) {
+        if (tid == 0) ss_s = any_nan ? __builtin_nan("") : __builtin_inf();
+    } else {
+        double tot_d;
+        const double base = block_exclusive_scan<double>(loc, wsum_d, &tot_d);
+        int cnt = 0;
+        {
+            double P = base;
+            for (int j = j0; j < j1; ++j) {
+                const double t = (double)x[j] * (double)x[j];
+                unsigned long long k;
+                cnt += norm_classify(P, t, &k) != 0;
+                P += t;
+            }
+        }
+        int nspec;
+        const int sbase = block_exclusive_scan<int>(cnt, wsum_i, &nspec);
+        if (nspec <= kNormMaxSpecial) {
+            for (int q = tid; q <= nspec; q += kNormThreads) seg[q] = 0;
+            __syncthreads();
+            {
+                double P = base;
+                int q = sbase;  // specials before element j
+                unsigned long long run = 0;
+                for (int j = j0; j < j1; ++j) {
+                    const double t = (double)x[j] * (double)x[j];
+                    unsigned long long k;
+                    const int c = norm_classify(P, t, &k);
+                    P += t;
+                    if (c == 0) {
+                        run += k;
+                        continue;
+                    }
+                    if (run) atomicAdd(&seg[q], run);
+                    run = 0;
+                    spec[q++] = c == 1 ? t : -((double)k + 1.0);
+                }
+                if (run) atomicAdd(&seg[q], run);
+            }
+            __syncthreads();
+            // Anchors: special 0 (always exact: the first nonzero term),
+            // every exact special, and every tie after an exact special.
+            const int sper = (nspec + kNormThreads - 1) / kNormThreads;
+            const int i0 = min(tid * sper, nspec), i1 = min(i0 + sper, nspec);
+            int acnt = 0;
+            for (int i = i0; i < i1; ++i) acnt += i == 0 || spec[i] >= 0.0 || spec[i - 1] >= 0.0;
+            int nanch;
+            const int abase = block_exclusive_scan<int>(acnt, wsum_i, &nanch);
+            for (int q = tid; q < nanch; q += kNormThreads) gap[q] = 0;
+            __syncthreads();
+            {
+                int a = abase - 1;  // anchor at or before special i
+                unsigned long long run = 0;
+                for (int i = i0; i < i1; ++i) {
+                    if (i == 0 || spec[i] >= 0.0 || spec[i - 1] >= 0.0) {
+                        if (run) atomicAdd(&gap[a], run);
+                        run = 0;
+                        alist[++a] = i;
+                    } else {
+                        const unsigned long long xq = seg[i] + (unsigned long long)(-spec[i]) - 1ull;
+                        run += xq + (xq & 1ull);
+                    }
+                }
+                if (run) atomicAdd(&gap[a], run);
+            }
+            __syncthreads();
+            if (tid < 64) {
+                // The walk, on all lanes of wave 0 alike: sd between binades,
+                // S in units of 2^(e-52) within one.
+                double sd = 0.0;
+                long long S = 0;
+                int e = 0;
+                for (int a0 = 0; a0 < nanch; a0 += 64) {
+                    long long sg = 0, gp = 0;
+                    double v = 0.0;
+                    if (a0 + tid < nanch) {
+                        const int i = alist[a0 + tid];
+                        sg = (long long)seg[i];
+                        v = spec[i];
+                        gp = (long long)gap[a0 + tid];
+                    }
+                    const int n = min(64, nanch - a0);
+                    for (int l = 0; l < n; ++l) {
+                        const double vl = __builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), l));
+                        S += readlane64(sg, l);
+                        if (vl < 0.0) {
+                            S = (S + (long long)(-vl)) & ~1LL;  // -vl = floor(t/u) + 1
+                        } else {
+                            sd = __builtin_ldexp((double)S, e - 52) + vl;
+                            e = ilogb_pos(sd);
+                            S = (long long)__builtin_ldexp(sd, 52 - e);
+                        }
+                        S += readlane64(gp, l);
+                    }
+                }
+                S += (long long)seg[nspec];
+                if (tid == 0) ss_s = nspec ? __builtin_ldexp((double)S, e - 52) : 0.0;
+            }
+        } else if (tid == 0) {
+            double acc = 0.0;
+            for (int j = 0; j < H; ++j) acc += (double)x[j] * (double)x[j];
+            ss_s = acc;
+        }
+    }
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((float)(ss_s / (double)H) + eps);
+#pragma unroll 4
+    for (int j = tid; j < H; j += kNormThreads) o[j] = x[j] * inv * Wt[j];
+}
+
 // ------------------------------------------------------------------ argmax
 
 __device__ inline unsigned long long block_max_key(unsigned long long k) {
@@ -2570,6 +2789,24 @@ int i4_unpack(void* handle, uint8_t* qw, float* scales, uint8_t* zp, int32_t* co
         }
     }
     return 0;
+}
+
+int i4_rmsnorm_dev(const float* dX, const float* dW, int M, int H, float eps, float* dOut, void* stream) {
+    if (M < 0 || H <= 0) {
+        set_err("need M >= 0 and H > 0 (got M %d, H %d)", M, H);
+        return -1;
+    }
+    if (M == 0) return 0;
+    if (!dX || !dW || !dOut) {
+        set_err("null device pointer");
+        return -2;
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (H <= kNormStage)
+        rmsnorm_kernel<true><<<(unsigned)M, kNormThreads, (size_t)H * sizeof(float), st>>>(dX, dW, H, eps, dOut);
+    else
+        rmsnorm_kernel<false><<<(unsigned)M, kNormThreads, 0, st>>>(dX, dW, H, eps, dOut);
+    return hip_ok(hipGetLastError(), "rmsnorm launch") ? 0 : -3;
 }
 
 }  // extern "C"

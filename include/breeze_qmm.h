@@ -117,6 +117,14 @@ int i4_unpack(void* handle, uint8_t* qw, float* scales, uint8_t* zp, int32_t* co
  * epilogue: dCs int32 [M, N, K/32].  Same kernels as i4_matmul_dev. */
 int i4_block_dots_dev(void* handle, const float* dA, int M, int32_t* dCs, void* stream);
 
+/* The decoder's RMSNorm (kernel/qwen35_decoder.cpp:134-140, an internal
+ * function there, called ahead of the projections at 279, 405 and 420) on
+ * device pointers: dOut[m, :] = (dX[m, :] * inv) * dW with
+ * inv = 1 / sqrtf((float)(ss / H) + eps) and ss the double sum of squares
+ * in element order, bit-identical to the reference's.  Asynchronous on
+ * `stream`.  Returns 0, or a negative code with i4_last_error() set. */
+int i4_rmsnorm_dev(const float* dX, const float* dW, int M, int H, float eps, float* dOut, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,6 +9,8 @@ does.  It holds:
 * a NumPy twin of the same arithmetic (``quantize_np``, ``block_dots_np``,
   ``chain_np``, ``matmul_np``), written independently and cross-checked with
   the C restatement, fast enough for mid-sized parity cases;
+* ``rmsnorm`` / ``sumsq``: the decoder's RMSNorm (qwen35_decoder.cpp:134-140),
+  whose double sum of squares runs strictly in element order;
 * ``dequantize_matmul_nbits``: the float MatMulNBits decode
   (breeze/quant.py:9-58) used by the reference's own accuracy tests;
 * ``make_config``: seeded MatMulNBits inputs for the five benchmark
@@ -50,6 +52,8 @@ class _COracle:
         lib.orc_chain.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp]
         lib.orc_matmul_nbits.argtypes = [_vp, _vp, _vp] + [_i] * 4 + [_vp, _i, _i, _vp, _vp]
         lib.orc_matmul_legacy.argtypes = [_vp] * 4 + [_i] * 4 + [_vp, _i, _i, _vp]
+        lib.orc_rmsnorm.argtypes = [_vp, _vp, _i, _i, ctypes.c_float, _vp]
+        lib.orc_sumsq.argtypes = [_vp, _i, _i, _vp]
         self.lib = lib
 
     def half_to_float(self, h):
@@ -146,6 +150,23 @@ class _COracle:
         if rc:
             raise ValueError(f"oracle legacy matmul failed ({rc})")
         return C
+
+    def rmsnorm(self, x, w, eps):
+        """The decoder's RMSNorm (qwen35_decoder.cpp:134-140) of x [s, H]."""
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        s, H = x.shape
+        out = np.empty_like(x)
+        self.lib.orc_rmsnorm(_p(x), _p(w), s, H, float(eps), _p(out))
+        return out
+
+    def sumsq(self, x):
+        """Per-row sequential double sum of squares (qwen35_decoder.cpp:137)."""
+        x = np.ascontiguousarray(x, np.float32)
+        s, H = x.shape
+        out = np.empty(s, np.float64)
+        self.lib.orc_sumsq(_p(x), s, H, _p(out))
+        return out
 
 
 _C = None

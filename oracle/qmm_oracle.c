@@ -12,6 +12,7 @@
  *   kernel/quantized_matmul.cpp   packing, activation quantizers, tile kernels
  *   breeze/quant.py               MatMulNBits dequant contract (zero points)
  *   breeze/cpu_backend.py         prepack validation and the legacy layout
+ *   kernel/qwen35_decoder.cpp     the decoder's RMSNorm ahead of the projections
  *
  * Build: see oracle/Makefile (-ffp-contract=off, no fast-math), so each
  * float operation below rounds exactly once, as written.
@@ -289,4 +290,30 @@ ORC_API int orc_matmul_legacy(const uint8_t* B, const float* scale, const int8_t
     free(sb);
     free(delta);
     return rc;
+}
+
+/* RMSNorm of the decoder (qwen35_decoder.cpp:134-140): per row, the sum of
+ * squares is accumulated in double, one element after the other from j = 0;
+ * inv = 1 / sqrtf((float)(ss / H) + eps) in float (correctly rounded divide
+ * and square root); out = (x * inv) * w, two float roundings. */
+ORC_API void orc_rmsnorm(const float* x, const float* w, int s, int H, float eps, float* out) {
+    for (int i = 0; i < s; ++i) {
+        const float* xr = x + (size_t)i * H;
+        float* o = out + (size_t)i * H;
+        double ss = 0;
+        for (int j = 0; j < H; ++j) ss += (double)xr[j] * xr[j];
+        const float inv = 1.0f / sqrtf((float)(ss / H) + eps);
+        for (int j = 0; j < H; ++j) o[j] = xr[j] * inv * w[j];
+    }
+}
+
+/* The double sum of squares alone (the first line of the row loop above),
+ * for tests of the sum's exactness. */
+ORC_API void orc_sumsq(const float* x, int s, int H, double* ss_out) {
+    for (int i = 0; i < s; ++i) {
+        const float* xr = x + (size_t)i * H;
+        double ss = 0;
+        for (int j = 0; j < H; ++j) ss += (double)xr[j] * xr[j];
+        ss_out[i] = ss;
+    }
 }
