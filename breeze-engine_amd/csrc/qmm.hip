@@ -1667,10 +1667,13 @@ int pick_pf_ct(int ntiles, int gy, int n_cu, const char* force) {
 // the "anchors" -- exact specials and the first tie after each -- need the
 // running sum: one wave walks them in order, with everything between two
 // anchors summed in parallel beforehand.  Rows with more than kNormMaxSpecial
-// specials are summed by one thread in element order.
-constexpr int kNormThreads = 256;
+// specials are summed by one thread in element order.  Rows up to kNormStage
+// wide are staged in LDS and each thread holds its (at most kNormPer) terms
+// and their classes in registers; wider rows are read from memory per pass.
+constexpr int kNormThreads = 1024;
 constexpr int kNormMaxSpecial = 1024;
-constexpr int kNormStage = 8192;  // rows up to this width are staged in LDS
+constexpr int kNormStage = 8192;
+constexpr int kNormPer = kNormStage / kNormThreads;
 constexpr double kNormBand = 0x1p-20;
 
 __device__ inline int ilogb_pos(double v) { return __builtin_amdgcn_frexp_exp(v) - 1; }
@@ -1749,13 +1752,30 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
     const int per = (H + kNormThreads - 1) / kNormThreads;
     const int j0 = min(tid * per, H), j1 = min(j0 + per, H);
 
+    // STAGED: this thread's terms (0 past its range) and, after the
+    // classification, their k and which of them are specials / ties.
+    double tv[STAGED ? kNormPer : 1];
+    unsigned long long kv[STAGED ? kNormPer : 1];
+    unsigned smask = 0, tmask = 0;
     double loc = 0.0;
     int nan = 0, inf = 0;
-    for (int j = j0; j < j1; ++j) {
-        const double t = (double)x[j] * (double)x[j];
-        nan |= t != t;
-        inf |= t == __builtin_inf();
-        loc += t;
+    if constexpr (STAGED) {
+#pragma unroll
+        for (int i = 0; i < kNormPer; ++i) {
+            const int j = j0 + i;
+            const float xv = j < j1 ? x[j] : 0.0f;
+            tv[i] = (double)xv * (double)xv;
+            nan |= tv[i] != tv[i];
+            inf |= tv[i] == __builtin_inf();
+            loc += tv[i];
+        }
+    } else {
+        for (int j = j0; j < j1; ++j) {
+            const double t = (double)x[j] * (double)x[j];
+            nan |= t != t;
+            inf |= t == __builtin_inf();
+            loc += t;
+        }
     }
     const int any_nan = __syncthreads_or(nan), any_inf = __syncthreads_or(inf);
     if (any_nan || any_inf) {
@@ -1764,7 +1784,17 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
         double tot_d;
         const double base = block_exclusive_scan<double>(loc, wsum_d, &tot_d);
         int cnt = 0;
-        {
+        if constexpr (STAGED) {
+            double P = base;
+#pragma unroll
+            for (int i = 0; i < kNormPer; ++i) {
+                const int c = norm_classify(P, tv[i], &kv[i]);
+                P += tv[i];
+                smask |= (c != 0 ? 1u : 0u) << i;
+                tmask |= (c == 2 ? 1u : 0u) << i;
+            }
+            cnt = __builtin_popcount(smask);
+        } else {
             double P = base;
             for (int j = j0; j < j1; ++j) {
                 const double t = (double)x[j] * (double)x[j];
@@ -1778,7 +1808,21 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
         if (nspec <= kNormMaxSpecial) {
             for (int q = tid; q <= nspec; q += kNormThreads) seg[q] = 0;
             __syncthreads();
-            {
+            if constexpr (STAGED) {
+                int q = sbase;  // specials before element i
+                unsigned long long run = 0;
+#pragma unroll
+                for (int i = 0; i < kNormPer; ++i) {
+                    if (!((smask >> i) & 1u)) {
+                        run += kv[i];
+                        continue;
+                    }
+                    if (run) atomicAdd(&seg[q], run);
+                    run = 0;
+                    spec[q++] = (tmask >> i) & 1u ? -((double)kv[i] + 1.0) : tv[i];
+                }
+                if (run) atomicAdd(&seg[q], run);
+            } else {
                 double P = base;
                 int q = sbase;  // specials before element j
                 unsigned long long run = 0;
