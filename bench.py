@@ -20,6 +20,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
 
 --workload times one workload alone and prints its own JSON line (for
 profiling one kernel); the default run prints the contract line above.
+``--workload rmsnorm[:ROWS]`` times the decoder's exact RMSNorm at width 5120.
 """
 import argparse
 import json
@@ -137,6 +138,32 @@ def cpu_baseline(name):
     }
 
 
+RMSNORM_H = 5120
+
+
+def time_rmsnorm(hb, torch, rows, steps, warmup):
+    """Per-call time (s) of the decoder's exact RMSNorm (i4_rmsnorm_dev) on
+    `rows` rows of width 5120 (the hidden size of the prefill and LM-head
+    shapes), timed like the matmul workloads.  The kernel is latency-bound on
+    one CU per row, so the rows are few and the time is per call."""
+    import numpy as np
+
+    rng = np.random.default_rng(7)
+    x = torch.from_numpy(rng.standard_normal((rows, RMSNORM_H)).astype(np.float32)).cuda()
+    w = torch.from_numpy((1 + 0.1 * rng.standard_normal(RMSNORM_H)).astype(np.float32)).cuda()
+    for _ in range(warmup):
+        hb.rmsnorm(x, w, 1e-6)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        hb.rmsnorm(x, w, 1e-6)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / steps
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -178,6 +205,12 @@ def main():
 
     if args.workload:
         name, _, r = args.workload.partition(":")
+        if name == "rmsnorm":
+            m = int(r) if r else 1
+            t = time_rmsnorm(hb, torch, m, args.steps, args.warmup)
+            print(json.dumps({"workload": f"RMSNorm M={m} H={RMSNORM_H} (in-order double sum, exact)",
+                              "steps": args.steps, "us": round(t * 1e6, 3)}), flush=True)
+            return
         if name not in workloads.LABELS:
             raise SystemExit(f"bench.py: unknown workload {name!r}; one of {sorted(workloads.LABELS)}")
         rows = int(r) if r else None
@@ -256,6 +289,8 @@ def main():
                 g = workloads.algorithmic_bytes(name, m) / t / 1e9
                 entry.update(gbs=round(g, 1), frac_hbm_peak=round(g / HBM_PEAK_GBS, 4))
             rows.append(entry)
+        t = time_rmsnorm(hb, torch, 1, args.steps, args.warmup)
+        rows.append({"workload": f"RMSNorm M=1 H={RMSNORM_H} (in-order double sum, exact)", "us": round(t * 1e6, 2)})
         result["workloads"] = rows
 
     if not args.no_cpu_baseline:
