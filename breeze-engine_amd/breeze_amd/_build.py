@@ -10,17 +10,19 @@ import sys
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(os.path.dirname(PKG), "csrc")
-SOURCES = ["qmm.hip"]
+# Host code and small kernels; the decode and prefill kernels, one unit per
+# (bits, activation mode) so the device passes run side by side.
+SOURCES = ["qmm.hip"] + [f"{k}_w{b}_{m}.hip" for k in ("dec", "pf") for b in (4, 8) for m in ("hp", "lp")]
 LIB_NAME = "libbreeze_qmm.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
+# Flags of both passes.
 FLAGS = [
     "--offload-arch=gfx950",
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     # Loadable by both the ROCm 7.2 runtime and the 7.0 runtime bundled with
     # PyTorch (one of the two serves the whole process).
     "-mcode-object-version=5",
@@ -29,6 +31,11 @@ FLAGS = [
     "-ffp-contract=off",
     "-fhip-fp32-correctly-rounded-divide-sqrt",
     "-fno-gpu-flush-denormals-to-zero",
+    "-Wall",
+]
+
+# Device pass only: the host target does not know these.
+DEVICE_FLAGS = [
     # No packed-FP32 instructions in any kernel.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # MFMA results in ordinary VGPRs: the epilogues read every MFMA result
@@ -37,7 +44,6 @@ FLAGS = [
     # Leading scalar kernel arguments arrive in SGPRs at wave launch, so a
     # kernel's first loads do not wait for a kernarg fetch.
     "-mllvm", "-amdgpu-kernarg-preload-count=14",
-    "-Wall",
 ]
 
 
@@ -45,20 +51,43 @@ def lib_path():
     return os.path.join(PKG, LIB_NAME)
 
 
-def build(verbose=False):
-    out = lib_path()
-    tmp = f"{out}.{os.getpid()}.tmp"
-    cmd = [HIPCC, *FLAGS, *(os.path.join(CSRC, s) for s in SOURCES), "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
+    return subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)
+
+
+def build(verbose=False):
+    """Device code objects and host code in two passes (run side by side),
+    so device-only flags never reach the host compiler; then one link."""
+    out = lib_path()
+    tag = f"{out}.{os.getpid()}"
+    tmp = f"{tag}.tmp"
+    srcs = [os.path.join(CSRC, s) for s in SOURCES]
+    fatbins = [f"{tag}.{i}.hipfb" for i in range(len(srcs))]
+    objs = [f"{tag}.{i}.o" for i in range(len(srcs))]
     try:
-        res = subprocess.run(cmd, capture_output=True, text=True)
-        if res.returncode != 0:
-            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr[-4000:]}")
+        procs = [(_run([HIPCC, "-x", "hip", *FLAGS, *DEVICE_FLAGS, "--offload-device-only", "-c", s, "-o", fb],
+                       verbose), s) for s, fb in zip(srcs, fatbins)]
+        for p, s in procs:
+            _, err = p.communicate()
+            if p.returncode != 0:
+                raise RuntimeError(f"hipcc (device pass of {s}) failed ({p.returncode}):\n{err[-4000:]}")
+        procs = [(_run([HIPCC, "-x", "hip", *FLAGS, "--offload-host-only", "-Xclang", "-fcuda-include-gpubinary",
+                        "-Xclang", fb, "-c", s, "-o", o], verbose), s) for s, fb, o in zip(srcs, fatbins, objs)]
+        for p, s in procs:
+            _, err = p.communicate()
+            if p.returncode != 0:
+                raise RuntimeError(f"hipcc (host pass of {s}) failed ({p.returncode}):\n{err[-4000:]}")
+        p = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
+        _, err = p.communicate()
+        if p.returncode != 0:
+            raise RuntimeError(f"link failed ({p.returncode}):\n{err[-4000:]}")
         os.replace(tmp, out)
     finally:
-        if os.path.exists(tmp):
-            os.unlink(tmp)
+        for f in (tmp, *fatbins, *objs):
+            if os.path.exists(f):
+                os.unlink(f)
     return out
 
 

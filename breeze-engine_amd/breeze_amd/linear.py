@@ -23,7 +23,8 @@ def backend():
 
 
 def prepare_weight(w_fp32):
-    """Store a dequantized ``[K, N]`` fp32 weight in the backend's native form."""
+    """Return the weight ``w_fp32`` (dequantized, ``[K, N]``) as the backend
+    keeps it: an fp16 device tensor with a GPU, else contiguous fp32 NumPy."""
     w = np.ascontiguousarray(w_fp32, dtype=np.float32)
     if _GPU:
         return torch.from_numpy(w).to(device="cuda", dtype=torch.float16)
@@ -31,7 +32,8 @@ def prepare_weight(w_fp32):
 
 
 def linear(a_fp32, w):
-    """Compute ``a @ w`` for a ``[.., K]`` activation, returning fp32 ``[.., N]``."""
+    """Product of an activation of shape ``[.., K]`` with a weight from
+    ``prepare_weight``; the result is an fp32 NumPy array of shape ``[.., N]``."""
     a = np.asarray(a_fp32)
     m = a.reshape(-1, a.shape[-1])
     n = int(w.shape[1])

@@ -1,0 +1,562 @@
+// dec_kernel.h -- the decode GEMV kernel (M <= 8) and its launcher,
+// instantiated per (bits, activation mode) by dec_w{4,8}_{hp,lp}.hip.
+#pragma once
+
+#include "qmm_common.h"
+
+namespace bq {
+
+// The leading scalar arguments are what the first activation and weight
+// loads need.  They are preloaded into SGPRs at wave launch (kernarg
+// preload, 14 SGPRs), so those loads do not wait for a kernarg fetch; the
+// rest of the arguments come from the struct as the code reaches them.
+// Tiles per workgroup group: the first rem_t groups own base_t + 1 tiles, the
+// rest base_t (ntiles = base_t * NG + rem_t).  misc = sc_shift | RG << 8 |
+// pair_xcd << 10 | phases per tile << 16.  PAIR: gate and up projections
+// in one launch; each output tile is the gate tile then the up tile of the
+// same columns, and C = silu(gate) * up.
+
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR, bool P64>
+__global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
+                                                             int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
+                                                             int pNG, int pngrp, int misc, GemvArgs args) {
+    GemvArgs a = args;
+    if (FUSED) a.A = static_cast<const float*>(act);
+    else a.Aq = static_cast<const uint8_t*>(act);
+    a.W = pW;
+    a.S = pS;
+    a.K = 32 * pnblk;
+    a.nblk = pnblk;
+    a.M = pM;
+    a.nbg = pnbg;
+    a.NG = pNG;
+    a.ngrp = pngrp;
+    a.nblk4 = (pnblk + 3) / 4 * 4;
+    a.sc_shift = misc & 31;
+    a.RG = (misc >> 8) & 3;
+    a.pair_xcd = (misc >> 10) & 1;
+    constexpr int JG = BITS == 8 ? 2 : 4;
+    constexpr int PP = dec_pitch(JG);
+    typedef float fvec __attribute__((ext_vector_type(JG)));
+    typedef int ivec __attribute__((ext_vector_type(JG)));
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    int g, rg;
+    if (a.RG == 1) {
+        g = blockIdx.x;
+        rg = 0;
+    } else if (a.pair_xcd) {
+        const int b = blockIdx.x;
+        g = (b >> 4) * 8 + (b & 7);
+        rg = (b >> 3) & 1;
+    } else {
+        g = blockIdx.x >> 1;
+        rg = blockIdx.x & 1;
+    }
+    const int m0 = rg * 4;
+    const int Mr = min(4, a.M - m0);
+
+    // Activation loads, ahead of all other set-up in program order: at kernel
+    // start the prologue's instructions are fetched cold, and timestamps put
+    // the load ~1.4 us after wave start when it sat behind the set-up code.
+    // K is a multiple of 32, so the rows m0.. of A are nb_rows contiguous
+    // 32-float blocks, and the staged scale and sum rows (pitch nblk4) are
+    // contiguous too: a block index is an offset, with no row/column split.
+    const int nb_rows = Mr * a.nblk;
+    uint4 av[kQuantPasses];
+    uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
+    if (FUSED) {
+        if (nb_rows > kQuantEarlyBlocks || wave < 8) {
+            const float* arow = a.A + (size_t)m0 * a.K + 4 * (tid & 7);
+            const bool all = nb_rows > kQuantEarlyBlocks;
+            const int qb = all ? 128 : 64;  // blocks per pass
+            const int npass_ld = all ? (nb_rows + 127) >> 7 : (nb_rows + 63) >> 6;
+#pragma unroll
+            for (int p = 0; p < kQuantPasses; ++p) {
+                if (p >= npass_ld) break;
+                const int blk = min(p * qb + (tid >> 3), nb_rows - 1);
+                av[p] = *reinterpret_cast<const uint4*>(arow + 32 * blk);
+            }
+        }
+    } else {
+        // Records of rows m0.. are contiguous: nb_rows*4 uint4, then the
+        // scale and sum(q) rows as uint4 (Mr * nblk4 / 4 each).
+        const uint4* rsrc = reinterpret_cast<const uint4*>(a.Aq + (size_t)m0 * a.nblk * 64);
+        const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+        // With one or two rows (block pairs) only the groups of 1024
+        // records that hold work are loaded; with more rows every group is
+        // (branches there cost more than the clamped loads).
+        r0 = rsrc[min(tid, nrec - 1)];
+        r1 = rsrc[min(1024 + tid, nrec - 1)];
+        r2 = rsrc[min(2048 + tid, nrec - 1)];
+        if (!P64 || nrec > 3072) {
+            r3 = rsrc[min(3072 + tid, nrec - 1)];
+            r4 = rsrc[min(4096 + tid, nrec - 1)];
+            r5 = rsrc[min(5120 + tid, nrec - 1)];
+        }
+        const int mi = min(tid, nmeta - 1);
+        rsa = *reinterpret_cast<const uint4*>(a.Sa + (size_t)m0 * a.nblk4 + 4 * mi);
+        rsq = *reinterpret_cast<const uint4*>(a.Sq + (size_t)m0 * a.nblk4 + 4 * mi);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int base_t = pbase_t, rem_t = prem_t;
+    const int t_begin = g * base_t + min(g, rem_t);
+    const int nT = base_t + (g < rem_t ? 1 : 0);
+    const int nbg = a.nbg;
+    const int npw = misc >> 16;                // phases per tile: ceil(nbg / 15)
+    const int U = nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
+
+    const DecLds lay = dec_lds(min(a.M, 4), a.nblk, JG, P64);
+    uint8_t* recs = smem + lay.recs;
+    float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
+    int* sq_l = reinterpret_cast<int*>(smem + lay.sq);
+    float* fbuf = reinterpret_cast<float*>(smem + lay.fbuf);  // [2][64][PP]
+
+    const int col = lane & 15, grp = lane >> 4;
+    const int me = min(grp, Mr - 1);
+
+    // Load cursor, kept incrementally: one scalar unit serves the CU's
+    // sixteen waves, which reach their scalar work together after each
+    // barrier, so every scalar instruction per unit lengthens every phase.
+    // The next unit is chunk ld_c (clamped to the tile's last chunk) of local
+    // tile ld_t, ld_rem units before the tile ends; ld_w, ld_s and ld_m index
+    // the tile's weights, scales and per-block metadata.  Past the end ld_c
+    // is out of range (no work) and the loads re-read the last tile.
+    //
+    // A producer with no chunk in a tile's short last phase still fills its
+    // ring slot.  That load's data is never used, so its weight address is
+    // the chunk this producer loads next in the following tile (chunk
+    // wave + 15, requested two phases later): the slot warms L2 for it.  The
+    // tiles of a workgroup are contiguous, so that is chunk nbg + wave + 15
+    // from the current tile.  On the last tile (and for gate/up pairs, whose
+    // next tile lies in the other array) the load re-reads the tile's last
+    // chunk instead, so every address stays inside the workgroup's tiles.
+    int ld_c = wave, ld_rem = npw, ld_t = 0, ld_sel = 0;  // ld_sel: up tile of a pair
+    uint32_t ld_w = (uint32_t)t_begin * nbg * 64;
+    uint32_t ld_s = (uint32_t)t_begin * a.ngrp * 16;
+    uint32_t ld_m = (uint32_t)t_begin * nbg * 16;
+    const int pf_c = nbg + kProducers + wave;
+    const bool pf = !PAIR && npw >= 2 && wave + kProducers < nbg;
+    int ld_idle = (pf && nT > 1) ? pf_c : nbg - 1;  // weight chunk of a load with no work
+    auto load_unit = [&](Unit<JG, EXTRA>& p) {
+        const int c = min(ld_c, nbg - 1);
+        const int cw = ld_c < nbg ? ld_c : ld_idle;
+        uint32_t wi = ld_w + cw * 64 + lane;                               // weight uint4 index
+        uint32_t mi = ld_m + c * 16 + col;                                 // per-block metadata (EXTRA)
+        uint32_t si = ld_s + (uint32_t)((c * JG) >> a.sc_shift) * 16 + col;  // scale index
+        // Opaque to the optimizer, so the loads are not split into
+        // uniform-address copies on branches of their own.
+        asm("" : "+v"(wi), "+v"(mi), "+v"(si));
+        const bool up = PAIR && ld_sel;
+        p.w = (up ? a.W2 : a.W)[wi];
+        if (EXTRA) {
+            const fvec sv = *reinterpret_cast<const fvec*>((up ? a.S2 : a.S) + (size_t)mi * JG);
+            const ivec dv = *reinterpret_cast<const ivec*>((up ? a.D2 : a.D) + (size_t)mi * JG);
+#pragma unroll
+            for (int jb = 0; jb < JG; ++jb) {
+                p.sc[EXTRA ? jb : 0] = sv[jb];
+                p.dl[EXTRA ? jb : 0] = dv[jb];
+            }
+            if (JG == 4) p.zp = *reinterpret_cast<const uint32_t*>((up ? a.Z2 : a.Z) + (size_t)mi * 4);
+        } else {
+            p.sc[0] = (up ? a.S2 : a.S)[si];
+        }
+        p.c = ld_c;
+        ld_c += kProducers;
+        if (--ld_rem == 0) {
+            ld_rem = npw;
+            if (PAIR && ld_sel == 0 && ld_t < nT) {
+                ld_sel = 1;  // the same tile's up projection
+                ld_c = wave;
+            } else {
+                if (PAIR) ld_sel = 0;
+                if (++ld_t < nT) {
+                    ld_c = wave;
+                    ld_w += nbg * 64;
+                    ld_s += a.ngrp * 16;
+                    ld_m += nbg * 16;
+                    if (ld_t + 1 == nT) ld_idle = nbg - 1;
+                } else {
+                    ld_c = 1 << 24;
+                }
+            }
+        }
+    };
+
+    // ---------------- prologue
+    // The activation loads went out first (above); the first R weight units
+    // follow, then the activations are quantized (or their records copied)
+    // into LDS while the weights stream in.  The scheduling barriers keep
+    // this issue order.
+    auto store_acts = [&]() {
+        if (FUSED) {
+            const bool all = nb_rows > kQuantEarlyBlocks;
+            const int qb = all ? 128 : 64;  // blocks per pass
+            const int npass = all ? (nb_rows + 127) >> 7 : wave < 8 ? (nb_rows + 63) >> 6 : 0;
+#pragma unroll
+            for (int p = 0; p < kQuantPasses; ++p) {
+                if (p >= npass) break;
+                const int blk = p * qb + (tid >> 3), e = tid & 7;
+                float s;
+                int sum;
+                uint32_t p0, p1;
+                quant8<HP>(make_float4(__uint_as_float(av[p].x), __uint_as_float(av[p].y),
+                                       __uint_as_float(av[p].z), __uint_as_float(av[p].w)),
+                           s, sum, p0, p1);
+                if (blk < nb_rows) {
+                    const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk), j = blk - m * a.nblk;
+                    if (P64) {
+                        // Lane e holds bytes 4(e&1).. of k-octet e>>1: the
+                        // slot's zero half, then the octet.
+                        uint32_t* sh = reinterpret_cast<uint32_t*>(recs + m * lay.rec_pitch + j * 128 +
+                                                                   (e >> 1) * 16) + (e & 1);
+                        sh[0] = 0u;
+                        sh[2] = p0;
+                        sh[16] = 0u;  // l octets, 64 B further
+                        sh[18] = p1;
+                    } else {
+                        // [chunk][h, l][k-octet][block of the chunk] of 8
+                        // bytes: a lane's A operands for a chunk are 8 JG
+                        // contiguous bytes.
+                        uint8_t* rec = recs + m * lay.rec_pitch + (j / JG) * (JG * 64) + (e >> 1) * (JG * 8) +
+                                       (j % JG) * 8 + 4 * (e & 1);
+                        *reinterpret_cast<uint32_t*>(rec) = p0;
+                        *reinterpret_cast<uint32_t*>(rec + JG * 32) = p1;
+                    }
+                    if (e == 0) {
+                        sa_l[m * lay.sa_pitch + j] = s;
+                        sq_l[m * lay.sa_pitch + j] = (EXTRA ? -1 : -8) * sum;
+                    }
+                }
+            }
+        } else {
+            // Rows land at the padded LDS pitches.
+            const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;
+            const int L = a.nblk * 4;
+            auto put = [&](int i, const uint4& v) {
+                i = min(i, nrec - 1);
+                const int m = (i >= L) + (i >= 2 * L) + (i >= 3 * L);
+                if (P64) {
+                    // Source uint4 q of a block: h or l (q >> 1) octets
+                    // 2(q & 1) and 2(q & 1) + 1, each into its slot.
+                    const int r = i - m * L, j = r >> 2, q = r & 3;
+                    uint4* slot = reinterpret_cast<uint4*>(recs + m * lay.rec_pitch + j * 128 + (q >> 1) * 64 +
+                                                           (q & 1) * 32);
+                    slot[0] = make_uint4(0u, 0u, v.x, v.y);
+                    slot[1] = make_uint4(0u, 0u, v.z, v.w);
+                } else {
+                    // Source uint4 q of a block: h or l (q >> 1) octets
+                    // 2(q & 1) and 2(q & 1) + 1, each to its place in the
+                    // [chunk][h, l][k-octet][block] layout.
+                    const int r = i - m * L, j = r >> 2, q = r & 3;
+                    uint8_t* o = recs + m * lay.rec_pitch + (j / JG) * (JG * 64) + (q >> 1) * (JG * 32) +
+                                 2 * (q & 1) * (JG * 8) + (j % JG) * 8;
+                    *reinterpret_cast<uint2*>(o) = make_uint2(v.x, v.y);
+                    *reinterpret_cast<uint2*>(o + JG * 8) = make_uint2(v.z, v.w);
+                }
+            };
+            // Threads past the end rewrite the last element with the value
+            // they loaded from it; with block pairs, groups of 1024 records
+            // without work are skipped (up to 3072 such stores to one LDS
+            // address otherwise).
+            put(tid, r0);
+            put(1024 + tid, r1);
+            put(2048 + tid, r2);
+            if (!P64 || nrec > 3072) {
+                put(3072 + tid, r3);
+                put(4096 + tid, r4);
+                put(5120 + tid, r5);
+            }
+            const int mi = min(tid, nmeta - 1);
+            const int mm = (4 * mi >= a.nblk4) + (4 * mi >= 2 * a.nblk4) + (4 * mi >= 3 * a.nblk4);
+            const int md = mi + mm * ((lay.sa_pitch - a.nblk4) >> 2);
+            reinterpret_cast<uint4*>(sa_l)[md] = rsa;
+            const uint32_t f = EXTRA ? 0xFFFFFFFFu : 0xFFFFFFF8u;  // -1 or -8
+            reinterpret_cast<uint4*>(sq_l)[md] = make_uint4(f * rsq.x, f * rsq.y, f * rsq.z, f * rsq.w);
+        }
+        {
+            uint32_t* cst = reinterpret_cast<uint32_t*>(smem + lay.consts);
+            if (P64) {
+                // [8 zeros][8 bytes of 64], then zeros; and each record row's
+                // closing zero slot.
+                if (tid < 128) cst[tid] = (tid == 2 || tid == 3) ? 0x40404040u : 0u;
+                if (tid < 4 * Mr) {
+                    uint32_t* z = reinterpret_cast<uint32_t*>(recs + (tid >> 2) * lay.rec_pitch + a.nblk * 128);
+                    z[tid & 3] = 0u;
+                }
+            } else if (tid < 128) {
+                cst[tid] = tid < 64 ? 0x40404040u : 0u;  // [0,256) bytes of 64, [256,512) zeros
+            }
+        }
+    };
+
+    if (wave == kChainWave) {
+        // ================= chain wave
+        // Its fold is one dependent FMA chain per output and paces the
+        // phases: first pick of the SIMD's issue slots over the producers.
+        __builtin_amdgcn_s_setprio(3);
+        store_acts();
+        lds_barrier();
+        // Lane (row me, column col) of the current tile.
+        const float* sa_row = sa_l + me * lay.sa_pitch;
+        const bool tail_pad = a.nblk != nbg * JG;  // the last chunk has padding blocks
+        float acc = 0.0f, gate = 0.0f;
+        unsigned long long best = 0;
+        int pr_t = 0, pr_p = 0, pr_sel = 0;
+        for (int u = 0; u < U; ++u) {
+            lds_barrier();
+            const float* fp = fbuf + ((u & 1) * 64 + lane) * PP;
+            const int c0 = kProducers * pr_p;
+            const float* sp = sa_row + c0 * JG;
+            if (c0 + kProducers < nbg || (c0 + kProducers == nbg && !tail_pad)) {
+                // Full phase: every block is real.  All fifteen chunks'
+                // reads, then the FMAs: right after the barrier the reads
+                // queue behind the producers' operand reads (~0.3 us), so
+                // one wait instead of one per group of chunks.
+                fvec fv[kProducers], sv[kProducers];
+#pragma unroll
+                for (int i = 0; i < kProducers; ++i) {
+                    fv[i] = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    sv[i] = *reinterpret_cast<const fvec*>(sp + i * JG);
+                }
+#pragma unroll
+                for (int i = 0; i < kProducers; ++i) {
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[i][jb], fv[i][jb], acc);
+                }
+            } else {
+                // The tile's last phase: whole chunks two at a time with
+                // wide reads, then the blocks of a padded last chunk.
+                const int nb = a.nblk - c0 * JG, nwc = nb / JG;
+                int i = 0;
+                for (; i + 2 <= nwc; i += 2) {
+                    const fvec f0 = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    const fvec s0 = *reinterpret_cast<const fvec*>(sp + i * JG);
+                    const fvec f1 = *reinterpret_cast<const fvec*>(fp + (i + 1) * JG);
+                    const fvec s1 = *reinterpret_cast<const fvec*>(sp + (i + 1) * JG);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s0[jb], f0[jb], acc);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s1[jb], f1[jb], acc);
+                }
+                if (i < nwc) {
+                    const fvec f0 = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    const fvec s0 = *reinterpret_cast<const fvec*>(sp + i * JG);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s0[jb], f0[jb], acc);
+                    ++i;
+                }
+                for (int b = i * JG; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
+            }
+            if (++pr_p == npw) {
+                if (PAIR && pr_sel == 0) {
+                    gate = acc;  // the up tile of the same columns follows
+                    pr_sel = 1;
+                } else {
+                    // silu(g) = g / (1 + exp(-g)) (qwen35_decoder.cpp:129),
+                    // times the up projection (qwen35_decoder.cpp:408).
+                    const float v = PAIR ? gate / (1.0f + expf(-gate)) * acc : acc;
+                    if (grp < Mr) {
+                        const int n = (t_begin + pr_t) * 16 + col;
+                        a.C[(size_t)(m0 + grp) * a.N + n] = v;
+                        if (!PAIR && a.idx) {
+                            const unsigned long long k = argmax_key(acc, n);
+                            best = k > best ? k : best;
+                        }
+                    }
+                    if (PAIR) pr_sel = 0;
+                    ++pr_t;
+                }
+                acc = 0.0f;
+                pr_p = 0;
+            }
+        }
+        if (!PAIR && a.idx) {
+            // Row maximum over the lanes of each row (lanes 16r..16r+15).
+#pragma unroll
+            for (int s = 1; s < 16; s <<= 1) {
+                const unsigned long long o = __shfl_xor(best, s, 16);
+                best = o > best ? o : best;
+            }
+            {
+                // Argmax without a second launch: each workgroup merges its
+                // row keys into idx_key with device-scope atomic max, waits
+                // for them, then takes a ticket; the workgroup holding the
+                // last ticket swaps the merged keys back to zero (re-arming
+                // them for the next call) and writes the indices.
+                if (col == 0 && grp < Mr) (void)atomicMax(a.key + m0 + grp, best);
+                __builtin_amdgcn_s_waitcnt(0);
+                unsigned int t = 0;
+                if (lane == 0) t = atomicAdd(a.ticket, 1u);
+                t = __shfl(t, 0);
+                if (t == gridDim.x - 1 && lane < a.M) {
+                    const unsigned long long k = atomicExch(a.key + lane, 0ull);
+                    a.idx[lane] = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+                    if (lane == 0) atomicExch(a.ticket, 0u);
+                }
+            }
+        }
+        return;
+    }
+
+    // ================= producers (waves 0..14)
+    // Quantizing in the prologue: the first weight units stream in while it
+    // runs.  Copying staged records (up to 96 KB per workgroup): the copy
+    // goes first, since weight requests issued beside it slowed it down
+    // (three and four rows: 11.8 -> 11.3 us).
+    Unit<JG, EXTRA> ring[R];
+    if (!FUSED) {
+        store_acts();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int d = 0; d < R; ++d) load_unit(ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (FUSED) store_acts();
+    lds_barrier();
+
+    // A operand: lane row arow = 4 * group + slot, k-octet kq.  Slots 0 and
+    // 1 are the h and l bytes; slots 2 and 3 are rows of 64, so their two
+    // results add up to the 128 * sum(b) term.  Output lane (col, grp) holds
+    // row grp.  The LDS sums of q hold the zero-point term's factor: -sum(q)
+    // for explicit zero points, -8 * sum(q) for the default zero point 8.
+    const int arow = lane & 15, arg = arow >> 2, ars = arow & 3, kq = lane >> 4;
+    const bool is_data = ars < 2 && arg < Mr;
+    const int data_base = lay.recs + arg * lay.rec_pitch + ars * (JG * 32) + kq * (JG * 8);
+    const int const_base = lay.consts + ((ars >= 2 && arg < Mr) ? 0 : 256) + kq * (JG * 8);
+    // P64: A row r = 8 * activation row + 4 * (block of the pair) + slot,
+    // read as 16 bytes from the zero-padded octet slots ([octet | zeros] for
+    // the pair's first block, [zeros | octet] for its second).  Output lane
+    // (col, grp): activation row grp >> 1, block 2 * mi + (grp & 1).
+    const int p_row = arow >> 3, p_sel = (arow >> 2) & 1;
+    const bool p_data = ars < 2 && p_row < Mr;
+    const int p_data_base = lay.recs + p_row * lay.rec_pitch + ars * 64 + kq * 16 + p_sel * 128 + 8 - 8 * p_sel;
+    const int p_const_base = lay.consts + ((ars >= 2 && p_row < Mr) ? 8 - 8 * p_sel : 16);
+    const int o_row = min(grp >> 1, Mr - 1), o_sel = grp & 1;
+    float* const p_fout = fbuf + (col + 16 * (grp >> 1)) * PP + wave * JG + o_sel;
+
+    for (int u0 = 0; u0 < U; u0 += R) {
+#pragma unroll
+        for (int d = 0; d < R; ++d) {
+            const bool live = u0 + d < U;  // uniform over the workgroup
+            const int c = ring[d].c;
+            const int buf = (u0 + d) & 1;
+            if (P64 && c < nbg) {
+                const Unit<JG, EXTRA>& cur = ring[d];
+                const int abase = p_data ? p_data_base + c * JG * 128 : p_const_base;
+                int2 nsq2 = make_int2(0, 0);  // this lane's block in each pair
+                if (BITS == 4) {
+                    const int* q = sq_l + o_row * lay.sa_pitch + c * 4 + o_sel;
+                    nsq2 = make_int2(q[0], q[2]);
+                }
+                float fo[JG / 2];
+#pragma unroll
+                for (int mi = 0; mi < JG / 2; ++mi) {
+                    // Blocks past nblk (last chunk) read padding; the chain
+                    // never folds them.
+                    uint4 bop = cur.w;
+                    if (BITS == 4) {
+                        const uint64_t b0 = unpack_b(cur.w, 2 * mi, 4), b1 = unpack_b(cur.w, 2 * mi + 1, 4);
+                        bop = make_uint4((uint32_t)b0, (uint32_t)(b0 >> 32), (uint32_t)b1, (uint32_t)(b1 >> 32));
+                    }
+                    const uint8_t* ap = smem + abase + (p_data ? mi * 256 : 0);
+                    const uint2 alo = *reinterpret_cast<const uint2*>(ap);
+                    const uint2 ahi = *reinterpret_cast<const uint2*>(ap + 8);
+                    const v4i dd = mfma64(make_uint4(alo.x, alo.y, ahi.x, ahi.y), bop);
+                    int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
+                    if (BITS == 4) {
+                        const int nsq = mi == 0 ? nsq2.x : nsq2.y;
+                        cs += EXTRA ? (int)(int8_t)((o_sel ? cur.zp >> 8 : cur.zp) >> (16 * mi)) * nsq : nsq;
+                    }
+                    float sc = cur.sc[0];
+                    if (EXTRA) {
+                        // Values first, then the lane's pick: a select
+                        // between array elements would index the unit in
+                        // memory.
+                        const int dl0 = cur.dl[EXTRA ? 2 * mi : 0], dl1 = cur.dl[EXTRA ? 2 * mi + 1 : 0];
+                        const float sc0 = cur.sc[EXTRA ? 2 * mi : 0], sc1 = cur.sc[EXTRA ? 2 * mi + 1 : 0];
+                        cs += (HP ? 256 : 1) * (o_sel ? dl1 : dl0);
+                        sc = o_sel ? sc1 : sc0;
+                    }
+                    fo[mi] = (float)cs * sc;
+                }
+                // Both results in one LDS instruction (ds_write2_b32): the
+                // phase is bounded by LDS instruction issue, ~8 CU cycles each.
+#pragma unroll
+                for (int mi = 0; mi < JG / 2; ++mi) p_fout[buf * 64 * PP + 2 * mi] = fo[mi];
+            } else if (!P64 && c < nbg) {
+                const Unit<JG, EXTRA>& cur = ring[d];
+                const int abase = is_data ? data_base + c * JG * 64 : const_base;
+                // The chunk's JG A operands of this lane: 8 JG contiguous bytes.
+                uint4 av4[JG / 2];
+#pragma unroll
+                for (int h = 0; h < JG / 2; ++h) av4[h] = *reinterpret_cast<const uint4*>(smem + abase + 16 * h);
+                int4 sqv = make_int4(0, 0, 0, 0);
+                if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * lay.sa_pitch + c * 4);
+                fvec fo;
+#pragma unroll
+                for (int jb = 0; jb < JG; ++jb) {
+                    // Blocks past nblk (last chunk) read padding; the chain
+                    // never folds them.
+                    const uint64_t bop = unpack_b(cur.w, jb, BITS);
+                    const uint4& a2 = av4[jb >> 1];
+                    const uint64_t aop = (jb & 1) ? ((uint64_t)a2.w << 32 | a2.z) : ((uint64_t)a2.y << 32 | a2.x);
+                    const v4i dd = mfma16(aop, bop);
+                    int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
+                    if (BITS == 4) {
+                        const int nsq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
+                        cs += EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) * nsq : nsq;
+                    }
+                    if (EXTRA) cs += (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
+                    fo[jb] = (float)cs * cur.sc[EXTRA ? jb : 0];
+                }
+                *reinterpret_cast<fvec*>(fbuf + (buf * 64 + lane) * PP + wave * JG) = fo;
+            }
+            load_unit(ring[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) lds_barrier();
+        }
+    }
+}
+
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR, bool P64>
+hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hipStream_t st) {
+    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, PAIR, P64>;
+    const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (EXTRA ? 8 : 0) | ((R / 2 - 1) << 4) |
+                    (PAIR ? 32 : 0) | (P64 ? 64 : 0);
+    if (!attr_set[key]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+        if (e != hipSuccess) return e;
+        attr_set[key] = true;
+    }
+    const void* act = FUSED ? static_cast<const void*>(a.A) : static_cast<const void*>(a.Aq);
+    const int npw = (a.nbg + kProducers - 1) / kProducers;
+    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 10 | npw << 16;
+    const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
+    kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, base_t, a.nblk, a.M, a.nbg, rem_t, a.NG, a.ngrp, misc, a);
+    return hipGetLastError();
+}
+
+template <int BITS, bool HP, bool FUSED, bool EXTRA>
+hipError_t launch_dec_r(bool* attr_set, const GemvArgs& a, int grid, int lds, bool pair, bool p64,
+                        hipStream_t st) {
+    if (p64) return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true, true>(attr_set, a, grid, lds, st)
+                         : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false, true>(attr_set, a, grid, lds, st);
+    return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true, false>(attr_set, a, grid, lds, st)
+                : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false, false>(attr_set, a, grid, lds, st);
+}
+
+template <int BITS, bool HP>
+hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds, bool pair, bool p64, bool fused,
+                           bool extra, hipStream_t st) {
+    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(attr_set, a, grid, lds, pair, p64, st)
+                            : launch_dec_r<BITS, HP, false, true>(attr_set, a, grid, lds, pair, p64, st);
+    return fused ? launch_dec_r<BITS, HP, true, false>(attr_set, a, grid, lds, pair, p64, st)
+                 : launch_dec_r<BITS, HP, false, false>(attr_set, a, grid, lds, pair, p64, st);
+}
+
+}  // namespace bq

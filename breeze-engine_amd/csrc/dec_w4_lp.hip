@@ -1,0 +1,7 @@
+// Decode kernels for INT4 weights, INT8 activations.
+#include "dec_kernel.h"
+
+namespace bq {
+template hipError_t launch_dec_bits<4, false>(bool*, const GemvArgs&, int, int, bool, bool, bool, bool,
+                                                    hipStream_t);
+}  // namespace bq

@@ -1,0 +1,7 @@
+// Decode kernels for INT8 weights, two-pass INT16 activations.
+#include "dec_kernel.h"
+
+namespace bq {
+template hipError_t launch_dec_bits<8, true>(bool*, const GemvArgs&, int, int, bool, bool, bool, bool,
+                                                    hipStream_t);
+}  // namespace bq

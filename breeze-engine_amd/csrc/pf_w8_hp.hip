@@ -1,0 +1,6 @@
+// Prefill GEMM kernels for INT8 weights, two-pass INT16 activations.
+#include "prefill_kernel.h"
+
+namespace bq {
+template hipError_t launch_pf<8, true>(bool*, const PfArgs&, int, int, dim3, hipStream_t);
+}  // namespace bq

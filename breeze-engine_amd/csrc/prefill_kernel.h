@@ -1,0 +1,516 @@
+// prefill_kernel.h -- the prefill GEMM (M > 8) and its launcher,
+// instantiated per (bits, activation mode) by pf_w{4,8}_{hp,lp}.hip.
+#pragma once
+
+#include "qmm_common.h"
+
+namespace bq {
+
+template <int BITS, bool HP, int SCM, int CT>
+__global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
+    using L = PfLayout<CT, SCM, BITS>;
+    extern __shared__ __align__(16) char pf_lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int col = lane & 15, grp = lane >> 4;
+    // Wave w: row pair w&3 (two 16-row tiles) and column half w>>2, so each
+    // SIMD (waves w and w+4) holds one wave of each half.
+    const int rp = wave & 3, half = wave >> 2;
+    const int t0 = blockIdx.x * CT;
+    const int rt0 = blockIdx.y * kPfWaves + 2 * rp;
+    const bool active = rt0 * 16 < a.M;
+    const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(pf_lds));
+    const int nch = a.nch;
+    const int nst = (nch + kPfChunks - 1) / kPfChunks;
+    const bool odd = a.nblk & 1;
+
+    // Shared part of a chunk (INT8) or stage (INT4): slot k of this wave
+    // loads the 1 KB at x0, u = k * kPfWaves + wave (clamped), lane bytes
+    // x0 + 16*lane.  INT8: x0 = min(u * 1024, kShared - 1024) in the chunk
+    // (overlapping slots write equal bytes).  INT4: raw tile u of the stage
+    // into chunk 0's weight area, or KB u - CT of the raw area.
+    const char* src0[L::kPerWave];
+    uint32_t step[L::kPerWave], gstep[L::kPerWave], x0s[L::kPerWave];
+    bool to_raw[L::kPerWave];
+#pragma unroll
+    for (int k = 0; k < L::kPerWave; ++k) {
+        const int u = min(k * kPfWaves + wave, L::kUnits - 1);
+        const int x0 = min(u * 1024, L::kShared - 1024);
+        const int x = x0 + 16 * lane;
+        x0s[k] = (uint32_t)x0;
+        gstep[k] = 0;
+        to_raw[k] = false;
+        if (BITS == 4) {
+            if (u < CT) {
+                const int tc = min(t0 + u, a.ntiles - 1);
+                src0[k] = a.W + (size_t)tc * a.nbg * 1024 + 16 * lane;
+                step[k] = 1024;
+                x0s[k] = (uint32_t)(u * 1024);
+            } else {
+                const int y = (u - CT) * 1024 + 16 * lane;
+                to_raw[k] = true;
+                x0s[k] = (uint32_t)(L::kRawOff + (u - CT) * 1024);
+                src0[k] = a.S;  // padding lanes: any valid source
+                step[k] = 0;
+                if (SCM == 2 && y < L::kRawZ) {
+                    const int tc = min(t0 + (y >> 8), a.ntiles - 1);
+                    src0[k] = a.S + (size_t)tc * a.nbg * 256 + (y & 255);
+                    step[k] = 256;
+                } else if (SCM == 2 && y < L::kRawUsed) {
+                    const int yz = y - L::kRawZ;
+                    const int tc = min(t0 + (yz >> 6), a.ntiles - 1);
+                    src0[k] = a.Z + (size_t)tc * a.nbg * 64 + (yz & 63);
+                    step[k] = 64;
+                } else if (SCM == 1 && y < L::kRawUsed) {
+                    const int tc = min(t0 + (y >> 6), a.ntiles - 1);
+                    src0[k] = a.S + (size_t)tc * a.ngrp * 64 + (y & 63);
+                    gstep[k] = 64;
+                }
+            }
+        } else if (x < L::kWS) {
+            const int tc = min(t0 + (x >> 10), a.ntiles - 1);
+            src0[k] = a.W + (size_t)tc * nch * 1024 + (x & 1023);
+            step[k] = 1024;
+        } else if (x < L::kSB) {
+            const int y = x - L::kWS;
+            const int tc = min(t0 + (y >> 7), a.ntiles - 1);
+            src0[k] = a.WS + (size_t)tc * nch * 128 + (y & 127);
+            step[k] = 128;
+        } else if (SCM == 2) {
+            const int y = x - L::kSB;
+            const int tc = min(t0 + (y >> 7), a.ntiles - 1);
+            src0[k] = a.S + (size_t)tc * nch * 128 + (y & 127);
+            step[k] = 128;
+        } else {
+            const int y = x - L::kSB;
+            const int tc = min(t0 + (y >> 6), a.ntiles - 1);
+            src0[k] = a.S + (size_t)tc * a.ngrp * 64 + (y & 63);
+            step[k] = 0;
+            gstep[k] = 64;
+        }
+    }
+    // This wave's two activation records per chunk.
+    const char* rec0 = a.R + (size_t)rt0 * nch * kRecBytes + 16 * lane;
+    const size_t rec_step = (size_t)nch * kRecBytes;  // next row tile
+
+    // Load d of this wave's kDmaChunk loads of chunk c into the chunk region
+    // at LDS address cbase: the shared slots, then 3 per activation record.
+    constexpr int kDmaChunk = L::kPerWave + 6;
+    // INT4: only chunk 0 of a stage (first) carries the stage's shared loads.
+    auto dma_slot = [&](int c, uint32_t cbase, int d, bool first) {
+        if (d < L::kPerWave) {
+            if (BITS == 8) {
+                const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
+                dma16(src0[d] + (size_t)c * step[d] + g * gstep[d], cbase + x0s[d]);
+            } else if (first) {
+                const int sg = c >> 1;
+                const size_t g = SCM == 1 ? (size_t)((4 * sg) >> a.sc_shift) : 0;
+                dma16(src0[d] + (size_t)sg * step[d] + g * gstep[d], (to_raw[d] ? lds0 : cbase) + x0s[d]);
+            }
+        } else {
+            const int e = d - L::kPerWave, r = e / 3, part = e % 3;
+            const int off = part == 0 ? 0 : part == 1 ? 1024 : 1152;
+            dma16(rec0 + r * rec_step + (size_t)c * kRecBytes + off,
+                  cbase + (uint32_t)(L::kA + (2 * rp + r) * kRecBytes + off));
+        }
+    };
+    auto issue_chunk = [&](int c, uint32_t cbase, bool first) {
+#pragma unroll
+        for (int d = 0; d < kDmaChunk; ++d) dma_slot(c, cbase, d, first);
+    };
+    auto issue_stage = [&](int g, int buf) {
+        const uint32_t sbase = lds0 + (uint32_t)(buf * L::kStage);
+#pragma unroll
+        for (int cc = 0; cc < kPfChunks; ++cc) {
+            const int c = g * kPfChunks + cc;
+            if (c < nch) issue_chunk(c, sbase + (uint32_t)(cc * L::kChunk), cc == 0);
+        }
+    };
+
+    // INT4: expands stage buffer buf in place (all threads; a workgroup
+    // barrier must follow).  Wave w takes tiles w, w + 8, ...; lane l holds
+    // weight lane l of the tile (column l & 15, k-octet l >> 4), so the LDS
+    // reads and writes are linear.  The nibble sums of a column's four
+    // octets (one per 16-lane row) meet by row swaps.
+    auto expand = [&](int buf) {
+        if constexpr (BITS == 4) {
+            char* sb = pf_lds + buf * L::kStage;
+            const char* raw = pf_lds + L::kRawOff;
+            const int c = lane & 15, o = lane >> 4, cc = o & 1;
+            for (int t = wave; t < CT; t += kPfWaves) {
+                const int wl = t * 1024 + 16 * lane;
+                const uint4 w = *reinterpret_cast<const uint4*>(sb + wl);
+                const uint32_t z = SCM == 2 ? *reinterpret_cast<const uint32_t*>(raw + L::kRawZ + t * 64 + 4 * c)
+                                            : 0x08080808u;
+                const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+                uint32_t lo[4], hi[4], nsum[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    // b = n - zp as a signed byte: n + (128 - zp), then flip
+                    // the top bit.  zp is a signed byte in [-112, 127]
+                    // (i4_prepack sends lower legacy zero points to the INT8
+                    // representation), so 128 - zp is in [1, 240] and
+                    // n + 128 - zp in [1, 255]: no carry crosses a byte.
+                    const int zs = SCM == 2 ? (int)(int8_t)(z >> (8 * b)) : 8;
+                    const uint32_t zr = (uint32_t)(128 - zs) * 0x01010101u;
+                    lo[b] = ((wv[b] & 0x0F0F0F0Fu) + zr) ^ 0x80808080u;
+                    hi[b] = (((wv[b] >> 4) & 0x0F0F0F0Fu) + zr) ^ 0x80808080u;
+                    nsum[b] = __builtin_amdgcn_udot8(wv[b], 0x11111111u, 0u, false);  // <= 120
+                }
+                *reinterpret_cast<uint4*>(sb + wl) = make_uint4(lo[0], hi[0], lo[1], hi[1]);
+                *reinterpret_cast<uint4*>(sb + L::kChunk + wl) = make_uint4(lo[2], hi[2], lo[3], hi[3]);
+                // Per-column nibble sums of blocks (0, 1) and (2, 3), two per
+                // dword, summed over the four rows (octets).
+                uint32_t ps[2] = {nsum[0] | nsum[1] << 16, nsum[2] | nsum[3] << 16};
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    const auto s32 = __builtin_amdgcn_permlane32_swap(ps[q], ps[q], false, false);
+                    const uint32_t y = s32[0] + s32[1];
+                    const auto s16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
+                    ps[q] = s16[0] + s16[1];
+                }
+                char* cb = sb + cc * L::kChunk;
+                if (o < 2) {
+                    // Row o: 128 * sum(n - zp) of chunk o's two blocks.
+                    const uint32_t p2 = cc ? ps[1] : ps[0];
+                    const uint32_t zz = SCM == 2 ? z >> (16 * cc) : 0x0808u;
+                    const int s0 = (int)(p2 & 0xFFFFu) - 32 * (int)(int8_t)zz;
+                    const int s1 = (int)(p2 >> 16) - 32 * (int)(int8_t)(zz >> 8);
+                    *reinterpret_cast<int2*>(cb + L::kWS + t * 128 + 8 * c) = make_int2(128 * s0, 128 * s1);
+                } else if (SCM == 2) {
+                    *reinterpret_cast<float2*>(cb + L::kSB + t * 128 + 8 * c) =
+                        *reinterpret_cast<const float2*>(raw + t * 256 + 16 * c + 8 * cc);
+                } else if (SCM == 1) {
+                    *reinterpret_cast<float*>(cb + L::kSB + t * 64 + 4 * c) =
+                        *reinterpret_cast<const float*>(raw + t * 64 + 4 * c);
+                }
+            }
+        }
+    };
+
+    // The whole K loop of one column half (CTW tiles from WG tile toff) on
+    // v_mfma_i32_32x32x32_i8: the wave's two 16-row records are its 32 rows
+    // and pairs of its tiles are 32-column groups, one MFMA per (group,
+    // 32-block) at the full INT8 rate (twice the 16x16x32 rate).  An odd
+    // last tile of the half takes 16x16x32 MFMAs on the 16-row records.
+    // Per (group, block) the h-byte MFMA's result, shifted left by 8 plus
+    // 128 * sum(b), is the l-byte MFMA's accumulator input, so that MFMA
+    // holds the exact block integer cs, and the lane folds
+    // acc = fma(s_a, f32(cs) * s_b, acc) in block order.
+    // Lane l: A row / output column c32 = l & 31, k half kh = l >> 5.  The
+    // operands come from the same LDS layout: a record's lane r + 16 * o
+    // holds k-octet o of row r, and a weight chunk's lane c + 16 * o holds
+    // k-octet o of column c for both blocks, so octets 2 kh and 2 kh + 1 are
+    // two 16-byte reads 256 bytes apart.
+    auto run32 = [&](auto ctw_tag, int toff) {
+        constexpr int CTW = decltype(ctw_tag)::value;
+        constexpr int NG = CTW / 2;
+        constexpr bool ODD = (CTW & 1) != 0;
+        const int c32 = lane & 31, kh = lane >> 5;
+        float sbg[NG], sbo = 0.0f;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            sbg[g] = 0.0f;
+            if (SCM == 0) {
+                const int t = min(t0 + toff + 2 * g + (c32 >> 4), a.ntiles - 1);
+                sbg[g] = reinterpret_cast<const float*>(a.S)[(size_t)t * a.ngrp * 16 + (c32 & 15)];
+                asm volatile("" ::"v"(sbg[g]));
+            }
+        }
+        if (ODD && SCM == 0) {
+            sbo = reinterpret_cast<const float*>(a.S)[(size_t)min(t0 + toff + CTW - 1, a.ntiles - 1) * a.ngrp * 16 + col];
+            asm volatile("" ::"v"(sbo));
+        }
+        float acc[NG][16], acco[2][4];
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acco[r][i] = 0.0f;
+
+        // dma_tag: 0 no loads, 1 or 2 the loads of chunk 0 or 1 of the next
+        // stage (c_next, at LDS nbase).
+        auto compute = [&](const char* cp, auto nb_tag, auto dma_tag, int c_next, uint32_t nbase) {
+            constexpr int NB = decltype(nb_tag)::value;
+            constexpr bool DMA = decltype(dma_tag)::value != 0;
+            constexpr bool FIRST = decltype(dma_tag)::value == 1;
+            constexpr int kAhead = 1;            // groups read ahead
+            constexpr int NGB = NG * NB;         // group steps
+            constexpr int NS = NGB + (ODD ? NB : 0);
+            const char* ar = cp + L::kA + 2 * rp * kRecBytes;
+            v4i a_h[2], a_l[2];
+            float sa[2][16];
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                // Two 8-byte halves 256 bytes apart: one ds_read2_b64 into
+                // the operand's four registers.
+                const char* rb = ar + (c32 >> 4) * kRecBytes + b * 1024 + 16 * ((c32 & 15) + 32 * kh);
+                const uint2 h0 = *reinterpret_cast<const uint2*>(rb), h1 = *reinterpret_cast<const uint2*>(rb + 256);
+                const uint2 l0 = *reinterpret_cast<const uint2*>(rb + 8), l1 = *reinterpret_cast<const uint2*>(rb + 264);
+                a_h[b] = v4i{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y};
+                a_l[b] = v4i{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    // rows 8q + 4kh .. +3: record (q >> 1), row 8 (q & 1) + 4 kh
+                    const float4 s4 = *reinterpret_cast<const float4*>(ar + (q >> 1) * kRecBytes + kRecA + b * 64 +
+                                                                       4 * (8 * (q & 1) + 4 * kh));
+                    sa[b][4 * q] = s4.x;
+                    sa[b][4 * q + 1] = s4.y;
+                    sa[b][4 * q + 2] = s4.z;
+                    sa[b][4 * q + 3] = s4.w;
+                }
+            }
+            // The odd tile: 16x16x32 operands, as in the path above, read at
+            // the last group step (its registers are free by then).
+            uint64_t ah[2][2], al[2][2];
+            float so[2][2][4];
+            uint4 bwo = make_uint4(0, 0, 0, 0);
+            int2 wso = make_int2(0, 0);
+            float sbo2[2] = {0.0f, 0.0f};
+            auto load_odd = [&]() {
+                if (!ODD) return;
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        const uint4 q = *reinterpret_cast<const uint4*>(ar + r * kRecBytes + b * 1024 + 16 * lane);
+                        ah[r][b] = (uint64_t)q.y << 32 | q.x;
+                        al[r][b] = (uint64_t)q.w << 32 | q.z;
+                        const float4 s4 = *reinterpret_cast<const float4*>(ar + r * kRecBytes + kRecA + b * 64 + 16 * grp);
+                        so[r][b][0] = s4.x;
+                        so[r][b][1] = s4.y;
+                        so[r][b][2] = s4.z;
+                        so[r][b][3] = s4.w;
+                    }
+                const int t = toff + CTW - 1;
+                bwo = *reinterpret_cast<const uint4*>(cp + t * 1024 + 16 * lane);
+                if (HP) wso = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * col);
+                if (SCM == 2) {
+                    const float2 f = *reinterpret_cast<const float2*>(cp + L::kSB + t * 128 + 8 * col);
+                    sbo2[0] = f.x;
+                    sbo2[1] = f.y;
+                } else if (SCM == 1) {
+                    sbo2[0] = sbo2[1] = *reinterpret_cast<const float*>(cp + L::kSB + t * 64 + 4 * col);
+                } else {
+                    sbo2[0] = sbo2[1] = sbo;
+                }
+            };
+            v4i bq[NG][2];  // B operand per group and block
+            int2 wsg[NG];
+            float sbv[NG][2];
+            auto load_group = [&](int g) {
+                if (g >= NG) return;
+                const int t = toff + 2 * g + (c32 >> 4);
+                const char* bp = cp + t * 1024 + 16 * ((c32 & 15) + 32 * kh);
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    const uint2 lo = *reinterpret_cast<const uint2*>(bp + 8 * b);
+                    const uint2 hi = *reinterpret_cast<const uint2*>(bp + 256 + 8 * b);
+                    bq[g][b] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+                }
+                if (HP) wsg[g] = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * (c32 & 15));
+                if (SCM == 2) {
+                    const float2 f = *reinterpret_cast<const float2*>(cp + L::kSB + t * 128 + 8 * (c32 & 15));
+                    sbv[g][0] = f.x;
+                    sbv[g][1] = f.y;
+                } else if (SCM == 1) {
+                    sbv[g][0] = sbv[g][1] = *reinterpret_cast<const float*>(cp + L::kSB + t * 64 + 4 * (c32 & 15));
+                } else {
+                    sbv[g][0] = sbv[g][1] = sbg[g];
+                }
+            };
+            auto bop32 = [&](int g, int b) -> v4i { return bq[g][b]; };
+            auto bopo = [&](int b) -> uint64_t {
+                return b == 0 ? ((uint64_t)bwo.y << 32 | bwo.x) : ((uint64_t)bwo.w << 32 | bwo.z);
+            };
+            v16i h32[NGB], d32[NGB];
+            v4i ho[2][2], dov[2][2];
+            const v16i z16 = {};
+            auto step_h = [&](int s) {
+                if (!HP || s >= NS) return;
+                if (s < NGB) {
+                    h32[s] = mfma32(a_h[s % NB], bop32(s / NB, s % NB), z16);
+                } else {
+                    const int b = s - NGB;
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) ho[b][r] = mfma16(ah[r][b], bopo(b));
+                }
+            };
+            auto step_d = [&](int s) {
+                if (s >= NS) return;
+                if (s < NGB) {
+                    const int g = s / NB, b = s % NB;
+                    if (HP) {
+                        const int s128 = b == 0 ? wsg[g].x : wsg[g].y;
+                        v16i ci;
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) ci[j] = (h32[s][j] << 8) + s128;
+                        d32[s] = mfma32(a_l[b], bop32(g, b), ci);
+                    } else {
+                        d32[s] = mfma32(a_h[b], bop32(g, b), z16);
+                    }
+                } else {
+                    const int b = s - NGB;
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        if (HP) {
+                            const int s128 = b == 0 ? wso.x : wso.y;
+                            const v4i ci = {(ho[b][r][0] << 8) + s128, (ho[b][r][1] << 8) + s128,
+                                            (ho[b][r][2] << 8) + s128, (ho[b][r][3] << 8) + s128};
+                            dov[b][r] = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)al[r][b], (long)bopo(b), ci, 0, 0, 0);
+                        } else {
+                            dov[b][r] = mfma16(ah[r][b], bopo(b));
+                        }
+                    }
+                }
+            };
+            auto step_e = [&](int s) {
+                if (s < NGB) {
+                    const int g = s / NB, b = s % NB;
+#pragma unroll
+                    for (int j = 0; j < 16; ++j)
+                        acc[g][j] = __builtin_fmaf(sa[b][j], (float)d32[s][j] * sbv[g][b], acc[g][j]);
+                } else {
+                    const int b = s - NGB;
+#pragma unroll
+                    for (int r = 0; r < 2; ++r)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            acco[r][i] = __builtin_fmaf(so[r][b][i], (float)dov[b][r][i] * sbo2[b], acco[r][i]);
+                }
+            };
+            // Depth-1 pipeline (registers: 16 accumulators per group): step
+            // s issues step s+1's h-byte MFMA, runs its own epilogue, which
+            // covers that MFMA's latency, then step s+1's shift-add and
+            // l-byte MFMA.
+#pragma unroll
+            for (int g = 0; g < kAhead; ++g) load_group(g);
+            if (NGB == 0) load_odd();
+            step_h(0);
+            step_d(0);
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                if (s < NGB && s % NB == 0) load_group(s / NB + kAhead);
+                if (s == NGB - 1) load_odd();
+                if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s, FIRST);
+                step_h(s + 1);
+                step_e(s);
+                step_d(s + 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (DMA) {
+#pragma unroll
+                for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d, FIRST);
+            }
+        };
+
+        static_assert(kPfChunks == 2, "stage loop");
+        constexpr std::integral_constant<int, 2> two{};
+        constexpr std::integral_constant<int, 1> one{};
+        constexpr std::integral_constant<int, 1> dma0{};
+        constexpr std::integral_constant<int, 2> dma1{};
+        constexpr std::integral_constant<int, 0> no_dma{};
+        issue_stage(0, 0);
+        for (int g = 0; g + 1 < nst; ++g) {
+            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+            lds_barrier();
+            if (BITS == 4) {
+                expand(g & 1);
+                lds_barrier();
+            }
+            const uint32_t nbase = lds0 + (uint32_t)(((g + 1) & 1) * L::kStage);
+            const int cn = (g + 1) * kPfChunks;
+            if (active) {
+                const char* sp = pf_lds + (g & 1) * L::kStage;
+                compute(sp, two, dma0, cn, nbase);
+                compute(sp + L::kChunk, two, dma1, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk);
+            } else {
+                issue_stage(g + 1, (g + 1) & 1);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(vm_wait(0));
+        lds_barrier();
+        if (BITS == 4) {
+            expand((nst - 1) & 1);
+            lds_barrier();
+        }
+        if (!active) return;
+        {
+            const char* sp = pf_lds + ((nst - 1) & 1) * L::kStage;
+            const int c0 = (nst - 1) * kPfChunks;
+            if (c0 + 1 < nch) {
+                compute(sp, two, no_dma, 0, 0u);
+                if (odd) compute(sp + L::kChunk, one, no_dma, 0, 0u);
+                else compute(sp + L::kChunk, two, no_dma, 0, 0u);
+            } else if (odd) {
+                compute(sp, one, no_dma, 0, 0u);
+            } else {
+                compute(sp, two, no_dma, 0, 0u);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            const int tile = t0 + toff + 2 * g + (c32 >> 4);
+            if (tile >= a.ntiles) continue;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const int m = rt0 * 16 + (j & 3) + 8 * (j >> 2) + 4 * kh;
+                if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + (c32 & 15)] = acc[g][j];
+            }
+        }
+        if (ODD) {
+            const int tile = t0 + toff + CTW - 1;
+            if (tile < a.ntiles) {
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int m = (rt0 + r) * 16 + 4 * grp + i;
+                        if (m < a.M) a.C[(size_t)m * a.N + tile * 16 + col] = acco[r][i];
+                    }
+            }
+        }
+    };
+    if (half == 0) run32(std::integral_constant<int, (CT + 1) / 2>{}, 0);
+    else run32(std::integral_constant<int, CT / 2>{}, (CT + 1) / 2);
+}
+
+
+template <int BITS, bool HP, int SCM, int CT>
+hipError_t launch_pf_t(bool* pf_attr, const PfArgs& p, dim3 grid, hipStream_t st) {
+    using L = PfLayout<CT, SCM, BITS>;
+    auto kern = prefill_kernel<BITS, HP, SCM, CT>;
+    int slot = 0;
+    while (kPfCts[slot] != CT) ++slot;
+    const int key = (HP ? 1 : 0) | SCM << 1 | slot << 3 | (BITS == 4 ? 32 : 0);
+    if (!pf_attr[key]) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
+        if (e != hipSuccess) return e;
+        pf_attr[key] = true;
+    }
+    kern<<<grid, kPfWaves * 64, L::kBytes, st>>>(p);
+    return hipGetLastError();
+}
+
+template <int BITS, bool HP, int SCM>
+hipError_t launch_pf_scm(bool* pf_attr, const PfArgs& p, int ct, dim3 grid, hipStream_t st) {
+    switch (ct) {
+        case 17: return launch_pf_t<BITS, HP, SCM, 17>(pf_attr, p, grid, st);
+        case 16: return launch_pf_t<BITS, HP, SCM, 16>(pf_attr, p, grid, st);
+        case 8: return launch_pf_t<BITS, HP, SCM, 8>(pf_attr, p, grid, st);
+        default: return launch_pf_t<BITS, HP, SCM, 4>(pf_attr, p, grid, st);
+    }
+}
+
+template <int BITS, bool HP>
+hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int ct, dim3 grid, hipStream_t st) {
+    if (scm == 2) return launch_pf_scm<BITS, HP, 2>(pf_attr, p, ct, grid, st);
+    if (scm == 1) return launch_pf_scm<BITS, HP, 1>(pf_attr, p, ct, grid, st);
+    return launch_pf_scm<BITS, HP, 0>(pf_attr, p, ct, grid, st);
+}
+
+}  // namespace bq

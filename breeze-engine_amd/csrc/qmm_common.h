@@ -1,0 +1,404 @@
+// qmm_common.h -- what the translation units of libbreeze_qmm.so share: the
+// handle and its device layout, the device helpers (quantizer, operand
+// unpacking, MFMA wrappers), the decode and prefill kernels' argument
+// structs and LDS layouts, and the launchers each kernel unit exports.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstdlib>
+#include <type_traits>
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+namespace bq {
+
+// ------------------------------------------------------------------ layout
+
+// Device weight layout: chunk (t, c) of 16-column tile t is 64 lanes x 16
+// bytes; lane l serves column 16t + (l & 15) and k-octet (l >> 4) of each
+// block -- the B operand of v_mfma_i32_16x16x32_i8, in natural k order.
+//   INT8: 2 blocks per chunk, 8 signed bytes (raw ^ 0x80) per block.
+//   INT4: 4 blocks per chunk, one dword per block whose byte b holds the
+//         nibbles of k = 8*octet + b (low) and k = 8*octet + 4 + b (high), so
+//         `w & 0x0F0F0F0F` and `(w >> 4) & 0x0F0F0F0F` are k 0..3 and 4..7.
+// Activation record per (row, block): 64 bytes, part 0 then part 1, each 32
+// bytes in natural k order: INT16 mode h then l (signed halves), INT8 mode q
+// then zeros.
+
+constexpr uint32_t kMagic = 0xB2EE2E51u;
+constexpr int kFlagZp = 1, kFlagDl = 2, kFlagScBlk = 4;
+
+struct Handle {
+    uint32_t magic;
+    int N, K, nblk, bits;  // bits of the device representation
+    int nbg;               // 16-byte chunks per tile along K
+    int nblk_pad;          // nbg * blocks per chunk
+    int nblk4;             // nblk rounded up to 4
+    int sc_shift, ngrp, sc_group;
+    bool sc_blk;           // scales stored per block [N][nblk_pad]
+    bool has_zp, has_dl;   // explicit zero points / legacy corr supplied
+    bool extra;            // per-block scale, zp (INT4) and corr arrays materialized
+    int device;
+    uint4* W;    // [N/16][nbg][64] 16-byte chunks
+    float* S;    // [N][ngrp], or [N][nblk_pad] when sc_blk
+    int8_t* Z;   // [N][nblk4] zero points (INT4 extra handles only)
+    int32_t* D;  // [N][nblk_pad] legacy corr delta (extra handles only)
+    int32_t* WS; // INT8 handles: 128 * per-block weight sums, [N/16][nbg][16][2]
+    size_t dev_bytes;
+};
+
+// Per-column metadata is tile-major, so the 16 columns a lane group reads
+// for one chunk are contiguous:
+//   scales (per column or per group of 2^sc_shift blocks): [N/16][ngrp][16];
+//   per-block arrays of EXTRA handles, JG blocks per chunk:
+//     scales, corr delta: [N/16][nbg][16][JG]; INT4 zero points: [N/16][nbg][16][4] bytes.
+__host__ __device__ inline size_t grp_index(int n, int j, int ngrp, int sc_shift) {
+    return ((size_t)(n >> 4) * ngrp + (j >> sc_shift)) * 16 + (n & 15);
+}
+__host__ __device__ inline size_t blk_index(int n, int j, int nbg, int JG) {
+    return (((size_t)(n >> 4) * nbg + j / JG) * 16 + (n & 15)) * JG + j % JG;
+}
+
+// ------------------------------------------------------------------ device helpers
+
+__device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
+__device__ inline int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
+__device__ inline int dpp_mirror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
+
+// max over the 8 lanes of an aligned lane octet.  Inputs are +0 or more and
+// never NaN, so their bit patterns order as the floats do.
+__device__ inline float max8(float xf) {
+    int x = __float_as_int(xf);
+    x = max(x, dpp_xor1(x));
+    x = max(x, dpp_xor2(x));
+    return __int_as_float(max(x, dpp_mirror8(x)));
+}
+
+__device__ inline int sum8(int x) {
+    x += dpp_xor1(x);
+    x += dpp_xor2(x);
+    return x + dpp_mirror8(x);
+}
+
+// Quantizes one 32-block with 8 lanes, 4 consecutive k per lane (lane e of
+// the octet holds k = 4e..4e+3).  All 64 lanes of the wave must call it.
+// Returns the block scale and sum(q) in every lane of the octet, and this
+// lane's 4 bytes of record part 0 and part 1.
+template <bool HP>
+__device__ inline void quant8(float4 v, float& s_out, int& sum_out, uint32_t& p0, uint32_t& p1) {
+    const float x[4] = {v.x, v.y, v.z, v.w};
+    // amax over the block from +0 with NaNs skipped, as the reference's
+    // `a > amax ? a : amax` does.  fmaxf returns the other operand of a quiet
+    // NaN; canonicalizing first makes every NaN quiet, and the +0 operand
+    // keeps a lane whose values are all NaN at 0.
+    const float a0 = fabsf(__builtin_canonicalizef(x[0])), a1 = fabsf(__builtin_canonicalizef(x[1]));
+    const float a2 = fabsf(__builtin_canonicalizef(x[2])), a3 = fabsf(__builtin_canonicalizef(x[3]));
+    float amax = fmaxf(fmaxf(fmaxf(a0, a1), 0.0f), fmaxf(a2, a3));
+    amax = max8(amax);
+    constexpr int qmax = HP ? 32767 : 127;
+    const float s = amax / (float)qmax;
+    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+    int sum = 0;
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float prod = x[i] * inv;
+        int q = 0;
+        if (__builtin_isfinite(prod)) {
+            q = (int)rintf(prod);
+            q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
+        }
+        sum += q;
+        if (HP) {
+            const uint32_t u = (uint32_t)(q + 32768);
+            w0 |= (((u >> 8) ^ 0x80u) & 0xFFu) << (8 * i);
+            w1 |= (((u & 0xFFu) ^ 0x80u) & 0xFFu) << (8 * i);
+        } else {
+            w0 |= ((uint32_t)q & 0xFFu) << (8 * i);
+        }
+    }
+    s_out = s;
+    sum_out = sum8(sum);
+    p0 = w0;
+    p1 = w1;
+}
+
+__device__ inline uint64_t unpack_b(const uint4& w, int jb, int bits) {
+    if (bits == 8) {
+        const uint32_t lo = jb == 0 ? w.x : w.z, hi = jb == 0 ? w.y : w.w;
+        return (uint64_t)hi << 32 | lo;
+    }
+    const uint32_t x = jb == 0 ? w.x : jb == 1 ? w.y : jb == 2 ? w.z : w.w;
+    return (uint64_t)((x >> 4) & 0x0F0F0F0Fu) << 32 | (x & 0x0F0F0F0Fu);
+}
+
+__device__ inline v4i mfma16(uint64_t a, uint64_t b) {
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8((long)a, (long)b, v4i{0, 0, 0, 0}, 0, 0, 0);
+}
+
+// v_mfma_i32_16x16x64_i8: A byte i of lane l multiplies B byte i of lane
+// (column + 16 * (l >> 4)), so a lane's first 8 bytes pair with the first
+// block of a decode chunk's block pair and its last 8 bytes with the second
+// (the decode parity tests with one and two rows pin this pairing: any other
+// would change the exact block sums).
+// v_mfma_i32_32x32x32_i8 (full INT8 rate, one 32-block of k): A byte i of
+// lane l is row l & 31, k 16 * (l >> 5) + i; B byte i of lane l is k
+// 16 * (l >> 5) + i, column l & 31; result j of lane l is row
+// (j & 3) + 8 * (j >> 2) + 4 * (l >> 5), column l & 31.
+typedef int v16i __attribute__((ext_vector_type(16)));
+__device__ inline v16i mfma32(const v4i& a, const v4i& b, const v16i& c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ inline v4i mfma64(const uint4& a, const uint4& b) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(v4i{(int)a.x, (int)a.y, (int)a.z, (int)a.w},
+                                                   v4i{(int)b.x, (int)b.y, (int)b.z, (int)b.w},
+                                                   v4i{0, 0, 0, 0}, 0, 0, 0);
+}
+
+
+// ------------------------------------------------------------------ decode GEMV (M <= 8)
+//
+// One workgroup of 16 waves per CU owns a contiguous range of 16-column
+// tiles for up to 4 activation rows (M 5..8: one workgroup per row group of
+// 4, the pair placed on the same XCD so the second read of every weight
+// chunk hits its L2).  Waves 0..14 produce: a tile's K range is cut into
+// phases of 15 chunks and producer w takes chunk 15p + w of phase p, so
+// every producer streams its weights in K order and the chunks of a phase
+// arrive together.  Per phase each producer runs the MFMA and the in-lane
+// epilogue of its chunk and writes f = f32(cs) * scale to an LDS phase
+// buffer.  Wave 15 loads no weights: after each phase's workgroup barrier
+// it folds that phase's blocks in order, acc = fma(s, f, acc), while the
+// producers work on the next phase (two phase buffers), and it writes C at
+// each tile end.  The phase buffer holds each output lane's f values
+// contiguously, so the fold of a full phase is wide LDS reads and one FMA
+// per block.
+//
+// Weight chunks are loaded R units ahead through a register ring; the first
+// R units go out at kernel start, behind only the activation loads, and
+// stream in while the activations are quantized into LDS (FUSED) or their
+// records, made by the stand-alone quantizer, are copied there.  Every load
+// is unconditional (units past the end re-read the last tile) and the ring is
+// unrolled, so the compiler's load waits stay exact across the loop back
+// edge.
+
+constexpr int kDecWaves = 16;
+constexpr int kChainWave = kDecWaves - 1;
+constexpr int kProducers = kDecWaves - 1;
+// The quantizing prologue (8 lanes per 32-block) runs on the first eight
+// waves when two passes of 64 blocks cover the activations: the last waves
+// of a workgroup start up to ~0.3 us after the first, and the prologue
+// barrier waits for the slowest quantizer.  More blocks take all sixteen
+// waves (at most kQuantPasses passes of 128).
+constexpr int kQuantEarlyBlocks = 128, kQuantPasses = 4;
+
+struct GemvArgs {
+    const uint4* W;
+    const float* S;
+    const int8_t* Z;
+    const int32_t* D;
+    const float* A;        // fp32 [M][K]
+    const uint8_t* Aq;     // [M][nblk][64] records (stand-alone quantizer)
+    const float* Sa;       // [M][nblk4]
+    const int* Sq;         // [M][nblk4]
+    float* C;              // [M][N]
+    int32_t* Cs;           // [M][N][nblk] (block-dot export)
+    int64_t* idx;              // [M] argmax, or NULL
+    unsigned int* ticket;      // with idx: workgroups done (0 between calls)
+    unsigned long long* key;   // with idx: [8] merged argmax keys (0 between calls)
+    // Second weight set for the gate/up pairing, in the same layout as W, S,
+    // Z, D (same N, K, bits and scale grouping).
+    const uint4* W2;
+    const float* S2;
+    const int8_t* Z2;
+    const int32_t* D2;
+    int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
+    int ntiles, NG, RG, pair_xcd;
+};
+
+// One weight chunk of a wave plus its per-column metadata.  EXTRA handles
+// (explicit zero points, legacy corr, scale groups smaller than a chunk)
+// carry materialized per-block arrays so every load is unconditional.
+template <int JG, bool EXTRA>
+struct Unit {
+    uint4 w;
+    float sc[EXTRA ? JG : 1];
+    int dl[EXTRA ? JG : 1];
+    uint32_t zp;  // INT4 zero points, one byte per block
+    int c;        // chunk to compute; nbg or more: none (past the end)
+};
+
+__device__ inline unsigned long long argmax_key(float v, int idx) {
+    uint32_t o;
+    if (v != v) {
+        o = 0xFFFFFFFFu;
+    } else if (v == 0.0f) {
+        o = 0x80000000u;
+    } else {
+        const uint32_t b = __float_as_uint(v);
+        o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    }
+    return (unsigned long long)o << 32 | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// Barrier that orders LDS only: outstanding global loads stay in flight.
+__device__ inline void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// f row pitch (floats) of the phase buffer: 15 chunks of JG blocks plus
+// padding that keeps the JG-wide stores and reads free of bank conflicts.
+__host__ __device__ constexpr int dec_pitch(int JG) { return kProducers * JG + (JG == 4 ? 8 : 4); }
+
+// LDS layout of the decode kernel for Mr_max activation rows per workgroup.
+// The host sizes the launch with it and the kernel rebuilds it from its
+// preloaded arguments.  With more than one row the row pitches are padded
+// so the rows read by one lane group fall on different banks: records 64 B
+// past a multiple of 256 B, block scales and sums 16 B past one.
+struct DecLds {
+    int rec_pitch;  // bytes per activation row of records
+    int sa_pitch;   // elements per row of block scales / sums
+    int recs, sa, sq, consts, fbuf, total;  // byte offsets, bytes used
+};
+
+__host__ __device__ inline int lds_take(int& off, int bytes) {
+    const int o = off;
+    off += (bytes + 15) / 16 * 16;
+    return o;
+}
+
+// P64 (one or two rows, block pairs per MFMA): each 8-byte k-octet of a
+// record sits in a 16-byte slot behind 8 zero bytes, 128 B per block plus
+// one zero slot at the row end, so one 16-byte read yields [octet | zeros]
+// or [zeros | octet]; the row pitch of the second row is 32 B past a
+// multiple of 256 B.
+__host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG, bool p64 = false) {
+    DecLds l;
+    // The 16x16x32 layout stores whole chunks ([h, l][k-octet][block]), so a
+    // row spans every chunk, padding blocks included.
+    l.rec_pitch = p64 ? nblk * 128 + 16 : (nblk + JG - 1) / JG * JG * 64;
+    l.sa_pitch = (nblk + 3) / 4 * 4;
+    if (Mr_max > 1) {
+        l.rec_pitch = p64 ? (l.rec_pitch + 223) / 256 * 256 + 32 : (l.rec_pitch + 191) / 256 * 256 + 64;
+        l.sa_pitch = (l.sa_pitch + 59) / 64 * 64 + 4;
+    }
+    int off = 0;
+    l.recs = lds_take(off, Mr_max * l.rec_pitch);
+    l.sa = lds_take(off, Mr_max * l.sa_pitch * 4);
+    l.sq = lds_take(off, Mr_max * l.sa_pitch * 4);
+    l.consts = lds_take(off, 512);
+    l.fbuf = lds_take(off, 2 * 64 * dec_pitch(JG) * 4);
+    l.total = off;
+    return l;
+}
+
+// Ring depth R (weight units in flight per wave).  Two units per producer
+// (30 KB per CU) measured fastest on every decode workload: deeper rings
+// put more requests in flight than the memory system turns into bandwidth.
+constexpr int kDecRing = 2;
+
+constexpr int kLdsMax = 160 * 1024;
+
+// ------------------------------------------------------------------ prefill GEMM (M > 8)
+//
+// One workgroup of 8 waves computes 128 rows x 16*CT columns over all of K.
+// Wave w owns rows 32 (w & 3) .. +31 and column half w >> 2 (the first
+// (CT+1)/2 tiles or the other CT/2), so each SIMD holds one wave of each
+// half.  Per 32-block, H = sum(h*b) comes from one MFMA, (H << 8) + 128*S is
+// the accumulator input of the l-byte MFMA, which then holds the exact block
+// integer cs, and the lane folds acc = fma(s_a, f32(cs) * s_b, acc) in block
+// order.  Pairs of tiles run on v_mfma_i32_32x32x32_i8, an odd last tile on
+// v_mfma_i32_16x16x32_i8.
+//
+// Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4,
+// 16 bytes per lane to LDS address M0 + 16*lane) through a ring of
+// kPfStages stages.  A stage holds one chunk (two blocks): the CT weight
+// tiles (1 KB each; the decode layout is the MFMA B operand), their weight
+// sums and scales (the shared part, loaded by all waves together), and each
+// wave's activation record.  The compiler does not see these loads: every
+// wave waits for its own with an explicit vmcnt, then the workgroup barrier
+// publishes the stage.
+//
+// INT4 weights (BITS 4) take the same core.  A stage is one INT4 chunk (four
+// blocks, 1 KB per tile), loaded raw into chunk 0's weight area; its scales
+// and zero points go to one raw area shared by both stages.  After the
+// stage barrier all 512 threads expand it in place: per byte, b = nibble -
+// zp as a signed byte (n + (128 - zp)) ^ 0x80, chunk 0 getting blocks 0-1
+// and chunk 1 blocks 2-3 in the INT8 chunk layout, plus 128 * sum(b) per
+// (column, block) for the two-pass product and the scales in the INT8
+// chunk layout.  A second barrier publishes the expanded stage.
+
+constexpr int kPfWaves = 8, kPfRows = 16 * kPfWaves;
+// Ring of kPfStages stages of kPfChunks chunks each.
+constexpr int kPfStages = 2, kPfChunks = 2;
+// Activation record per (16-row tile, chunk): [block 2][lane 64][h 8 B, l 8 B]
+// in MFMA A-operand order (lane: row lane&15, k-octet lane>>4), then the
+// block scales [block 2][row 16] float.
+constexpr int kRecA = 2048, kRecBytes = kRecA + 128;
+
+struct PfArgs {
+    const char* W;   // INT8: [ntiles][nch][64 lanes][16 B]; INT4: [ntiles][nbg][64][16 B]
+    const char* WS;  // INT8: [ntiles][nch][16][2] int32
+    const char* S;   // scales (grp_index / blk_index layouts)
+    const char* Z;   // INT4 per-block zero points [ntiles][nbg][16][4] (SCM 2 only)
+    const char* R;   // activation records [Mpad/16][nch][kRecBytes]
+    float* C;        // [M][N]
+    int M, N, nblk, nch, ngrp, sc_shift, ntiles;
+    int nbg;         // INT4: 4-block chunks per tile
+};
+
+// SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
+// One chunk's LDS region: [CT weight tiles, 1 KB each][weight sums, 128 B
+// per tile][block or group scales][8 activation records].  INT4 adds the raw
+// area after the two stages: group scales (SCM 1, 64 B per tile) or block
+// scales then zero points (SCM 2, 256 + 64 B per tile), in whole KB.
+template <int CT, int SCM, int BITS>
+struct PfLayout {
+    static constexpr int kWS = CT * 1024;
+    static constexpr int kSB = kWS + CT * 128;
+    static constexpr int kShared = kSB + (SCM == 2 ? CT * 128 : SCM == 1 ? CT * 64 : 0);
+    static constexpr int kA = kShared;
+    static constexpr int kChunk = kA + kPfWaves * kRecBytes;
+    static constexpr int kStage = kPfChunks * kChunk;
+    static constexpr int kRawZ = CT * 256;  // SCM 2: zero points after the block scales
+    static constexpr int kRawUsed = BITS == 8 ? 0 : SCM == 2 ? CT * 320 : SCM == 1 ? CT * 64 : 0;
+    static constexpr int kRaw = (kRawUsed + 1023) / 1024 * 1024;
+    static constexpr int kRawOff = kPfStages * kStage;
+    // DMA units of 1 KB per stage (INT8: per chunk): INT8 the chunk's shared
+    // part, INT4 the CT raw tiles and the raw area.
+    static constexpr int kUnits = BITS == 8 ? (kShared + 1023) / 1024 : CT + kRaw / 1024;
+    static constexpr int kPerWave = (kUnits + kPfWaves - 1) / kPfWaves;
+    static constexpr int kBytes = kRawOff + kRaw;
+    static_assert(kShared % 64 == 0 && kBytes <= 160 * 1024, "layout");
+};
+
+__device__ inline uint32_t lds_address(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// 16 bytes per lane from global `src` to LDS byte address lds + 16*lane.
+__device__ inline void dma16(const void* src, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
+}
+
+// s_waitcnt immediate: vmcnt(n), no wait on the other counters.
+__host__ __device__ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+
+
+constexpr int kPfCts[] = {17, 16, 8, 4};
+
+// Launchers, one explicit instantiation per (bits, activation mode) in the
+// kernel units dec_w*.hip and pf_w*.hip.  attr_set / pf_attr: this device's
+// flags of kernels whose dynamic LDS limit is already raised.
+template <int BITS, bool HP>
+hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds, bool pair, bool p64, bool fused,
+                           bool extra, hipStream_t st);
+template <int BITS, bool HP>
+hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int ct, dim3 grid, hipStream_t st);
+
+}  // namespace bq

@@ -1,7 +1,8 @@
 """The GPU path inside a captured HIP graph: the per-layer sequence of the
 decoder's MLP (qwen35_decoder.cpp:405-409: gate and up projections, SiLU
 times up, down projection) and the LM head's argmax, captured once after one
-uncaptured call per shape and replayed.  Every replay is checked bit for bit
+uncaptured call per shape on the capturing stream (which sizes that
+stream's device scratch) and replayed.  Every replay is checked bit for bit
 against the same sequence run eagerly on the same inputs, with eager work and
 synchronisations between the replays."""
 import numpy as np
@@ -30,12 +31,15 @@ def test_captured_mlp_block_replays_bit_exact(gpu, hb, hi_prec, rows, bits):
     try:
         hb.set_hi_prec(True)
         inputs = [torch.from_numpy(rng.normal(size=(rows, H)).astype(np.float32)).cuda() for _ in range(4)]
-        want = [_mlp(hb, torch, *hs, x, inter, H) for x in inputs]  # also the uncaptured first calls
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            want = [_mlp(hb, torch, *hs, x, inter, H) for x in inputs]  # also the uncaptured first calls
         torch.cuda.synchronize()
 
         x_static = inputs[0].clone()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=cap):
             y_static = _mlp(hb, torch, *hs, x_static, inter, H)
         for i, x in enumerate(inputs):
             x_static.copy_(x)
@@ -60,11 +64,14 @@ def test_captured_argmax_replays_exact(gpu, hb, hi_prec):
     try:
         hb.set_hi_prec(True)
         inputs = [torch.from_numpy(rng.normal(size=(1, K)).astype(np.float32)).cuda() for _ in range(3)]
-        want = [hb.matmul_argmax(h, x, N) for x in inputs]
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            want = [hb.matmul_argmax(h, x, N) for x in inputs]
         torch.cuda.synchronize()
         x_static = inputs[0].clone()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        with torch.cuda.graph(graph, stream=cap):
             logits, idx = hb.matmul_argmax(h, x_static, N)
         for i, x in enumerate(inputs):
             x_static.copy_(x)

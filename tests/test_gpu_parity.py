@@ -25,12 +25,9 @@ def _run_both(hb, torch, h, A, N):
 
 
 @pytest.mark.parametrize("N,K", [(16, 32), (48, 96), (64, 512), (32, 4096)])
-@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("dtype", [np.float16, np.float32])
-@pytest.mark.parametrize("explicit_zeros", [False, True])
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
 def test_matmul_bit_exact(gpu, hb, orc, hi_prec, N, K, bits, dtype, explicit_zeros):
-    if bits == 8 and explicit_zeros:
-        pytest.skip("INT8 takes no explicit zero points")
     rng = np.random.default_rng(N + K + bits)
     qw, sc, qz = rng_weights(rng, N, K, bits, dtype, explicit_zeros)
     h = hb.prepack(qw, sc, qz, K, N, bits=bits)
@@ -47,11 +44,8 @@ def test_matmul_bit_exact(gpu, hb, orc, hi_prec, N, K, bits, dtype, explicit_zer
         hb.free(h)
 
 
-@pytest.mark.parametrize("bits", [4, 8])
-@pytest.mark.parametrize("explicit_zeros", [False, True])
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
 def test_block_integers_exact(gpu, hb, orc, hi_prec, bits, explicit_zeros):
-    if bits == 8 and explicit_zeros:
-        pytest.skip("INT8 takes no explicit zero points")
     N, K = 64, 1024
     rng = np.random.default_rng(11 + bits)
     qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
@@ -174,11 +168,91 @@ def test_legacy_corr_is_honoured(gpu, hb, orc, hi_prec, bits):
     try:
         for hp in (False, True):
             hb.set_hi_prec(hp)
-            A = rng.normal(size=(5, K)).astype(np.float32)
-            want = orc.matmul_legacy(B, scale, zp, corr, N, K, bits, A, hp)
-            assert bits_equal(hb.matmul(h, A, N), want)
+            # 5 rows: the decode kernel; 9 and 17: the rows kernel's corr
+            # delta in row chunks of 8 (quantized_matmul.cpp:542-550).
+            for rows in (5, 9, 17):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                want = orc.matmul_legacy(B, scale, zp, corr, N, K, bits, A, hp)
+                assert bits_equal(hb.matmul(h, A, N), want), (hp, rows)
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("zp_lo,zp_hi", [(-112, 0), (-112, 16), (-5, 3), (100, 128)])
+def test_legacy_int4_signed_zero_points(gpu, hb, orc, hi_prec, zp_lo, zp_hi):
+    """Legacy INT4 handles keep signed int8 zero points from -112 up
+    (b = nibble - zp never wraps there) with a consistent corr, so they stay
+    INT4 with explicit zero points: the decode kernel (1, 3, 8 rows) and the
+    prefill GEMM's in-LDS nibble expansion (9, 17, 130 rows), whose per-byte
+    n - zp must not borrow across bytes for negative zp.  33 blocks: a
+    partial last 4-block chunk."""
+    N, K = 64, 1056
+    nblk = K // 32
+    rng = np.random.default_rng(zp_lo + 1000)
+    B = rng.integers(0, 256, (N // 16, nblk, 8, 32), dtype=np.uint8)
+    scale = rng.uniform(0.001, 0.02, (N // 16, nblk, 16)).astype(np.float32)
+    zp = rng.integers(zp_lo, zp_hi, (N // 16, nblk, 16)).astype(np.int8)
+    # corr = 128 * sum(b): the oracle's delta against a zero corr.
+    _, _, full = orc.unpack_legacy(B, scale, zp, np.zeros_like(scale, dtype=np.int32), N, K, 4)
+    corr = np.ascontiguousarray(full.reshape(N // 16, 16, nblk).transpose(0, 2, 1)).astype(np.int32)
+    h = hb._lib.i4_prepack(hb._p(B), hb._p(scale), hb._p(zp), hb._p(corr), N, K, nblk, 4)
+    assert h, hb.last_error()
+    try:
+        info = hb.handle_info(h)
+        assert info["bits"] == 4 and not info["has_corr_delta"], info
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for rows in (1, 3, 8, 9, 17, 130):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                A[rng.random(A.shape) < 0.01] *= 20.0
+                want = orc.matmul_legacy(B, scale, zp, corr, N, K, 4, A, hp)
+                got = hb.matmul(h, gpu.from_numpy(A).cuda(), N)
+                gpu.cuda.synchronize()
+                assert bits_equal(got.cpu().numpy(), want), (hp, rows)
+    finally:
+        hb.free(h)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_matmul_region_entry_point(gpu, hb, orc, hi_prec, bits):
+    """i4_matmul_region (quantized_matmul.cpp:558-572) with the caller's
+    scratch (2*M*K bytes) and ascale (M*K/32 floats) buffers, M <= 8 as the
+    reference allows: the same outputs as the oracle, bit for bit."""
+    N, K = 96, 640
+    rng = np.random.default_rng(40 + bits)
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, bits == 4)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        for hp in (False, True):
+            hb.set_hi_prec(hp)
+            for rows in (1, 3, 8):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                C = np.full((rows, N), np.nan, np.float32)
+                scratch = np.zeros(2 * rows * K, np.uint8)
+                ascale = np.zeros(rows * (K // 32), np.float32)
+                hb._lib.i4_matmul_region(hb._vp(h), hb._p(A), rows, hb._p(C), hb._p(scratch), hb._p(ascale))
+                assert hb.last_error() == "", hb.last_error()
+                assert bits_equal(C, orc.matmul(qw, sc, qz, N, K, bits, A, hp)), (hp, rows)
+    finally:
+        hb.free(h)
+
+
+def test_linear_fp16_backend_values(gpu):
+    """breeze_amd.linear on the GPU (fp16 weight and activation, fp32
+    accumulate): within fp16 input rounding of the fp32 product."""
+    from breeze_amd import linear
+
+    assert linear.backend() == "torch-hip-fp16"
+    rng = np.random.default_rng(6)
+    w = rng.normal(size=(512, 96)).astype(np.float32)
+    a = rng.normal(size=(2, 3, 512)).astype(np.float32)
+    out = linear.linear(a, linear.prepare_weight(w))
+    assert out.shape == (2, 3, 96) and out.dtype == np.float32
+    ref = a.astype(np.float64) @ w.astype(np.float64)
+    # Each input rounds to fp16 (relative 2^-11); the products' errors add
+    # up over K = 512 terms of typical size |a||w| ~ 1.
+    err = np.max(np.abs(out - ref)) / np.max(np.abs(ref))
+    assert err < 2e-3, err
 
 
 @pytest.mark.parametrize("bits", [4, 8])
