@@ -76,6 +76,8 @@ try:
     _lib.i4_matmul_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
     _lib.i4_matmul_argmax_dev.restype = _i
     _lib.i4_matmul_argmax_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
+    _lib.i4_matmul_noalloc_dev.restype = _i
+    _lib.i4_matmul_noalloc_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
     _lib.i4_matmul_silu_mul_dev.restype = _i
     _lib.i4_matmul_silu_mul_dev.argtypes = [_vp, _vp, _vp, _i, _vp, _vp]
     _lib.i4_block_dots_dev.restype = _i

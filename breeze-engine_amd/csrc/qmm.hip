@@ -637,6 +637,9 @@ struct Scratch {
     unsigned int* ticket = nullptr;  // decode argmax: ticket counter, then 8 row keys; zero between calls
     float* gate = nullptr;           // gate projection of the unpaired gate/up path
     size_t gate_cap = 0;
+    // Set for i4_matmul_noalloc_dev: the buffers above are carved from the
+    // device's static scratch array and can never grow.
+    bool fixed = false;
 };
 
 struct Workspace {
@@ -669,6 +672,24 @@ Scratch* scratch_for(Workspace& w, hipStream_t st) {
     return s;
 }
 
+// ------------------------------------------------------------------ no-allocation scratch
+//
+// i4_matmul_noalloc_dev takes all of its device scratch from `scratch`, a
+// static array that every device holding this library keeps until the
+// process ends.  Host code never passes the array's name to a kernel (on the
+// host it is only a stand-in for the symbol): each device's own address of
+// it comes from hipGetSymbolAddress, once per device with that device
+// current, and is kept in g_noalloc_ptr.  Layout per call: [0, 256) the
+// decode argmax state (ticket and 8 row keys, cleared by a fill kernel on
+// every call that uses it), then the activation records of this call (the
+// stand-alone quantizer's records, scales and sums, or the prefill
+// records), then the argmax partials.  Calls that overlap on one device
+// share the array and race.
+constexpr size_t kNoAllocBytes = 16u << 20;
+constexpr size_t kNoAllocState = 256;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+uint8_t* g_noalloc_ptr[kMaxDevices];
+
 __global__ void fill_u32_kernel(uint32_t* __restrict__ p, int n, uint32_t v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
@@ -683,10 +704,17 @@ bool capturing(hipStream_t st) {
     return cs != hipStreamCaptureStatusNone;
 }
 
-// Makes *p hold at least `need` elements for work on stream st.
+// Makes *p hold at least `need` elements for work on stream st.  A fixed
+// scratch (the no-allocation entry point) never grows.
 template <typename T>
-bool grow(Workspace& w, hipStream_t st, T** p, size_t* cap, size_t need, const char* what) {
+bool grow(Workspace& w, hipStream_t st, T** p, size_t* cap, size_t need, const char* what, bool fixed = false) {
     if (need <= *cap) return true;
+    if (fixed) {
+        set_err("%s: this call needs %zu bytes of scratch in one buffer, more than the no-allocation entry "
+                "point's fixed scratch holds for it (%zu bytes)",
+                what, need * sizeof(T), *cap * sizeof(T));
+        return false;
+    }
     if (capturing(st)) {
         set_err("%s: this call needs %zu bytes of device scratch that the stream does not have yet, and "
                 "memory cannot be allocated while the stream is capturing; make one call of this shape "
@@ -705,8 +733,9 @@ bool grow(Workspace& w, hipStream_t st, T** p, size_t* cap, size_t need, const c
 
 bool ensure_quant(Workspace& w, Scratch& s, hipStream_t st, size_t rows, size_t nblk4) {
     const size_t n = rows * nblk4;
-    return grow(w, st, &s.aq, &s.aq_cap, n * 64, "workspace alloc") &&
-           grow(w, st, &s.sa, &s.sa_cap, n, "workspace alloc") && grow(w, st, &s.sq, &s.sq_cap, n, "workspace alloc");
+    return grow(w, st, &s.aq, &s.aq_cap, n * 64, "workspace alloc", s.fixed) &&
+           grow(w, st, &s.sa, &s.sa_cap, n, "workspace alloc", s.fixed) &&
+           grow(w, st, &s.sq, &s.sq_cap, n, "workspace alloc", s.fixed);
 }
 
 // ------------------------------------------------------------------ host helpers
@@ -992,7 +1021,8 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     const int nch_rec = (h->nblk + 1) / 2;  // record chunks of two blocks
     if (pre) {
         // Records in MFMA operand order for the prefill GEMM.
-        if (!grow(w, st, &s.rec, &s.rec_cap, (size_t)(Mpad / 16) * nch_rec * kRecBytes, "workspace alloc")) return -4;
+        if (!grow(w, st, &s.rec, &s.rec_cap, (size_t)(Mpad / 16) * nch_rec * kRecBytes, "workspace alloc", s.fixed))
+            return -4;
         const size_t threads = (size_t)Mpad * nch_rec * 2 * 8;
         const unsigned qb = (unsigned)((threads + 255) / 256);
         if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);
@@ -1030,6 +1060,10 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
             a.D2 = h2->D;
         }
         if (dIdx) {
+            if (!s.ticket && s.fixed) {
+                set_err("internal: fixed scratch without argmax state");
+                return -5;
+            }
             if (!s.ticket) {
                 // Allocated and zeroed once per stream, outside capture; the
                 // kernel's last workgroup re-arms it to zero.
@@ -1096,7 +1130,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     if (dIdx && !dots && !dec) {
         // The decode kernel merges its own argmax (last workgroup).
         const int nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
-        if (!grow(w, st, &s.parts, &s.parts_cap, (size_t)M * nparts, "argmax workspace")) return -4;
+        if (!grow(w, st, &s.parts, &s.parts_cap, (size_t)M * nparts, "argmax workspace", s.fixed)) return -4;
         argmax_partial_kernel<<<dim3(nparts, M), 256, 0, st>>>(dC, h->N, s.parts);
         argmax_final_kernel<<<M, 256, 0, st>>>(s.parts, nparts, M, dIdx);
         if (!hip_ok(hipGetLastError(), "argmax launch")) return -5;
@@ -1358,6 +1392,70 @@ int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC, int64_
     }
     const hipStream_t st = static_cast<hipStream_t>(stream);
     return with_scratch(h, st, [&](Workspace& w, Scratch& s) { return run(w, s, h, dA, M, dC, nullptr, dIdx, st); });
+}
+
+int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream) {
+    Handle* h = as_handle(handle);
+    if (!h) return -1;
+    if (M < 0) {
+        set_err("M must be >= 0 (got %d)", M);
+        return -2;
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    if (dev != h->device) {
+        set_err("handle lives on device %d but device %d is current", h->device, dev);
+        return -3;
+    }
+    if (dev < 0 || dev >= kMaxDevices) {
+        set_err("device ordinal %d out of range", dev);
+        return -3;
+    }
+    Workspace& w = g_ws[dev];
+    std::lock_guard<std::mutex> lock(w.mu);
+    if (!g_noalloc_ptr[dev]) {
+        void* p = nullptr;
+        if (!hip_ok(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "no-allocation scratch address")) return -4;
+        g_noalloc_ptr[dev] = static_cast<uint8_t*>(p);
+    }
+    uint8_t* base = g_noalloc_ptr[dev];
+    // Argmax partials at the end (they follow the matmul launch, so their
+    // room is set aside first), activation records in between.
+    const size_t nparts = dIdx ? (size_t)M * ((h->N + kArgmaxChunk - 1) / kArgmaxChunk) : 0;
+    const size_t parts_bytes = (nparts * sizeof(unsigned long long) + 255) / 256 * 256;
+    if (kNoAllocState + parts_bytes > kNoAllocBytes) {
+        set_err("no-allocation scratch: %d rows of argmax partials need %zu bytes, more than %zu", M, parts_bytes,
+                kNoAllocBytes - kNoAllocState);
+        return -4;
+    }
+    const size_t region = kNoAllocBytes - kNoAllocState - parts_bytes;
+    Scratch s{};
+    s.fixed = true;
+    s.stream = st;
+    s.ticket = reinterpret_cast<unsigned int*>(base);
+    s.parts = reinterpret_cast<unsigned long long*>(base + kNoAllocBytes - parts_bytes);
+    s.parts_cap = parts_bytes / sizeof(unsigned long long);
+    uint8_t* recs = base + kNoAllocState;
+    s.rec = recs;
+    s.rec_cap = region;
+    // Stand-alone quantizer records for this call's rows: [M][nblk4] of 64 B
+    // records, then the scales and sums.
+    const size_t nq = (size_t)M * h->nblk4;
+    if (nq * 72 <= region) {
+        s.aq = recs;
+        s.sa = reinterpret_cast<float*>(recs + nq * 64);
+        s.sq = reinterpret_cast<int*>(recs + nq * 68);
+        s.aq_cap = nq * 64;
+        s.sa_cap = s.sq_cap = nq;
+    }
+    if (dIdx && M > 0) {
+        // The decode argmax merges into this state and needs it zero; a
+        // kernel clears it (a graph may capture this call).
+        fill_u32_kernel<<<1, 64, 0, st>>>(s.ticket, 18, 0u);
+        if (!hip_ok(hipGetLastError(), "argmax state clear")) return -5;
+    }
+    return run(w, s, h, dA, M, dC, nullptr, dIdx, st);
 }
 
 int i4_block_dots_dev(void* handle, const float* dA, int M, int32_t* dCs, void* stream) {

@@ -100,6 +100,20 @@ int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC,
  * elementwise kernel with the same arithmetic.  Returns as i4_matmul_dev. */
 int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* dC, void* stream);
 
+/* i4_matmul_dev, or i4_matmul_argmax_dev when dIdx is not NULL, that
+ * allocates nothing: no hipMalloc, hipFree or allocating library call.  It
+ * has no counterpart in the reference; it is for callers that cannot
+ * allocate, such as code under HIP graph capture or serving loops that
+ * forbid it.  All of its device scratch is one static 16 MiB array per
+ * device, so a call whose activation records do not fit is refused (-4,
+ * i4_last_error() says why): about 72 bytes per row and 32-block of K when
+ * the decode kernel stages its records (up to 8 rows, M*K above 16384), and
+ * about 68 bytes per 32-block of K per row, rows rounded up to 128, for
+ * more than 8 rows.  Calls that overlap on one device share the array and
+ * race: serialize them.  Outputs are those of i4_matmul_dev /
+ * i4_matmul_argmax_dev, bit for bit. */
+int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream);
+
 /* Handle facts: out[0..7] = N, K, bits, scale group (blocks per distinct
  * scale, 0 = one per column), has_zero_points, has_corr_delta,
  * device bytes held, device ordinal.  Returns 0 or -1. */
