@@ -11,9 +11,17 @@ over >= 512 MB of copies so no call is served from the 256 MB last-level
 cache.  The other workloads are timed the same way and reported under
 ``workloads``.
 
+Each workload: prepack, one untimed call per weight copy, the warmup
+calls, synchronize, then the timed calls between two HIP events on the
+library's stream (a short spin kernel ahead of the first event keeps the
+host's first enqueue out of the region), synchronize.  The other workloads
+run first and the headline last, on a GPU that has been busy.
+
 ``cpu_baseline`` times the reference CPU kernel (kernel/quantized_matmul.cpp
 of breeze-engine, compiled from its own source into oracle/_ref) on this
-host's cores for the same workload; without it, the oracle's scalar C port.
+host's cores for every workload (oracle/cpu_bench.py, a child process with
+the reference benchmark's OpenMP placement, one thread per physical core of
+the GPU's NUMA node); without that build, the oracle's scalar C port.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
                        [--no-cpu-baseline] [--workload NAME[:ROWS]]
@@ -49,6 +57,18 @@ def _handles(hb, d, min_bytes):
             for _ in range(n)]
 
 
+def gate(torch, stream):
+    """Holds the stream for ~0.1-1 ms with a spin kernel ahead of the timed
+    region, so the host has enqueued the first timed calls before the GPU
+    reaches them.  Without it, the region would start on an idle GPU and
+    count the host's first ctypes enqueue (a few us) once per region, which
+    at 20 steps adds ~5% to a 7.5 us call: the timed calls then measure
+    the back-to-back rate of a loop whose host stays ahead of the GPU, as
+    in serving.  The spin kernel ends before e0 is recorded."""
+    with torch.cuda.stream(stream):
+        torch.cuda._sleep(1_000_000)
+
+
 def time_workload(hb, torch, name, rows, steps, warmup, argmax=False):
     """Per-call time (s) of one workload: `warmup` untimed calls, then
     `steps` calls bracketed by synchronisation and HIP events on the stream
@@ -73,12 +93,19 @@ def time_workload(hb, torch, name, rows, steps, warmup, argmax=False):
         def call(h):
             return lib.i4_matmul_dev(hb._vp(h), ap, M, op, sp)
     try:
+        # One untimed call per weight copy first: the first touch of each
+        # copy's pages (and TLB entries) is set-up, not a step.  Then the
+        # `warmup` steps.
+        for h in hs:
+            if call(h) != 0:
+                raise RuntimeError(f"{name}: {hb.last_error()}")
         for i in range(warmup):
             if call(hs[i % len(hs)]) != 0:
                 raise RuntimeError(f"{name}: {hb.last_error()}")
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        gate(torch, stream)
         e0.record(stream)
         for i in range(steps):
             call(hs[i % len(hs)])
@@ -93,49 +120,70 @@ def time_workload(hb, torch, name, rows, steps, warmup, argmax=False):
             hb.free(h)
 
 
-def cpu_baseline(name):
-    """The reference CPU kernel on this host, same workload, bounded sample:
-    3 warmup calls, then calls until 3 s or 200 calls, whichever comes
-    first."""
-    from breeze_amd import workloads
-    from oracle import oracle
-
-    d = workloads.make_config(name)
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores))))
-    ref = h = None
-    if oracle.ref_available():
-        kind = "reference"
-        ref = oracle.Ref(threads=cores)
-        h = ref.prepack(d["qweight"], d["scales"], None, d["N"], d["K"], d["bits"])
-
-        def run():
-            ref.matmul(h, d["A"], d["N"], hi_prec=True)
-    else:
-        kind, cores = "port", 1
-        orc = oracle.c_oracle()
-
-        def run():
-            orc.matmul(d["qweight"], d["scales"], None, d["N"], d["K"], d["bits"], d["A"], True)
+def gpu_local_cpus(torch):
+    """Logical CPUs of the GPU's NUMA node that this process may use, and
+    how they were found.  Falls back to the whole affinity mask."""
+    allowed = sorted(os.sched_getaffinity(0))
+    note = "affinity mask (GPU NUMA node unknown)"
     try:
-        for _ in range(3):
-            run()
-        n, t0 = 0, time.perf_counter()
-        while n < 200 and (n < 3 or time.perf_counter() - t0 < 3.0):
-            run()
-            n += 1
-        dt = (time.perf_counter() - t0) / n
-    finally:
-        if ref is not None:
-            ref.free(h)
+        p = torch.cuda.get_device_properties(0)
+        bdf = f"{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0"
+        with open(f"/sys/bus/pci/devices/{bdf}/numa_node") as f:
+            node = int(f.read())
+        if node >= 0:
+            with open(f"/sys/devices/system/node/node{node}/cpulist") as f:
+                from oracle.cpu_bench import parse_cpulist
+                local = sorted(parse_cpulist(f.read()) & set(allowed))
+            if local:
+                return local, f"NUMA node {node} of GPU {bdf}, within this process's affinity mask"
+            note = f"affinity mask (none of NUMA node {node}'s CPUs is allowed)"
+        else:
+            note = f"affinity mask (GPU {bdf} reports no NUMA node)"
+    except (OSError, ValueError, AttributeError, RuntimeError) as e:
+        note = f"affinity mask (GPU NUMA node unknown: {type(e).__name__}: {e})"
+    return allowed, note
+
+
+def cpu_baseline(torch):
+    """The reference CPU kernel on this host's cores for every workload, in
+    a child process (oracle/cpu_bench.py) with the reference benchmark's
+    OpenMP placement: one thread per physical core of the GPU's NUMA node,
+    OMP_PROC_BIND=spread, OMP_PLACES=cores, OMP_WAIT_POLICY=active."""
+    import subprocess
+
+    from oracle.cpu_bench import physical_cores
+
+    cpus, where = gpu_local_cpus(torch)
+    T = len(physical_cores(cpus))
+    env = dict(os.environ, OMP_NUM_THREADS=str(T), OMP_PROC_BIND="spread", OMP_PLACES="cores",
+               OMP_WAIT_POLICY="active")
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "oracle", "cpu_bench.py"),
+                        "--cpus", ",".join(map(str, cpus))],
+                       env=env, stdout=subprocess.PIPE, text=True, timeout=900)
+    if r.returncode != 0:
+        raise RuntimeError(f"cpu baseline failed ({r.returncode})")
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    head = next(w for w in res["workloads"] if w["workload"] == workloads_label(HEADLINE))
     return {
-        "value": round(workloads.algorithmic_bytes(name) / dt / 1e9, 2),
+        "value": head["gbs"],
         "unit": "GB/s",
-        "cores": cores,
-        "kind": kind,
-        "sample": f"{workloads.LABELS[name]}, hi-prec mode, {n} timed calls after 3 warmup "
-                  f"({dt * 1e6:.1f} us/call), {cores} OpenMP thread(s)",
+        "cores": res["threads"],
+        "kind": res["kind"],
+        "sample": f"{head['workload']}, hi-prec mode, {head['calls']} timed calls after 3 warmup "
+                  f"({head['us']} us/call); every workload below the same way (at most 20 calls or about "
+                  f"4 s each); threads one per physical core on {where}",
+        "cpu_model": res["cpu_model"],
+        "cpus": res["cpus"],
+        "omp": res["omp"],
+        "build": res["build"],
+        "workloads": res["workloads"],
     }
+
+
+def workloads_label(name, M=None):
+    from breeze_amd import workloads
+
+    return workloads.LABELS[name].format(M=M)
 
 
 RMSNORM_H = 5120
@@ -156,6 +204,7 @@ def time_rmsnorm(hb, torch, rows, steps, warmup):
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    gate(torch, stream)
     e0.record(stream)
     for _ in range(steps):
         hb.rmsnorm(x, w, 1e-6)
@@ -225,6 +274,33 @@ def main():
         print(json.dumps(entry), flush=True)
         return
 
+    rows = None
+    if not args.headline_only:
+        # The other workloads first: the headline is timed last, on a GPU
+        # that has been busy for a while (clocks settled).
+        rows = []
+        # The decode workloads take about 10 us a call: same steps and warmup
+        # as the headline.  The LM head and the prefill GEMMs take 140-300 us:
+        # fewer steps keep the run short.
+        for name, r in (("w8_gemv", None), ("w4_gemv", None), ("w4_decode", 1), ("w4_decode", 2),
+                        ("w4_decode", 4), ("w4_decode", 8), ("w8_lmhead", None), ("w8_prefill", None),
+                        ("w4_prefill", None)):
+            long_call = name in ("w8_lmhead", "w8_prefill", "w4_prefill")
+            t, m = time_workload(hb, torch, name, r, max(10, args.steps // 4) if long_call else args.steps,
+                                 max(3, args.warmup // 4) if long_call else args.warmup,
+                                 argmax=name == "w8_lmhead")
+            entry = {"workload": workloads.LABELS[name].format(M=m), "us": round(t * 1e6, 2)}
+            if name.endswith("prefill"):
+                tops = workloads.algorithmic_ops(name, m) / t / 1e12
+                entry.update(tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
+            else:
+                g = workloads.algorithmic_bytes(name, m) / t / 1e9
+                entry.update(gbs=round(g, 1), frac_hbm_peak=round(g / HBM_PEAK_GBS, 4))
+            rows.append(entry)
+            print(f"bench: {entry}", file=sys.stderr, flush=True)
+        t = time_rmsnorm(hb, torch, 1, args.steps, args.warmup)
+        rows.append({"workload": f"RMSNorm M=1 H={RMSNORM_H} (in-order double sum, exact)", "us": round(t * 1e6, 2)})
+
     t_step, M = time_workload(hb, torch, HEADLINE, None, args.steps, args.warmup)
     nbytes = workloads.algorithmic_bytes(HEADLINE)
     gbs = nbytes / t_step / 1e9
@@ -268,33 +344,11 @@ def main():
             "traffic_source": traffic_note,
         },
     }
-
-    if not args.headline_only:
-        rows = []
-        # The decode workloads take about 10 us a call: same steps and warmup
-        # as the headline.  The LM head and the prefill GEMMs take 140-300 us:
-        # fewer steps keep the run short.
-        for name, r in (("w8_gemv", None), ("w4_gemv", None), ("w4_decode", 1), ("w4_decode", 2),
-                        ("w4_decode", 4), ("w4_decode", 8), ("w8_lmhead", None), ("w8_prefill", None),
-                        ("w4_prefill", None)):
-            long_call = name in ("w8_lmhead", "w8_prefill", "w4_prefill")
-            t, m = time_workload(hb, torch, name, r, max(10, args.steps // 4) if long_call else args.steps,
-                                 max(3, args.warmup // 4) if long_call else args.warmup,
-                                 argmax=name == "w8_lmhead")
-            entry = {"workload": workloads.LABELS[name].format(M=m), "us": round(t * 1e6, 2)}
-            if name.endswith("prefill"):
-                tops = workloads.algorithmic_ops(name, m) / t / 1e12
-                entry.update(tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
-            else:
-                g = workloads.algorithmic_bytes(name, m) / t / 1e9
-                entry.update(gbs=round(g, 1), frac_hbm_peak=round(g / HBM_PEAK_GBS, 4))
-            rows.append(entry)
-        t = time_rmsnorm(hb, torch, 1, args.steps, args.warmup)
-        rows.append({"workload": f"RMSNorm M=1 H={RMSNORM_H} (in-order double sum, exact)", "us": round(t * 1e6, 2)})
+    if rows is not None:
         result["workloads"] = rows
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(HEADLINE)
+        result["cpu_baseline"] = cpu_baseline(torch)
     else:
         result["cpu_baseline"] = None
 
