@@ -186,28 +186,103 @@ def workloads_label(name, M=None):
     return workloads.LABELS[name].format(M=M)
 
 
+# Projections of one activation in the Qwen3.5-27B decoder
+# (kernel/qwen35_decoder.cpp:285-288 and 334-336), W4 group-128 weights.
+MULTI_SHAPES = {
+    "linear-attention in_qkv/in_z/in_b/in_a": (5120, (10240, 6144, 48, 48)),
+    "full-attention q/k/v": (5120, (12288, 1024, 1024)),
+}
+
+
+def time_multi(hb, torch, label, rows, steps, warmup):
+    """Per-call time (s) of the projections of one activation as one
+    i4_matmul_multi_dev launch and as one i4_matmul_dev launch each, timed
+    like the matmul workloads (weights rotated over >= 512 MB)."""
+    import ctypes
+
+    import numpy as np
+
+    from breeze_amd import workloads
+
+    K, Ns = MULTI_SHAPES[label]
+    rng = np.random.default_rng(11)
+    sets = []
+    per_set = sum(N * K // 2 for N in Ns)
+    for _ in range(max(1, -(-ROTATE_BYTES // per_set))):
+        hs = []
+        for N in Ns:
+            qw, sc = workloads.make_weights(rng, 4, N, K, 4)
+            hs.append(hb.prepack(qw, sc, None, K, N, bits=4))
+        sets.append(hs)
+    A = torch.from_numpy(rng.standard_normal((rows, K)).astype(np.float32)).cuda()
+    outs = [torch.empty((rows, N), dtype=torch.float32, device="cuda") for N in Ns]
+    stream = torch.cuda.current_stream()
+    sp, ap = hb._vp(stream.cuda_stream), hb._vp(A.data_ptr())
+    cv = (ctypes.c_void_p * len(Ns))(*[o.data_ptr() for o in outs])
+    hvs = [(ctypes.c_void_p * len(Ns))(*[int(h) for h in hs]) for hs in sets]
+    lib = hb._lib
+
+    def one(i):
+        return lib.i4_matmul_multi_dev(hvs[i % len(sets)], len(Ns), ap, rows, cv, sp)
+
+    def each(i):
+        rc = 0
+        for h, o in zip(sets[i % len(sets)], outs):
+            rc |= lib.i4_matmul_dev(hb._vp(h), ap, rows, hb._vp(o.data_ptr()), sp)
+        return rc
+
+    res = {}
+    try:
+        for key, call in (("one_launch", one), ("per_projection", each)):
+            for i in range(len(sets) + warmup):
+                if call(i) != 0:
+                    raise RuntimeError(f"{label}: {hb.last_error()}")
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            gate(torch, stream)
+            e0.record(stream)
+            for i in range(steps):
+                call(i)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            res[key] = e0.elapsed_time(e1) * 1e-3 / steps
+    finally:
+        for hs in sets:
+            for h in hs:
+                hb.free(h)
+    return res
+
+
 RMSNORM_H = 5120
 
 
 def time_rmsnorm(hb, torch, rows, steps, warmup):
     """Per-call time (s) of the decoder's exact RMSNorm (i4_rmsnorm_dev) on
     `rows` rows of width 5120 (the hidden size of the prefill and LM-head
-    shapes), timed like the matmul workloads.  The kernel is latency-bound on
-    one CU per row, so the rows are few and the time is per call."""
+    shapes), called through the C ABI with preallocated buffers and timed
+    like the matmul workloads."""
     import numpy as np
 
     rng = np.random.default_rng(7)
     x = torch.from_numpy(rng.standard_normal((rows, RMSNORM_H)).astype(np.float32)).cuda()
     w = torch.from_numpy((1 + 0.1 * rng.standard_normal(RMSNORM_H)).astype(np.float32)).cuda()
-    for _ in range(warmup):
-        hb.rmsnorm(x, w, 1e-6)
+    out = torch.empty_like(x)
     stream = torch.cuda.current_stream()
+    sp, xp, wp, op = (hb._vp(v) for v in (stream.cuda_stream, x.data_ptr(), w.data_ptr(), out.data_ptr()))
+    lib = hb._lib
+
+    def call():
+        return lib.i4_rmsnorm_dev(xp, wp, rows, RMSNORM_H, 1e-6, op, sp)
+
+    for _ in range(warmup):
+        if call() != 0:
+            raise RuntimeError(f"rmsnorm: {hb.last_error()}")
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     gate(torch, stream)
     e0.record(stream)
     for _ in range(steps):
-        hb.rmsnorm(x, w, 1e-6)
+        call()
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e-3 / steps
@@ -254,6 +329,13 @@ def main():
 
     if args.workload:
         name, _, r = args.workload.partition(":")
+        if name == "multi":
+            m = int(r) if r else 1
+            for label in MULTI_SHAPES:
+                res = time_multi(hb, torch, label, m, args.steps, args.warmup)
+                print(json.dumps({"workload": f"{label} M={m}", "us": {k: round(v * 1e6, 3) for k, v in res.items()}}),
+                      flush=True)
+            return
         if name == "rmsnorm":
             m = int(r) if r else 1
             t = time_rmsnorm(hb, torch, m, args.steps, args.warmup)
@@ -300,6 +382,15 @@ def main():
             print(f"bench: {entry}", file=sys.stderr, flush=True)
         t = time_rmsnorm(hb, torch, 1, args.steps, args.warmup)
         rows.append({"workload": f"RMSNorm M=1 H={RMSNORM_H} (in-order double sum, exact)", "us": round(t * 1e6, 2)})
+        for label in MULTI_SHAPES:
+            for m in (1, 4):
+                r = time_multi(hb, torch, label, m, args.steps, args.warmup)
+                K, Ns = MULTI_SHAPES[label]
+                rows.append({"workload": f"Qwen3.5-27B {label} W4 group-128, K={K} N={'/'.join(map(str, Ns))}, "
+                                         f"M={m}",
+                             "us_one_launch": round(r["one_launch"] * 1e6, 2),
+                             "us_per_projection": round(r["per_projection"] * 1e6, 2)})
+                print(f"bench: {rows[-1]}", file=sys.stderr, flush=True)
 
     t_step, M = time_workload(hb, torch, HEADLINE, None, args.steps, args.warmup)
     nbytes = workloads.algorithmic_bytes(HEADLINE)

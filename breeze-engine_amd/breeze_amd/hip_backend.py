@@ -78,6 +78,8 @@ try:
     _lib.i4_matmul_argmax_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
     _lib.i4_matmul_noalloc_dev.restype = _i
     _lib.i4_matmul_noalloc_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
+    _lib.i4_matmul_multi_dev.restype = _i
+    _lib.i4_matmul_multi_dev.argtypes = [_vp, _i, _vp, _i, _vp, _vp]
     _lib.i4_matmul_silu_mul_dev.restype = _i
     _lib.i4_matmul_silu_mul_dev.argtypes = [_vp, _vp, _vp, _i, _vp, _vp]
     _lib.i4_block_dots_dev.restype = _i
@@ -290,6 +292,25 @@ def matmul_silu_mul(gate, up, a2d, N):
     _check_rc(_lib.i4_matmul_silu_mul_dev(_vp(gate), _vp(up), _vp(a.data_ptr()), int(M), _vp(out.data_ptr()),
                                           _torch_stream(a)), "i4_matmul_silu_mul_dev")
     return out
+
+
+def matmul_multi(handles, a2d, Ns):
+    """GPU torch tensor [M, K] -> [a @ W_i for each handle] (fp32 [M, N_i]):
+    projections of one activation, e.g. the decoder's in_qkv, in_z, in_b,
+    in_a (kernel/qwen35_decoder.cpp:285-288), in one launch when they share
+    a device layout; asynchronous on the current stream."""
+    _require_lib()
+    import torch
+    if not 1 <= len(handles) <= 4 or len(handles) != len(Ns):
+        raise ValueError("matmul_multi takes 1 to 4 handles and one N per handle")
+    a = a2d.to(torch.float32).contiguous()
+    M = a.shape[0]
+    outs = [torch.empty((M, int(n)), dtype=torch.float32, device=a.device) for n in Ns]
+    hv = (ctypes.c_void_p * len(handles))(*[int(h) for h in handles])
+    cv = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    _check_rc(_lib.i4_matmul_multi_dev(hv, len(handles), _vp(a.data_ptr()), int(M), cv, _torch_stream(a)),
+              "i4_matmul_multi_dev")
+    return outs
 
 
 def rmsnorm(x2d, w, eps):

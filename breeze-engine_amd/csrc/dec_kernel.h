@@ -16,7 +16,7 @@ namespace bq {
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
 
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR, bool P64>
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64, int PW>
 __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
                                                              int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
                                                              int pNG, int pngrp, int misc, GemvArgs args) {
@@ -35,6 +35,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     a.sc_shift = misc & 31;
     a.RG = (misc >> 8) & 3;
     a.pair_xcd = (misc >> 10) & 1;
+    constexpr bool PAIR = FUSE == kFusePair, MULTI = FUSE == kFuseMulti;
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int PP = dec_pitch(JG);
     typedef float fvec __attribute__((ext_vector_type(JG)));
@@ -134,12 +135,23 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // from the current tile.  On the last tile (and for gate/up pairs, whose
     // next tile lies in the other array) the load re-reads the tile's last
     // chunk instead, so every address stays inside the workgroup's tiles.
+    //
+    // With several projections (MULTI) the weights and scales of segment
+    // ld_k are at lw and ls; the cursor moves to the next segment's arrays
+    // when a tile crosses into it, and the idle loads never leave a tile.
     int ld_c = wave, ld_rem = npw, ld_t = 0, ld_sel = 0;  // ld_sel: up tile of a pair
-    uint32_t ld_w = (uint32_t)t_begin * nbg * 64;
-    uint32_t ld_s = (uint32_t)t_begin * a.ngrp * 16;
+    int ld_k = 0, t_off = 0;  // MULTI: segment of the next tile, and its first tile
+    if (MULTI) {
+        ld_k = (t_begin >= args.seg_end[0]) + (t_begin >= args.seg_end[1]) + (t_begin >= args.seg_end[2]);
+        t_off = ld_k ? args.seg_end[ld_k - 1] : 0;
+    }
+    const uint4* lw = MULTI ? args.segW[ld_k] : a.W;
+    const float* ls = MULTI ? args.segS[ld_k] : a.S;
+    uint32_t ld_w = (uint32_t)(t_begin - t_off) * nbg * 64;
+    uint32_t ld_s = (uint32_t)(t_begin - t_off) * a.ngrp * 16;
     uint32_t ld_m = (uint32_t)t_begin * nbg * 16;
     const int pf_c = nbg + kProducers + wave;
-    const bool pf = !PAIR && npw >= 2 && wave + kProducers < nbg;
+    const bool pf = !PAIR && !MULTI && npw >= 2 && wave + kProducers < nbg;
     int ld_idle = (pf && nT > 1) ? pf_c : nbg - 1;  // weight chunk of a load with no work
     auto load_unit = [&](Unit<JG, EXTRA>& p) {
         const int c = min(ld_c, nbg - 1);
@@ -151,7 +163,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         // uniform-address copies on branches of their own.
         asm("" : "+v"(wi), "+v"(mi), "+v"(si));
         const bool up = PAIR && ld_sel;
-        p.w = (up ? a.W2 : a.W)[wi];
+        p.w = (up ? a.W2 : lw)[wi];
         if (EXTRA) {
             const fvec sv = *reinterpret_cast<const fvec*>((up ? a.S2 : a.S) + (size_t)mi * JG);
             const ivec dv = *reinterpret_cast<const ivec*>((up ? a.D2 : a.D) + (size_t)mi * JG);
@@ -162,7 +174,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             }
             if (JG == 4) p.zp = *reinterpret_cast<const uint32_t*>((up ? a.Z2 : a.Z) + (size_t)mi * 4);
         } else {
-            p.sc[0] = (up ? a.S2 : a.S)[si];
+            p.sc[0] = (up ? a.S2 : ls)[si];
         }
         p.c = ld_c;
         ld_c += kProducers;
@@ -178,6 +190,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     ld_w += nbg * 64;
                     ld_s += a.ngrp * 16;
                     ld_m += nbg * 16;
+                    if (MULTI && t_begin + ld_t == args.seg_end[ld_k]) {
+                        ++ld_k;
+                        lw = args.segW[ld_k];
+                        ls = args.segS[ld_k];
+                        ld_w = 0;
+                        ld_s = 0;
+                    }
                     if (ld_t + 1 == nT) ld_idle = nbg - 1;
                 } else {
                     ld_c = 1 << 24;
@@ -305,7 +324,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         const bool tail_pad = a.nblk != nbg * JG;  // the last chunk has padding blocks
         float acc = 0.0f, gate = 0.0f;
         unsigned long long best = 0;
-        int pr_t = 0, pr_p = 0, pr_sel = 0;
+        int pr_t = 0, pr_p = 0, pr_sel = 0, pr_k = 0;
         for (int u = 0; u < U; ++u) {
             lds_barrier();
             const float* fp = fbuf + ((u & 1) * 64 + lane) * PP;
@@ -359,7 +378,16 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     // silu(g) = g / (1 + exp(-g)) (qwen35_decoder.cpp:129),
                     // times the up projection (qwen35_decoder.cpp:408).
                     const float v = PAIR ? gate / (1.0f + expf(-gate)) * acc : acc;
-                    if (grp < Mr) {
+                    if (MULTI) {
+                        // Tiles come in increasing order: step into the
+                        // segment of this one.
+                        const int gt = t_begin + pr_t;
+                        while (gt >= args.seg_end[pr_k]) ++pr_k;
+                        if (grp < Mr) {
+                            const int t0k = pr_k ? args.seg_end[pr_k - 1] : 0;
+                            args.segC[pr_k][(size_t)(m0 + grp) * args.segN[pr_k] + (gt - t0k) * 16 + col] = v;
+                        }
+                    } else if (grp < Mr) {
                         const int n = (t_begin + pr_t) * 16 + col;
                         a.C[(size_t)(m0 + grp) * a.N + n] = v;
                         if (!PAIR && a.idx) {
@@ -374,7 +402,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 pr_p = 0;
             }
         }
-        if (!PAIR && a.idx) {
+        if (!PAIR && !MULTI && a.idx) {
             // Row maximum over the lanes of each row (lanes 16r..16r+15).
 #pragma unroll
             for (int s = 1; s < 16; s <<= 1) {
@@ -408,10 +436,16 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // goes first, since weight requests issued beside it slowed it down
     // (three and four rows: 11.8 -> 11.3 us).
     Unit<JG, EXTRA> ring[R];
+    // Window: the first PW units, loaded with the ring's first R at kernel
+    // start, so the weights stream while the activations arrive and are
+    // quantized; the ring takes over from unit PW.
+    Unit<JG, EXTRA> win[PW > 0 ? PW : 1];
     if (!FUSED) {
         store_acts();
         __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int d = 0; d < PW; ++d) load_unit(win[d]);
 #pragma unroll
     for (int d = 0; d < R; ++d) load_unit(ring[d]);
     __builtin_amdgcn_sched_barrier(0);
@@ -438,83 +472,91 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int o_row = min(grp >> 1, Mr - 1), o_sel = grp & 1;
     float* const p_fout = fbuf + (col + 16 * (grp >> 1)) * PP + wave * JG + o_sel;
 
-    for (int u0 = 0; u0 < U; u0 += R) {
+    // Computes one unit into phase buffer buf.
+    auto consume = [&](const Unit<JG, EXTRA>& cur, int buf) {
+        const int c = cur.c;
+        if (P64 && c < nbg) {
+            const int abase = p_data ? p_data_base + c * JG * 128 : p_const_base;
+            int2 nsq2 = make_int2(0, 0);  // this lane's block in each pair
+            if (BITS == 4) {
+                const int* q = sq_l + o_row * lay.sa_pitch + c * 4 + o_sel;
+                nsq2 = make_int2(q[0], q[2]);
+            }
+            float fo[JG / 2];
+#pragma unroll
+            for (int mi = 0; mi < JG / 2; ++mi) {
+                // Blocks past nblk (last chunk) read padding; the chain
+                // never folds them.
+                uint4 bop = cur.w;
+                if (BITS == 4) {
+                    const uint64_t b0 = unpack_b(cur.w, 2 * mi, 4), b1 = unpack_b(cur.w, 2 * mi + 1, 4);
+                    bop = make_uint4((uint32_t)b0, (uint32_t)(b0 >> 32), (uint32_t)b1, (uint32_t)(b1 >> 32));
+                }
+                const uint8_t* ap = smem + abase + (p_data ? mi * 256 : 0);
+                const uint2 alo = *reinterpret_cast<const uint2*>(ap);
+                const uint2 ahi = *reinterpret_cast<const uint2*>(ap + 8);
+                const v4i dd = mfma64(make_uint4(alo.x, alo.y, ahi.x, ahi.y), bop);
+                int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
+                if (BITS == 4) {
+                    const int nsq = mi == 0 ? nsq2.x : nsq2.y;
+                    cs += EXTRA ? (int)(int8_t)((o_sel ? cur.zp >> 8 : cur.zp) >> (16 * mi)) * nsq : nsq;
+                }
+                float sc = cur.sc[0];
+                if (EXTRA) {
+                    // Values first, then the lane's pick: a select
+                    // between array elements would index the unit in
+                    // memory.
+                    const int dl0 = cur.dl[EXTRA ? 2 * mi : 0], dl1 = cur.dl[EXTRA ? 2 * mi + 1 : 0];
+                    const float sc0 = cur.sc[EXTRA ? 2 * mi : 0], sc1 = cur.sc[EXTRA ? 2 * mi + 1 : 0];
+                    cs += (HP ? 256 : 1) * (o_sel ? dl1 : dl0);
+                    sc = o_sel ? sc1 : sc0;
+                }
+                fo[mi] = (float)cs * sc;
+            }
+            // Both results in one LDS instruction (ds_write2_b32): the
+            // phase is bounded by LDS instruction issue, ~8 CU cycles each.
+#pragma unroll
+            for (int mi = 0; mi < JG / 2; ++mi) p_fout[buf * 64 * PP + 2 * mi] = fo[mi];
+        } else if (!P64 && c < nbg) {
+            const int abase = is_data ? data_base + c * JG * 64 : const_base;
+            // The chunk's JG A operands of this lane: 8 JG contiguous bytes.
+            uint4 av4[JG / 2];
+#pragma unroll
+            for (int h = 0; h < JG / 2; ++h) av4[h] = *reinterpret_cast<const uint4*>(smem + abase + 16 * h);
+            int4 sqv = make_int4(0, 0, 0, 0);
+            if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * lay.sa_pitch + c * 4);
+            fvec fo;
+#pragma unroll
+            for (int jb = 0; jb < JG; ++jb) {
+                // Blocks past nblk (last chunk) read padding; the chain
+                // never folds them.
+                const uint64_t bop = unpack_b(cur.w, jb, BITS);
+                const uint4& a2 = av4[jb >> 1];
+                const uint64_t aop = (jb & 1) ? ((uint64_t)a2.w << 32 | a2.z) : ((uint64_t)a2.y << 32 | a2.x);
+                const v4i dd = mfma16(aop, bop);
+                int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
+                if (BITS == 4) {
+                    const int nsq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
+                    cs += EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) * nsq : nsq;
+                }
+                if (EXTRA) cs += (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
+                fo[jb] = (float)cs * cur.sc[EXTRA ? jb : 0];
+            }
+            *reinterpret_cast<fvec*>(fbuf + (buf * 64 + lane) * PP + wave * JG) = fo;
+        }
+    };
+
+#pragma unroll
+    for (int d = 0; d < PW; ++d) {
+        consume(win[d], d & 1);
+        __builtin_amdgcn_sched_barrier(0);
+        if (d < U) lds_barrier();  // uniform over the workgroup
+    }
+    for (int u0 = PW; u0 < U; u0 += R) {
 #pragma unroll
         for (int d = 0; d < R; ++d) {
             const bool live = u0 + d < U;  // uniform over the workgroup
-            const int c = ring[d].c;
-            const int buf = (u0 + d) & 1;
-            if (P64 && c < nbg) {
-                const Unit<JG, EXTRA>& cur = ring[d];
-                const int abase = p_data ? p_data_base + c * JG * 128 : p_const_base;
-                int2 nsq2 = make_int2(0, 0);  // this lane's block in each pair
-                if (BITS == 4) {
-                    const int* q = sq_l + o_row * lay.sa_pitch + c * 4 + o_sel;
-                    nsq2 = make_int2(q[0], q[2]);
-                }
-                float fo[JG / 2];
-#pragma unroll
-                for (int mi = 0; mi < JG / 2; ++mi) {
-                    // Blocks past nblk (last chunk) read padding; the chain
-                    // never folds them.
-                    uint4 bop = cur.w;
-                    if (BITS == 4) {
-                        const uint64_t b0 = unpack_b(cur.w, 2 * mi, 4), b1 = unpack_b(cur.w, 2 * mi + 1, 4);
-                        bop = make_uint4((uint32_t)b0, (uint32_t)(b0 >> 32), (uint32_t)b1, (uint32_t)(b1 >> 32));
-                    }
-                    const uint8_t* ap = smem + abase + (p_data ? mi * 256 : 0);
-                    const uint2 alo = *reinterpret_cast<const uint2*>(ap);
-                    const uint2 ahi = *reinterpret_cast<const uint2*>(ap + 8);
-                    const v4i dd = mfma64(make_uint4(alo.x, alo.y, ahi.x, ahi.y), bop);
-                    int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
-                    if (BITS == 4) {
-                        const int nsq = mi == 0 ? nsq2.x : nsq2.y;
-                        cs += EXTRA ? (int)(int8_t)((o_sel ? cur.zp >> 8 : cur.zp) >> (16 * mi)) * nsq : nsq;
-                    }
-                    float sc = cur.sc[0];
-                    if (EXTRA) {
-                        // Values first, then the lane's pick: a select
-                        // between array elements would index the unit in
-                        // memory.
-                        const int dl0 = cur.dl[EXTRA ? 2 * mi : 0], dl1 = cur.dl[EXTRA ? 2 * mi + 1 : 0];
-                        const float sc0 = cur.sc[EXTRA ? 2 * mi : 0], sc1 = cur.sc[EXTRA ? 2 * mi + 1 : 0];
-                        cs += (HP ? 256 : 1) * (o_sel ? dl1 : dl0);
-                        sc = o_sel ? sc1 : sc0;
-                    }
-                    fo[mi] = (float)cs * sc;
-                }
-                // Both results in one LDS instruction (ds_write2_b32): the
-                // phase is bounded by LDS instruction issue, ~8 CU cycles each.
-#pragma unroll
-                for (int mi = 0; mi < JG / 2; ++mi) p_fout[buf * 64 * PP + 2 * mi] = fo[mi];
-            } else if (!P64 && c < nbg) {
-                const Unit<JG, EXTRA>& cur = ring[d];
-                const int abase = is_data ? data_base + c * JG * 64 : const_base;
-                // The chunk's JG A operands of this lane: 8 JG contiguous bytes.
-                uint4 av4[JG / 2];
-#pragma unroll
-                for (int h = 0; h < JG / 2; ++h) av4[h] = *reinterpret_cast<const uint4*>(smem + abase + 16 * h);
-                int4 sqv = make_int4(0, 0, 0, 0);
-                if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * lay.sa_pitch + c * 4);
-                fvec fo;
-#pragma unroll
-                for (int jb = 0; jb < JG; ++jb) {
-                    // Blocks past nblk (last chunk) read padding; the chain
-                    // never folds them.
-                    const uint64_t bop = unpack_b(cur.w, jb, BITS);
-                    const uint4& a2 = av4[jb >> 1];
-                    const uint64_t aop = (jb & 1) ? ((uint64_t)a2.w << 32 | a2.z) : ((uint64_t)a2.y << 32 | a2.x);
-                    const v4i dd = mfma16(aop, bop);
-                    int cs = HP ? (dd[0] * 256 + dd[1]) + (dd[2] + dd[3]) : dd[0];
-                    if (BITS == 4) {
-                        const int nsq = jb == 0 ? sqv.x : jb == 1 ? sqv.y : jb == 2 ? sqv.z : sqv.w;
-                        cs += EXTRA ? (int)(int8_t)(cur.zp >> (8 * jb)) * nsq : nsq;
-                    }
-                    if (EXTRA) cs += (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
-                    fo[jb] = (float)cs * cur.sc[EXTRA ? jb : 0];
-                }
-                *reinterpret_cast<fvec*>(fbuf + (buf * 64 + lane) * PP + wave * JG) = fo;
-            }
+            consume(ring[d], (u0 + d) & 1);
             load_unit(ring[d]);
             __builtin_amdgcn_sched_barrier(0);
             if (live) lds_barrier();
@@ -522,11 +564,16 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     }
 }
 
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, bool PAIR, bool P64>
+// Window depths instantiated for handles without per-block metadata and
+// without the gate/up pairing (index into attribute keys: position + 1).
+constexpr int kDecWindows[] = {3, 7};
+
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64, int PW>
 hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hipStream_t st) {
-    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, PAIR, P64>;
+    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, FUSE, P64, PW>;
+    const int wsel = PW == 0 ? 0 : PW == kDecWindows[0] ? 1 : 2;
     const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (EXTRA ? 8 : 0) | ((R / 2 - 1) << 4) |
-                    (PAIR ? 32 : 0) | (P64 ? 64 : 0);
+                    (P64 ? 32 : 0) | FUSE << 6 | wsel << 8;
     if (!attr_set[key]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
@@ -541,22 +588,57 @@ hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hi
     return hipGetLastError();
 }
 
+// Window depth: the deepest instantiated one that the workgroup with the
+// fewest units fills together with the ring (units past a workgroup's end
+// would only re-read its last chunk).  Off unless BREEZE_HIP_DEC_PW names an
+// instantiated depth: issuing the window's units costs ~20 scalar
+// instructions each on the CU's one scalar unit, shared by all sixteen
+// waves, and every decode workload measured slower with it.
+inline int pick_dec_window(const GemvArgs& a, int R) {
+    const char* f = std::getenv("BREEZE_HIP_DEC_PW");
+    if (!f) return 0;
+    const int v = std::atoi(f);
+    for (int w : kDecWindows)
+        if (w == v) return v;
+    return 0;
+}
+
+template <int BITS, bool HP, bool FUSED, bool EXTRA, bool P64>
+hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, hipStream_t st) {
+    if (fuse == kFusePair)
+        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePair, P64, 0>(attr_set, a, grid, lds, st);
+    if constexpr (!EXTRA) {
+        if (fuse == kFuseMulti)
+            return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseMulti, P64, 0>(attr_set, a, grid, lds, st);
+        switch (pick_dec_window(a, kDecRing)) {
+            case kDecWindows[0]:
+                return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, kDecWindows[0]>(attr_set, a,
+                                                                                                       grid, lds, st);
+            case kDecWindows[1]:
+                return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, kDecWindows[1]>(attr_set, a,
+                                                                                                       grid, lds, st);
+            default: break;
+        }
+    } else if (fuse == kFuseMulti) {
+        return hipErrorInvalidValue;  // the host sends per-block-metadata handles one by one
+    }
+    return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, 0>(attr_set, a, grid, lds, st);
+}
+
 template <int BITS, bool HP, bool FUSED, bool EXTRA>
-hipError_t launch_dec_r(bool* attr_set, const GemvArgs& a, int grid, int lds, bool pair, bool p64,
+hipError_t launch_dec_r(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, bool p64,
                         hipStream_t st) {
-    if (p64) return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true, true>(attr_set, a, grid, lds, st)
-                         : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false, true>(attr_set, a, grid, lds, st);
-    return pair ? launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, true, false>(attr_set, a, grid, lds, st)
-                : launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, false, false>(attr_set, a, grid, lds, st);
+    return p64 ? launch_dec_w<BITS, HP, FUSED, EXTRA, true>(attr_set, a, grid, lds, fuse, st)
+               : launch_dec_w<BITS, HP, FUSED, EXTRA, false>(attr_set, a, grid, lds, fuse, st);
 }
 
 template <int BITS, bool HP>
-hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds, bool pair, bool p64, bool fused,
+hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, bool p64, bool fused,
                            bool extra, hipStream_t st) {
-    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(attr_set, a, grid, lds, pair, p64, st)
-                            : launch_dec_r<BITS, HP, false, true>(attr_set, a, grid, lds, pair, p64, st);
-    return fused ? launch_dec_r<BITS, HP, true, false>(attr_set, a, grid, lds, pair, p64, st)
-                 : launch_dec_r<BITS, HP, false, false>(attr_set, a, grid, lds, pair, p64, st);
+    if (extra) return fused ? launch_dec_r<BITS, HP, true, true>(attr_set, a, grid, lds, fuse, p64, st)
+                            : launch_dec_r<BITS, HP, false, true>(attr_set, a, grid, lds, fuse, p64, st);
+    return fused ? launch_dec_r<BITS, HP, true, false>(attr_set, a, grid, lds, fuse, p64, st)
+                 : launch_dec_r<BITS, HP, false, false>(attr_set, a, grid, lds, fuse, p64, st);
 }
 
 }  // namespace bq

@@ -2,6 +2,6 @@
 #include "dec_kernel.h"
 
 namespace bq {
-template hipError_t launch_dec_bits<8, true>(bool*, const GemvArgs&, int, int, bool, bool, bool, bool,
+template hipError_t launch_dec_bits<8, true>(bool*, const GemvArgs&, int, int, int, bool, bool, bool,
                                                     hipStream_t);
 }  // namespace bq

@@ -382,9 +382,25 @@ __device__ inline int norm_classify(double P, double t, unsigned long long* k) {
     return 0;
 }
 
+// Only (float)(ss / H) of the sum enters the output.  The kernel first forms
+// a tree sum T of the same terms, each term passing through at most
+// D = per + 22 roundings (its thread's run, a 64-lane butterfly, the 16 wave
+// totals in order).  All terms are >= 0 and exact (squares of floats), so
+// |T - S| <= gamma_D * S and the reference's in-order sum satisfies
+// |ss - S| <= gamma_(H-1) * S: ss lies within E = (H + D + 2) * 2^-53 * T
+// (with slack for gamma and for rounding T -/+ E) of T.  S -> (float)(S / H)
+// is monotone, so when T - E and T + E map to the same float, ss maps to it
+// too and the in-order reconstruction is skipped.
+__device__ inline bool norm_mean_from_bound(double T, int H, int per, float* mean) {
+    const double E = (double)(H + per + 24) * 0x1p-53 * T * (1.0 + 0x1p-10);
+    const float lo = (float)((T - E) / (double)H), hi = (float)((T + E) / (double)H);
+    *mean = lo;
+    return lo == hi;
+}
+
 template <bool STAGED>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ X, const float* __restrict__ Wt,
-                                                                int H, float eps, float* __restrict__ Out) {
+                                                                int H, float eps, float* __restrict__ Out, int exact_only) {
     extern __shared__ float norm_row[];                      // STAGED: the row
     __shared__ double spec[kNormMaxSpecial];                 // t, or -(floor(t/u) + 1) for a tie
     __shared__ unsigned long long seg[kNormMaxSpecial + 1];  // sum of k with q specials before
@@ -393,16 +409,72 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
     __shared__ double wsum_d[kNormThreads / 64];
     __shared__ int wsum_i[kNormThreads / 64];
     __shared__ double ss_s;
+    __shared__ float mean_s;  // (float)(ss / H)
     const float* xg = X + (size_t)blockIdx.x * H;
     float* o = Out + (size_t)blockIdx.x * H;
-    const int tid = threadIdx.x;
-    if (STAGED) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int per = (H + kNormThreads - 1) / kNormThreads;
+
+    // Shortcut: a tree sum T of the squares (elements tid + 1024 i, in
+    // registers when STAGED; a 64-lane butterfly; the 16 wave totals in
+    // order) and its error bound.  Any tree serves the bound, which needs
+    // only its depth: at most per + 22 roundings per term.
+    float xv[STAGED ? kNormPer : 1], wv[STAGED ? kNormPer : 1];
+    double loc = 0.0;
+    if constexpr (STAGED) {
+#pragma unroll
+        for (int i = 0; i < kNormPer; ++i) {
+            const int j = tid + i * kNormThreads;
+            xv[i] = j < H ? xg[j] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kNormPer; ++i) {
+            const int j = tid + i * kNormThreads;
+            wv[i] = j < H ? Wt[j] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kNormPer; ++i) loc += (double)xv[i] * (double)xv[i];
+    } else {
+        for (int j = tid; j < H; j += kNormThreads) loc += (double)xg[j] * (double)xg[j];
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) loc += __shfl_xor(loc, d);
+    if (lane == 0) wsum_d[tid >> 6] = loc;
+    __syncthreads();
+    double T = 0.0;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) T += wsum_d[w];
+    {
+        float mean = 0.0f;
+        // Uniform: every thread holds the same T.  NaN or inf totals (a
+        // NaN or inf term; finite squares cannot overflow) take the long way.
+        if (T - T == 0.0 && !exact_only && norm_mean_from_bound(T, H, per, &mean)) {
+            const float inv = 1.0f / sqrtf(mean + eps);
+            if constexpr (STAGED) {
+#pragma unroll
+                for (int i = 0; i < kNormPer; ++i) {
+                    const int j = tid + i * kNormThreads;
+                    if (j < H) o[j] = xv[i] * inv * wv[i];
+                }
+            } else {
 #pragma unroll 4
-        for (int j = tid; j < H; j += kNormThreads) norm_row[j] = xg[j];
+                for (int j = tid; j < H; j += kNormThreads) o[j] = xg[j] * inv * Wt[j];
+            }
+            return;
+        }
+    }
+    __syncthreads();  // wsum_d is reused below
+
+    // The in-order reconstruction.
+    if (STAGED) {
+#pragma unroll
+        for (int i = 0; i < kNormPer; ++i) {
+            const int j = tid + i * kNormThreads;
+            if (j < H) norm_row[j] = xv[i];
+        }
         __syncthreads();
     }
     const float* x = STAGED ? norm_row : xg;
-    const int per = (H + kNormThreads - 1) / kNormThreads;
     const int j0 = min(tid * per, H), j1 = min(j0 + per, H);
 
     // STAGED: this thread's terms (0 past its range) and, after the
@@ -410,32 +482,28 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
     double tv[STAGED ? kNormPer : 1];
     unsigned long long kv[STAGED ? kNormPer : 1];
     unsigned smask = 0, tmask = 0;
-    double loc = 0.0;
-    int nan = 0, inf = 0;
+    loc = 0.0;
     if constexpr (STAGED) {
 #pragma unroll
         for (int i = 0; i < kNormPer; ++i) {
             const int j = j0 + i;
             const float xv = j < j1 ? x[j] : 0.0f;
             tv[i] = (double)xv * (double)xv;
-            nan |= tv[i] != tv[i];
-            inf |= tv[i] == __builtin_inf();
             loc += tv[i];
         }
     } else {
-        for (int j = j0; j < j1; ++j) {
-            const double t = (double)x[j] * (double)x[j];
-            nan |= t != t;
-            inf |= t == __builtin_inf();
-            loc += t;
-        }
+        for (int j = j0; j < j1; ++j) loc += (double)x[j] * (double)x[j];
     }
-    const int any_nan = __syncthreads_or(nan), any_inf = __syncthreads_or(inf);
+    double tot_d;
+    const double base = block_exclusive_scan<double>(loc, wsum_d, &tot_d);
+    // Every thread holds the same total.  Squares of floats are at most
+    // 2^256 and at most 2^31 of them cannot overflow a double, so the total
+    // is NaN exactly when a term is (then the reference's sum is NaN too)
+    // and +inf exactly when a term is and none is NaN (then its sum is +inf).
+    const bool any_nan = tot_d != tot_d, any_inf = tot_d == __builtin_inf();
     if (any_nan || any_inf) {
         if (tid == 0) ss_s = any_nan ? __builtin_nan("") : __builtin_inf();
     } else {
-        double tot_d;
-        const double base = block_exclusive_scan<double>(loc, wsum_d, &tot_d);
         int cnt = 0;
         if constexpr (STAGED) {
             double P = base;
@@ -560,9 +628,19 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
         }
     }
     __syncthreads();
-    const float inv = 1.0f / sqrtf((float)(ss_s / (double)H) + eps);
+    if (tid == 0) mean_s = (float)(ss_s / (double)H);
+    __syncthreads();
+    const float inv = 1.0f / sqrtf(mean_s + eps);
+    if constexpr (STAGED) {
+#pragma unroll
+        for (int i = 0; i < kNormPer; ++i) {
+            const int j = tid + i * kNormThreads;
+            if (j < H) o[j] = x[j] * inv * wv[i];
+        }
+    } else {
 #pragma unroll 4
-    for (int j = tid; j < H; j += kNormThreads) o[j] = x[j] * inv * Wt[j];
+        for (int j = tid; j < H; j += kNormThreads) o[j] = x[j] * inv * Wt[j];
+    }
 }
 
 // ------------------------------------------------------------------ argmax
@@ -651,7 +729,7 @@ struct Workspace {
     size_t hA_cap = 0, hC_cap = 0;
     hipStream_t stream = nullptr;
     int n_cu = 0;
-    bool attr_set[128] = {};
+    bool attr_set[1024] = {};
     bool pf_attr[64] = {};
 };
 
@@ -954,20 +1032,30 @@ int device_cus(Workspace& w, int dev) {
 // dC / dCs is non-null; dIdx (optional) receives the per-row argmax.
 constexpr int kNotPairable = -100;  // run() with h2: the decode kernel does not take this call
 
-// Gate and up handles the paired decode kernel can stream together: the same
-// device, shape and device layout.
-bool same_layout(const Handle* a, const Handle* b) {
-    return a->device == b->device && a->N == b->N && a->K == b->K && a->bits == b->bits && a->nbg == b->nbg &&
+// Handles one decode launch can stream together: the same device and
+// device layout; the gate/up pairing also needs the same N.
+bool same_layout_but_n(const Handle* a, const Handle* b) {
+    return a->device == b->device && a->K == b->K && a->bits == b->bits && a->nbg == b->nbg &&
            a->sc_shift == b->sc_shift && a->ngrp == b->ngrp && a->sc_blk == b->sc_blk && a->extra == b->extra &&
            (a->Z == nullptr) == (b->Z == nullptr) && (a->D == nullptr) == (b->D == nullptr);
 }
+bool same_layout(const Handle* a, const Handle* b) { return a->N == b->N && same_layout_but_n(a, b); }
+
+// Projections of one activation in one decode launch (i4_matmul_multi_dev).
+struct Multi {
+    const Handle* h[kMaxSeg];
+    float* C[kMaxSeg];
+    int n;
+};
 
 // h2 (gate/up pairing): a second handle with the same layout (same_layout).
 // Returns kNotPairable, having launched nothing, when the decode kernel does
 // not take the call.
 // The caller holds w.mu; s is the scratch of st.
+// mp (multi-projection): h is mp->h[0] and dC is mp->C[0]; returns
+// kNotPairable, having launched nothing, unless one decode launch takes all.
 int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, int32_t* dCs, int64_t* dIdx,
-        hipStream_t st, const Handle* h2 = nullptr) {
+        hipStream_t st, const Handle* h2 = nullptr, const Multi* mp = nullptr) {
     if (M < 0) {
         set_err("M must be >= 0 (got %d)", M);
         return -2;
@@ -1013,7 +1101,8 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     const bool p64 = lds_p64 > 0;
     const int lds = p64 ? lds_p64 : (M <= 8 && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     const bool dec = lds > 0;
-    if (h2 && !dec) return kNotPairable;
+    if ((h2 || mp) && !dec) return kNotPairable;
+    if (mp && (h->extra || dIdx)) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
     // Prefill GEMM: more than 8 rows without a legacy corr.
     const bool pre = !dec && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
@@ -1042,6 +1131,26 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
 
     hipError_t e;
     if (dec) {
+        if (mp) {
+            int t = 0;
+            for (int k = 0; k < kMaxSeg; ++k) {
+                if (k < mp->n) {
+                    a.segW[k] = mp->h[k]->W;
+                    a.segS[k] = mp->h[k]->S;
+                    a.segC[k] = mp->C[k];
+                    a.segN[k] = mp->h[k]->N;
+                    t += mp->h[k]->N / 16;
+                    a.seg_end[k] = t;
+                } else {
+                    a.segW[k] = nullptr;
+                    a.segS[k] = nullptr;
+                    a.segC[k] = nullptr;
+                    a.segN[k] = 0;
+                    a.seg_end[k] = std::numeric_limits<int>::max();
+                }
+            }
+            a.ntiles = t;
+        }
         const int n_cu = device_cus(w, dev);
         a.RG = (M + 3) / 4;
         if (a.RG == 1) {
@@ -1088,10 +1197,11 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         }
         const int grid = a.NG * a.RG;
         const bool x = h->extra;
-        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w.attr_set, a, grid, lds, pair, p64, fused, x, st)
-                                 : launch_dec_bits<8, false>(w.attr_set, a, grid, lds, pair, p64, fused, x, st);
-        else e = hp ? launch_dec_bits<4, true>(w.attr_set, a, grid, lds, pair, p64, fused, x, st)
-                    : launch_dec_bits<4, false>(w.attr_set, a, grid, lds, pair, p64, fused, x, st);
+        const int fz = pair ? kFusePair : mp ? kFuseMulti : kFusePlain;
+        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)
+                                 : launch_dec_bits<8, false>(w.attr_set, a, grid, lds, fz, p64, fused, x, st);
+        else e = hp ? launch_dec_bits<4, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)
+                    : launch_dec_bits<4, false>(w.attr_set, a, grid, lds, fz, p64, fused, x, st);
     } else if (pre) {
         PfArgs p{};
         p.W = reinterpret_cast<const char*>(h->W);
@@ -1383,6 +1493,44 @@ int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* 
     });
 }
 
+int i4_matmul_multi_dev(void* const* handles, int n, const float* dA, int M, float* const* dC, void* stream) {
+    if (!handles || !dC || n < 1 || n > kMaxSeg) {
+        set_err("need 1 to %d handles and as many outputs (got %d)", kMaxSeg, n);
+        return -2;
+    }
+    Multi mp{};
+    mp.n = n;
+    for (int i = 0; i < n; ++i) {
+        Handle* h = as_handle(handles[i]);
+        if (!h) return -1;
+        if (!dC[i]) {
+            set_err("null device pointer");
+            return -2;
+        }
+        if (i > 0 && (h->K != mp.h[0]->K || h->device != mp.h[0]->device)) {
+            set_err("projections of one activation need one K and one device");
+            return -2;
+        }
+        mp.h[i] = h;
+        mp.C[i] = dC[i];
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    Handle* h0 = const_cast<Handle*>(mp.h[0]);
+    return with_scratch(h0, st, [&](Workspace& w, Scratch& s) {
+        bool one = n > 1;
+        for (int i = 1; i < n; ++i) one = one && same_layout_but_n(h0, mp.h[i]);
+        if (one) {
+            const int rc = run(w, s, h0, dA, M, mp.C[0], nullptr, nullptr, st, nullptr, &mp);
+            if (rc != kNotPairable) return rc;
+        }
+        for (int i = 0; i < n; ++i) {
+            const int rc = run(w, s, const_cast<Handle*>(mp.h[i]), dA, M, mp.C[i], nullptr, nullptr, st);
+            if (rc) return rc;
+        }
+        return 0;
+    });
+}
+
 int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream) {
     Handle* h = as_handle(handle);
     if (!h) return -1;
@@ -1597,10 +1745,14 @@ int i4_rmsnorm_dev(const float* dX, const float* dW, int M, int H, float eps, fl
         return -2;
     }
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    // BREEZE_HIP_NORM_EXACT=1 always takes the in-order reconstruction (tests).
+    const char* ex = std::getenv("BREEZE_HIP_NORM_EXACT");
+    const int exact_only = ex && ex[0] == '1';
     if (H <= kNormStage)
-        rmsnorm_kernel<true><<<(unsigned)M, kNormThreads, (size_t)H * sizeof(float), st>>>(dX, dW, H, eps, dOut);
+        rmsnorm_kernel<true><<<(unsigned)M, kNormThreads, (size_t)H * sizeof(float), st>>>(dX, dW, H, eps, dOut,
+                                                                                           exact_only);
     else
-        rmsnorm_kernel<false><<<(unsigned)M, kNormThreads, 0, st>>>(dX, dW, H, eps, dOut);
+        rmsnorm_kernel<false><<<(unsigned)M, kNormThreads, 0, st>>>(dX, dW, H, eps, dOut, exact_only);
     return hip_ok(hipGetLastError(), "rmsnorm launch") ? 0 : -3;
 }
 

@@ -217,7 +217,21 @@ struct GemvArgs {
     const int32_t* D2;
     int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
     int ntiles, NG, RG, pair_xcd;
+    // Multi-projection launch: up to kMaxSeg weight sets of one layout (all
+    // but N alike) whose 16-column tiles are concatenated in order; segment
+    // k owns tiles [seg_end[k - 1], seg_end[k]) and writes segC[k], a
+    // [M][segN[k]] array.  Unused entries have seg_end = INT_MAX.
+    const uint4* segW[4];
+    const float* segS[4];
+    float* segC[4];
+    int segN[4];
+    int seg_end[4];
 };
+constexpr int kMaxSeg = 4;
+
+// Decode kernel modes: one weight set, the gate/up pair with the SiLU
+// epilogue, or several projections of one activation.
+constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2;
 
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
 // (explicit zero points, legacy corr, scale groups smaller than a chunk)
@@ -396,7 +410,7 @@ constexpr int kPfCts[] = {17, 16, 8, 4};
 // kernel units dec_w*.hip and pf_w*.hip.  attr_set / pf_attr: this device's
 // flags of kernels whose dynamic LDS limit is already raised.
 template <int BITS, bool HP>
-hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds, bool pair, bool p64, bool fused,
+hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, bool p64, bool fused,
                            bool extra, hipStream_t st);
 template <int BITS, bool HP>
 hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int ct, dim3 grid, hipStream_t st);

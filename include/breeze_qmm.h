@@ -114,6 +114,18 @@ int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* 
  * i4_matmul_argmax_dev, bit for bit. */
 int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream);
 
+/* Several projections of one activation in one launch, replacing
+ * consecutive i4_matmul calls on the same input (kernel/qwen35_decoder.cpp:
+ * 285-288 in_qkv, in_z, in_b, in_a; 334-336 q, k, v):
+ *   dC[i][M, N_i] = dA[M, K] * W_i,  i < n <= 4, one K for all.
+ * Each output is bit-identical to i4_matmul_dev's.  With M <= 8 and handles
+ * of one device layout (all but N alike, no per-block metadata) it is one
+ * decode launch whose workgroups share out the concatenated column tiles
+ * (the activation is quantized once per workgroup, and small projections
+ * ride along with large ones); otherwise one launch per handle.  Returns as
+ * i4_matmul_dev. */
+int i4_matmul_multi_dev(void* const* handles, int n, const float* dA, int M, float* const* dC, void* stream);
+
 /* Handle facts: out[0..7] = N, K, bits, scale group (blocks per distinct
  * scale, 0 = one per column), has_zero_points, has_corr_delta,
  * device bytes held, device ordinal.  Returns 0 or -1. */

@@ -1,12 +1,17 @@
 """GPU parity of the decoder's RMSNorm (kernel/qwen35_decoder.cpp:134-140).
 
-i4_rmsnorm_dev rebuilds the reference's in-order double sum of squares in
-parallel; every output must equal the oracle's bit for bit (both NaN where
-the oracle gives NaN).  The rows stress what that rebuild depends on: exact
-ties of both parities, terms that round away, binade crossings, zeros,
-leading zeros, outliers, denormal and non-finite inputs, a row whose
-partial sums hug a power of two (the in-order fallback), and ragged widths
-around the 256-thread split.
+i4_rmsnorm_dev takes (float)(ss / H) from a tree sum and its error bound
+when the bound decides it, and otherwise rebuilds the reference's in-order
+double sum of squares in parallel; every output must equal the oracle's bit
+for bit (both NaN where the oracle gives NaN).  Each case runs twice: as
+shipped, and with BREEZE_HIP_NORM_EXACT=1, which always takes the in-order
+rebuild.  The rows stress what that rebuild depends on: exact ties of both
+parities, terms that round away, binade crossings, zeros, leading zeros,
+outliers, denormal and non-finite inputs, a row whose partial sums hug a
+power of two (the single-thread fallback), and a row whose mean is a float
+rounding midpoint (the bound cannot decide it).  Widths straddle the
+kernel's one-to-two terms per thread step (1024/1025) and its staged /
+unstaged switch (8192/8193).
 """
 import numpy as np
 import pytest
@@ -55,12 +60,21 @@ def _rows(H, seed):
     rows.append(r)
     r = rng.standard_normal(H).astype(F) * F(3e38)
     rows.append(r.astype(F))
+    # Mean exactly between two floats when H is a power of two: x0^2 =
+    # 1 + 2^-11 + 2^-24.
+    r = np.zeros(H, F)
+    r[0] = F(1 + 2.0 ** -12)
+    rows.append(r)
     return np.stack(rows)
 
 
-@pytest.mark.parametrize("H", [1, 7, 255, 256, 257, 1000, 2048, 5120, 12288])
-def test_rmsnorm_bit_exact(gpu, hb, orc, H):
+@pytest.mark.parametrize("mode", ["auto", "exact"])
+@pytest.mark.parametrize("H", [1, 4, 7, 255, 256, 257, 1000, 1024, 1025, 2048, 5120, 8192, 8193, 12288])
+def test_rmsnorm_bit_exact(gpu, hb, orc, monkeypatch, H, mode):
     import torch
+
+    if mode == "exact":
+        monkeypatch.setenv("BREEZE_HIP_NORM_EXACT", "1")
 
     x = _rows(H, H)
     rng = np.random.default_rng(H + 1)

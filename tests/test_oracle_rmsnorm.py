@@ -96,3 +96,62 @@ def test_non_finite_rows(orc):
     # inf: inv = 1/inf = 0, finite entries 0, the inf one inf*0 = NaN.
     assert np.all(out[0][np.isfinite(x[0])] == 0) and np.isnan(out[0, 5])
     assert np.all(np.isnan(out[1])) and np.all(np.isnan(out[2]))
+
+
+def _kernel_tree_sum(x):
+    """The double sum of squares in the order of the GPU RMSNorm's shortcut:
+    thread t of 1024 sums the terms t, t + 1024, ... in order, a 64-lane
+    butterfly (lane l adds lane l ^ d for d = 32, 16, .., 1) gives each
+    wave's total, and the 16 wave totals are added in order."""
+    H = len(x)
+    per = -(-H // 1024)
+    t = np.zeros(1024 * per)
+    t[:H] = x.astype(np.float64) ** 2
+    runs = t.reshape(per, 1024)
+    loc = np.zeros(1024)
+    for i in range(per):  # each thread's run, in order
+        loc = loc + runs[i]
+    total = 0.0
+    lanes = np.arange(64)
+    for w in range(16):
+        v = loc[64 * w:64 * (w + 1)].copy()
+        for d in (32, 16, 8, 4, 2, 1):
+            v = v + v[lanes ^ d]
+        total = total + float(v[0])
+    return total, per
+
+
+def _bound_rows(rng, H):
+    rows = [rng.standard_normal(H).astype(F), np.ones(H, F),
+            (rng.standard_normal(H) * np.exp(rng.uniform(-40, 40, H))).astype(F)]
+    r = np.full(H, 2.0 ** -30, F)
+    r[0] = 1.0
+    rows.append(r)  # every term after the 1 rounds away in order, not in the tree
+    ties = np.where(rng.random(H) < 0.5, F(2.0 ** -26), F(3 * 2.0 ** -26)).astype(F)
+    ties[0] = 1.5
+    rows.append(ties)
+    r = rng.standard_normal(H).astype(F)
+    r[H // 2] = 1e18
+    rows.append(r)
+    return rows
+
+
+@pytest.mark.parametrize("H", [1, 7, 1000, 1025, 5120, 8192])
+def test_tree_sum_bound_holds_and_decides_the_mean(orc, H):
+    """The GPU RMSNorm's shortcut: with T its tree sum, the reference's
+    in-order sum ss lies within E = (H + per + 24) 2^-53 T (1 + 2^-10) of T,
+    so when (float)((T - E)/H) == (float)((T + E)/H), that is
+    (float)(ss / H).  Checked against the oracle's in-order sum; the row of
+    terms that round away in order (but add up in the tree) needs the H
+    term of E: a bound of the tree's own depth alone is too small there."""
+    rng = np.random.default_rng(H)
+    for i, x in enumerate(_bound_rows(rng, H)):
+        ss = float(orc.sumsq(x[None, :])[0])
+        T, per = _kernel_tree_sum(x)
+        E = (H + per + 24) * 2.0 ** -53 * T * (1 + 2.0 ** -10)
+        assert abs(T - ss) <= E, (H, i, T, ss)
+        lo, hi = np.float32((T - E) / H), np.float32((T + E) / H)
+        if lo == hi:
+            assert lo == np.float32(ss / H), (H, i)
+        if i == 3 and H in (5120, 8192):
+            assert abs(T - ss) > (per + 24) * 2.0 ** -53 * T, (H, T, ss)
