@@ -231,9 +231,23 @@ def time_multi(hb, torch, label, rows, steps, warmup):
             rc |= lib.i4_matmul_dev(hb._vp(h), ap, rows, hb._vp(o.data_ptr()), sp)
         return rc
 
+    # The decoder's RMSNorm ahead of the projections: in the projection
+    # launch's prologue, or as its own launch first.
+    ln = torch.from_numpy((1 + 0.1 * rng.standard_normal(K)).astype(np.float32)).cuda()
+    hn = torch.empty_like(A)
+    lp, hp = hb._vp(ln.data_ptr()), hb._vp(hn.data_ptr())
+
+    def norm_one(i):
+        return lib.i4_rmsnorm_matmul_multi_dev(ap, lp, 1e-6, hvs[i % len(sets)], len(Ns), rows, cv, None, sp)
+
+    def norm_then_one(i):
+        rc = lib.i4_rmsnorm_dev(ap, lp, rows, K, 1e-6, hp, sp)
+        return rc | lib.i4_matmul_multi_dev(hvs[i % len(sets)], len(Ns), hp, rows, cv, sp)
+
     res = {}
     try:
-        for key, call in (("one_launch", one), ("per_projection", each)):
+        for key, call in (("one_launch", one), ("per_projection", each), ("norm_in_launch", norm_one),
+                          ("norm_then_launch", norm_then_one)):
             for i in range(len(sets) + warmup):
                 if call(i) != 0:
                     raise RuntimeError(f"{label}: {hb.last_error()}")
@@ -389,7 +403,9 @@ def main():
                 rows.append({"workload": f"Qwen3.5-27B {label} W4 group-128, K={K} N={'/'.join(map(str, Ns))}, "
                                          f"M={m}",
                              "us_one_launch": round(r["one_launch"] * 1e6, 2),
-                             "us_per_projection": round(r["per_projection"] * 1e6, 2)})
+                             "us_per_projection": round(r["per_projection"] * 1e6, 2),
+                             "us_rmsnorm_in_launch": round(r["norm_in_launch"] * 1e6, 2),
+                             "us_rmsnorm_then_launch": round(r["norm_then_launch"] * 1e6, 2)})
                 print(f"bench: {rows[-1]}", file=sys.stderr, flush=True)
 
     t_step, M = time_workload(hb, torch, HEADLINE, None, args.steps, args.warmup)

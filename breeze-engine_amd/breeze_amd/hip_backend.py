@@ -80,6 +80,8 @@ try:
     _lib.i4_matmul_noalloc_dev.argtypes = [_vp, _vp, _i, _vp, _vp, _vp]
     _lib.i4_matmul_multi_dev.restype = _i
     _lib.i4_matmul_multi_dev.argtypes = [_vp, _i, _vp, _i, _vp, _vp]
+    _lib.i4_rmsnorm_matmul_multi_dev.restype = _i
+    _lib.i4_rmsnorm_matmul_multi_dev.argtypes = [_vp, _vp, ctypes.c_float, _vp, _i, _i, _vp, _vp, _vp]
     _lib.i4_matmul_silu_mul_dev.restype = _i
     _lib.i4_matmul_silu_mul_dev.argtypes = [_vp, _vp, _vp, _i, _vp, _vp]
     _lib.i4_block_dots_dev.restype = _i
@@ -311,6 +313,31 @@ def matmul_multi(handles, a2d, Ns):
     _check_rc(_lib.i4_matmul_multi_dev(hv, len(handles), _vp(a.data_ptr()), int(M), cv, _torch_stream(a)),
               "i4_matmul_multi_dev")
     return outs
+
+
+def rmsnorm_matmul_multi(x2d, w, eps, handles, Ns, want_hn=False):
+    """GPU torch tensors x [M, K], w [K] -> [hn @ W_i for each handle], and hn
+    when want_hn, with hn = rmsnorm(x, w, eps): the decoder's norm and the
+    projections that read it (kernel/qwen35_decoder.cpp:279, 285-288), in
+    one launch when the decode kernel quantizes the activation itself;
+    asynchronous on the current stream."""
+    _require_lib()
+    import torch
+    if not 1 <= len(handles) <= 4 or len(handles) != len(Ns):
+        raise ValueError("rmsnorm_matmul_multi takes 1 to 4 handles and one N per handle")
+    x = x2d.to(torch.float32).contiguous()
+    M, K = x.shape
+    wv = w.to(device=x.device, dtype=torch.float32).contiguous()
+    if wv.numel() != K:
+        raise ValueError(f"w has {wv.numel()} elements, x rows have {K}")
+    outs = [torch.empty((M, int(n)), dtype=torch.float32, device=x.device) for n in Ns]
+    hn = torch.empty_like(x) if want_hn else None
+    hv = (ctypes.c_void_p * len(handles))(*[int(h) for h in handles])
+    cv = (ctypes.c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    _check_rc(_lib.i4_rmsnorm_matmul_multi_dev(_vp(x.data_ptr()), _vp(wv.data_ptr()), float(eps), hv, len(handles),
+                                               int(M), cv, _vp(hn.data_ptr()) if want_hn else None,
+                                               _torch_stream(x)), "i4_rmsnorm_matmul_multi_dev")
+    return (outs, hn) if want_hn else outs
 
 
 def rmsnorm(x2d, w, eps):

@@ -35,7 +35,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     a.sc_shift = misc & 31;
     a.RG = (misc >> 8) & 3;
     a.pair_xcd = (misc >> 10) & 1;
-    constexpr bool PAIR = FUSE == kFusePair, MULTI = FUSE == kFuseMulti;
+    constexpr bool PAIR = FUSE == kFusePair, NORM = FUSE == kFuseNormMulti;
+    constexpr bool MULTI = FUSE == kFuseMulti || NORM;
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int PP = dec_pitch(JG);
     typedef float fvec __attribute__((ext_vector_type(JG)));
@@ -67,6 +68,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // contiguous too: a block index is an offset, with no row/column split.
     const int nb_rows = Mr * a.nblk;
     uint4 av[kQuantPasses];
+    uint4 wn[NORM ? kQuantPasses : 1];  // NORM: the norm weights of those elements
     uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
     if (FUSED) {
         if (nb_rows > kQuantEarlyBlocks || wave < 8) {
@@ -79,6 +81,16 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 if (p >= npass_ld) break;
                 const int blk = min(p * qb + (tid >> 3), nb_rows - 1);
                 av[p] = *reinterpret_cast<const uint4*>(arow + 32 * blk);
+            }
+            if (NORM) {
+#pragma unroll
+                for (int p = 0; p < kQuantPasses; ++p) {
+                    if (p >= npass_ld) break;
+                    const int blk = min(p * qb + (tid >> 3), nb_rows - 1);
+                    const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk);
+                    wn[NORM ? p : 0] =
+                        *reinterpret_cast<const uint4*>(a.normW + 32 * (blk - m * a.nblk) + 4 * (tid & 7));
+                }
             }
         }
     } else {
@@ -215,6 +227,51 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             const bool all = nb_rows > kQuantEarlyBlocks;
             const int qb = all ? 128 : 64;  // blocks per pass
             const int npass = all ? (nb_rows + 127) >> 7 : wave < 8 ? (nb_rows + 63) >> 6 : 0;
+            // NORM: the decoder's RMSNorm of each row first, hn = (x * inv) * w
+            // with inv = 1 / sqrtf((float)(ss / K) + eps)
+            // (kernel/qwen35_decoder.cpp:134-140), bit for bit.  The block
+            // sums of squares (4 terms in a lane, an 8-lane DPP sum) go to
+            // the idle phase buffer, every wave adds up each row's (a lane
+            // run of at most 8, a 16-lane DPP sum, the 4 row sums: at most
+            // 20 roundings a term) and norm_mean_from_bound decides the
+            // mean; a row it does not decide takes the in-order sum.  Any
+            // summation order serves: the mean either comes from the bound,
+            // which proves it equal to the reference's, or from the in-order
+            // sum itself.
+            float inv_r[NORM ? 4 : 1];
+            if constexpr (NORM) {
+                double* nsq = reinterpret_cast<double*>(fbuf);
+#pragma unroll
+                for (int p = 0; p < kQuantPasses; ++p) {
+                    if (p >= npass) break;
+                    const int blk = p * qb + (tid >> 3);
+                    const float x0 = __uint_as_float(av[p].x), x1 = __uint_as_float(av[p].y);
+                    const float x2 = __uint_as_float(av[p].z), x3 = __uint_as_float(av[p].w);
+                    double t = (double)x0 * (double)x0;
+                    t += (double)x1 * (double)x1;
+                    t += (double)x2 * (double)x2;
+                    t += (double)x3 * (double)x3;
+                    t = sum8_f64(t);
+                    if ((tid & 7) == 0 && blk < nb_rows) nsq[blk] = t;
+                }
+                lds_barrier();
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    inv_r[r] = 0.0f;
+                    if (r >= Mr || npass == 0) continue;
+                    double v = 0.0;
+                    for (int i = lane; i < a.nblk; i += 64) v += nsq[r * a.nblk + i];
+                    v = sum16_f64(v);
+                    v = (__builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 0)) +
+                         __builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 16))) +
+                        (__builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 32)) +
+                         __builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 48)));
+                    float mean;
+                    if (a.norm_exact || !(v - v == 0.0) || !norm_mean_from_bound(v, a.K, 0, &mean))
+                        mean = (float)(norm_sumsq_inorder(a.A + (size_t)(m0 + r) * a.K, a.K) / (double)a.K);
+                    inv_r[r] = 1.0f / sqrtf(mean + a.norm_eps);
+                }
+            }
 #pragma unroll
             for (int p = 0; p < kQuantPasses; ++p) {
                 if (p >= npass) break;
@@ -222,9 +279,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 float s;
                 int sum;
                 uint32_t p0, p1;
-                quant8<HP>(make_float4(__uint_as_float(av[p].x), __uint_as_float(av[p].y),
-                                       __uint_as_float(av[p].z), __uint_as_float(av[p].w)),
-                           s, sum, p0, p1);
+                float4 xq = make_float4(__uint_as_float(av[p].x), __uint_as_float(av[p].y),
+                                        __uint_as_float(av[p].z), __uint_as_float(av[p].w));
+                if constexpr (NORM) {
+                    const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk);
+                    const float inv = m == 0 ? inv_r[0] : m == 1 ? inv_r[1] : m == 2 ? inv_r[2] : inv_r[3];
+                    xq = make_float4(xq.x * inv * __uint_as_float(wn[p].x), xq.y * inv * __uint_as_float(wn[p].y),
+                                     xq.z * inv * __uint_as_float(wn[p].z), xq.w * inv * __uint_as_float(wn[p].w));
+                    if (a.normOut && g == 0 && blk < nb_rows)
+                        *reinterpret_cast<float4*>(a.normOut + (size_t)m0 * a.K + 32 * blk + 4 * e) = xq;
+                }
+                quant8<HP>(xq, s, sum, p0, p1);
                 if (blk < nb_rows) {
                     const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk), j = blk - m * a.nblk;
                     if (P64) {
@@ -610,6 +675,13 @@ hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, in
     if constexpr (!EXTRA) {
         if (fuse == kFuseMulti)
             return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseMulti, P64, 0>(attr_set, a, grid, lds, st);
+        if constexpr (FUSED) {
+            if (fuse == kFuseNormMulti)
+                return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseNormMulti, P64, 0>(attr_set, a, grid, lds,
+                                                                                              st);
+        } else if (fuse == kFuseNormMulti) {
+            return hipErrorInvalidValue;  // the host normalizes first when the prologue does not quantize
+        }
         switch (pick_dec_window(a, kDecRing)) {
             case kDecWindows[0]:
                 return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, kDecWindows[0]>(attr_set, a,
@@ -619,7 +691,7 @@ hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, in
                                                                                                        grid, lds, st);
             default: break;
         }
-    } else if (fuse == kFuseMulti) {
+    } else if (fuse >= kFuseMulti) {
         return hipErrorInvalidValue;  // the host sends per-block-metadata handles one by one
     }
     return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, 0>(attr_set, a, grid, lds, st);

@@ -337,11 +337,6 @@ __device__ inline bool near_pow2(double v) {
     return m < 0.5 * (1.0 + kNormBand) || m > 1.0 - kNormBand;
 }
 
-__device__ inline long long readlane64(long long v, int l) {
-    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)v, l);
-    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)((unsigned long long)v >> 32), l);
-    return (long long)((unsigned long long)hi << 32 | lo);
-}
 
 template <typename T>
 __device__ inline T block_exclusive_scan(T v, T* wsum, T* total) {
@@ -382,22 +377,11 @@ __device__ inline int norm_classify(double P, double t, unsigned long long* k) {
     return 0;
 }
 
-// Only (float)(ss / H) of the sum enters the output.  The kernel first forms
-// a tree sum T of the same terms, each term passing through at most
-// D = per + 22 roundings (its thread's run, a 64-lane butterfly, the 16 wave
-// totals in order).  All terms are >= 0 and exact (squares of floats), so
-// |T - S| <= gamma_D * S and the reference's in-order sum satisfies
-// |ss - S| <= gamma_(H-1) * S: ss lies within E = (H + D + 2) * 2^-53 * T
-// (with slack for gamma and for rounding T -/+ E) of T.  S -> (float)(S / H)
-// is monotone, so when T - E and T + E map to the same float, ss maps to it
-// too and the in-order reconstruction is skipped.
-__device__ inline bool norm_mean_from_bound(double T, int H, int per, float* mean) {
-    const double E = (double)(H + per + 24) * 0x1p-53 * T * (1.0 + 0x1p-10);
-    const float lo = (float)((T - E) / (double)H), hi = (float)((T + E) / (double)H);
-    *mean = lo;
-    return lo == hi;
-}
-
+// Only (float)(ss / H) of the sum enters the output: the kernel first forms
+// a tree sum of the squares (its thread's run, a 64-lane butterfly, the 16
+// wave totals in order: at most per + 22 roundings per term) and lets
+// norm_mean_from_bound decide; only when it cannot does it rebuild the
+// in-order sum.
 template <bool STAGED>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __restrict__ X, const float* __restrict__ Wt,
                                                                 int H, float eps, float* __restrict__ Out, int exact_only) {
@@ -715,6 +699,8 @@ struct Scratch {
     unsigned int* ticket = nullptr;  // decode argmax: ticket counter, then 8 row keys; zero between calls
     float* gate = nullptr;           // gate projection of the unpaired gate/up path
     size_t gate_cap = 0;
+    float* hn = nullptr;  // normalized rows when the norm runs as its own launch
+    size_t hn_cap = 0;
     // Set for i4_matmul_noalloc_dev: the buffers above are carved from the
     // device's static scratch array and can never grow.
     bool fixed = false;
@@ -1046,6 +1032,12 @@ struct Multi {
     const Handle* h[kMaxSeg];
     float* C[kMaxSeg];
     int n;
+    // RMSNorm of the activation in the launch's prologue (the activation
+    // holds the rows before the norm).
+    bool norm = false;
+    const float* normW = nullptr;
+    float* normOut = nullptr;
+    float eps = 0.0f;
 };
 
 // h2 (gate/up pairing): a second handle with the same layout (same_layout).
@@ -1104,6 +1096,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     if ((h2 || mp) && !dec) return kNotPairable;
     if (mp && (h->extra || dIdx)) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
+    if (mp && mp->norm && !fused) return kNotPairable;
     // Prefill GEMM: more than 8 rows without a legacy corr.
     const bool pre = !dec && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
     const int Mpad = (M + kPfRows - 1) / kPfRows * kPfRows;
@@ -1150,6 +1143,11 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
                 }
             }
             a.ntiles = t;
+            a.normW = mp->normW;
+            a.normOut = mp->normOut;
+            a.norm_eps = mp->eps;
+            const char* ex = std::getenv("BREEZE_HIP_NORM_EXACT");
+            a.norm_exact = ex && ex[0] == '1';
         }
         const int n_cu = device_cus(w, dev);
         a.RG = (M + 3) / 4;
@@ -1197,7 +1195,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         }
         const int grid = a.NG * a.RG;
         const bool x = h->extra;
-        const int fz = pair ? kFusePair : mp ? kFuseMulti : kFusePlain;
+        const int fz = pair ? kFusePair : mp ? (mp->norm ? kFuseNormMulti : kFuseMulti) : kFusePlain;
         if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)
                                  : launch_dec_bits<8, false>(w.attr_set, a, grid, lds, fz, p64, fused, x, st);
         else e = hp ? launch_dec_bits<4, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)
@@ -1268,6 +1266,28 @@ int with_scratch(const Handle* h, hipStream_t st, F&& f) {
     Scratch* s = scratch_for(w, st);
     if (!s) return -4;
     return f(w, *s);
+}
+
+// The decoder's RMSNorm on device pointers (i4_rmsnorm_dev), on stream st.
+int launch_rmsnorm(const float* dX, const float* dW, int M, int H, float eps, float* dOut, hipStream_t st) {
+    if (M < 0 || H <= 0) {
+        set_err("need M >= 0 and H > 0 (got M %d, H %d)", M, H);
+        return -1;
+    }
+    if (M == 0) return 0;
+    if (!dX || !dW || !dOut) {
+        set_err("null device pointer");
+        return -2;
+    }
+    // BREEZE_HIP_NORM_EXACT=1 always takes the in-order reconstruction (tests).
+    const char* ex = std::getenv("BREEZE_HIP_NORM_EXACT");
+    const int exact_only = ex && ex[0] == '1';
+    if (H <= kNormStage)
+        rmsnorm_kernel<true><<<(unsigned)M, kNormThreads, (size_t)H * sizeof(float), st>>>(dX, dW, H, eps, dOut,
+                                                                                           exact_only);
+    else
+        rmsnorm_kernel<false><<<(unsigned)M, kNormThreads, 0, st>>>(dX, dW, H, eps, dOut, exact_only);
+    return hip_ok(hipGetLastError(), "rmsnorm launch") ? 0 : -3;
 }
 
 bool check_dims(int N, int K, int bits) {
@@ -1735,25 +1755,70 @@ int i4_unpack(void* handle, uint8_t* qw, float* scales, uint8_t* zp, int32_t* co
 }
 
 int i4_rmsnorm_dev(const float* dX, const float* dW, int M, int H, float eps, float* dOut, void* stream) {
-    if (M < 0 || H <= 0) {
-        set_err("need M >= 0 and H > 0 (got M %d, H %d)", M, H);
-        return -1;
+    return launch_rmsnorm(dX, dW, M, H, eps, dOut, static_cast<hipStream_t>(stream));
+}
+
+int i4_rmsnorm_matmul_multi_dev(const float* dX, const float* dNormW, float eps, void* const* handles, int n, int M,
+                                float* const* dC, float* dHn, void* stream) {
+    if (!handles || !dC || n < 1 || n > kMaxSeg) {
+        set_err("need 1 to %d handles and as many outputs (got %d)", kMaxSeg, n);
+        return -2;
     }
-    if (M == 0) return 0;
-    if (!dX || !dW || !dOut) {
+    if (!dX || !dNormW) {
         set_err("null device pointer");
         return -2;
     }
+    Multi mp{};
+    mp.n = n;
+    for (int i = 0; i < n; ++i) {
+        Handle* h = as_handle(handles[i]);
+        if (!h) return -1;
+        if (!dC[i]) {
+            set_err("null device pointer");
+            return -2;
+        }
+        if (i > 0 && (h->K != mp.h[0]->K || h->device != mp.h[0]->device)) {
+            set_err("projections of one activation need one K and one device");
+            return -2;
+        }
+        mp.h[i] = h;
+        mp.C[i] = dC[i];
+    }
+    mp.norm = true;
+    mp.normW = dNormW;
+    mp.normOut = dHn;
+    mp.eps = eps;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    // BREEZE_HIP_NORM_EXACT=1 always takes the in-order reconstruction (tests).
-    const char* ex = std::getenv("BREEZE_HIP_NORM_EXACT");
-    const int exact_only = ex && ex[0] == '1';
-    if (H <= kNormStage)
-        rmsnorm_kernel<true><<<(unsigned)M, kNormThreads, (size_t)H * sizeof(float), st>>>(dX, dW, H, eps, dOut,
-                                                                                           exact_only);
-    else
-        rmsnorm_kernel<false><<<(unsigned)M, kNormThreads, 0, st>>>(dX, dW, H, eps, dOut, exact_only);
-    return hip_ok(hipGetLastError(), "rmsnorm launch") ? 0 : -3;
+    Handle* h0 = const_cast<Handle*>(mp.h[0]);
+    const int K = h0->K;
+    return with_scratch(h0, st, [&](Workspace& w, Scratch& s) {
+        bool one = true;
+        for (int i = 1; i < n; ++i) one = one && same_layout_but_n(h0, mp.h[i]);
+        if (one && M > 0) {
+            const int rc = run(w, s, h0, dX, M, mp.C[0], nullptr, nullptr, st, nullptr, &mp);
+            if (rc != kNotPairable) return rc;
+        }
+        if (M <= 0) return M < 0 ? run(w, s, h0, dX, M, mp.C[0], nullptr, nullptr, st) : 0;
+        // The norm as its own launch, then the projections.
+        float* hn = dHn;
+        if (!hn) {
+            if (!grow(w, st, &s.hn, &s.hn_cap, (size_t)M * K, "workspace alloc")) return -4;
+            hn = s.hn;
+        }
+        int rc = launch_rmsnorm(dX, dNormW, M, K, eps, hn, st);
+        if (rc) return rc;
+        Multi plain = mp;
+        plain.norm = false;
+        if (one) {
+            rc = run(w, s, h0, hn, M, plain.C[0], nullptr, nullptr, st, nullptr, &plain);
+            if (rc != kNotPairable) return rc;
+        }
+        for (int i = 0; i < n; ++i) {
+            rc = run(w, s, const_cast<Handle*>(mp.h[i]), hn, M, mp.C[i], nullptr, nullptr, st);
+            if (rc) return rc;
+        }
+        return 0;
+    });
 }
 
 }  // extern "C"

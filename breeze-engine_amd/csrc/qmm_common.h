@@ -226,12 +226,20 @@ struct GemvArgs {
     float* segC[4];
     int segN[4];
     int seg_end[4];
+    // RMSNorm in the prologue (kFuseNormMulti): A holds the rows before the
+    // norm; normW [K] its weights, normOut [M][K] (or NULL) receives the
+    // normalized rows.
+    const float* normW;
+    float* normOut;
+    float norm_eps;
+    int norm_exact;  // always take the in-order sum (tests)
 };
 constexpr int kMaxSeg = 4;
 
 // Decode kernel modes: one weight set, the gate/up pair with the SiLU
-// epilogue, or several projections of one activation.
-constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2;
+// epilogue, several projections of one activation, and the same with the
+// decoder's RMSNorm applied to the activation in the prologue.
+constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3;
 
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
 // (explicit zero points, legacy corr, scale groups smaller than a chunk)
@@ -256,6 +264,77 @@ __device__ inline unsigned long long argmax_key(float v, int idx) {
         o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     }
     return (unsigned long long)o << 32 | (uint32_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+// RMSNorm's mean (float)(ss / H) from a tree sum T of the squares (all
+// >= 0, each exact): every term passes through at most D = per + 22
+// roundings of the tree, so |T - S| <= gamma_D * S for the exact sum S, and
+// the reference's in-order double sum ss (kernel/qwen35_decoder.cpp:137)
+// satisfies |ss - S| <= gamma_(H-1) * S; ss lies within E = (H + D + 2) *
+// 2^-53 * T (with slack for gamma and for rounding T -/+ E) of T.
+// S -> (float)(S / H) is monotone, so when T - E and T + E map to the same
+// float, that is (float)(ss / H).  Returns whether the bound decided it.
+__device__ inline bool norm_mean_from_bound(double T, int H, int per, float* mean) {
+    const double E = (double)(H + per + 24) * 0x1p-53 * T * (1.0 + 0x1p-10);
+    const float lo = (float)((T - E) / (double)H), hi = (float)((T + E) / (double)H);
+    *mean = lo;
+    return lo == hi;
+}
+
+__device__ inline long long readlane64(long long v, int l) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)v, l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)((unsigned long long)v >> 32), l);
+    return (long long)((unsigned long long)hi << 32 | lo);
+}
+
+// Sums of doubles over lane groups by DPP (no LDS permutes): every lane of
+// each aligned 8-lane octet, or 16-lane row, gets its group's sum, each term
+// passing through 3 or 4 roundings.
+__device__ inline double dpp_f64(double v, int ctrl) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+    int lo = (int)(unsigned)b, hi = (int)(unsigned)(b >> 32);
+    switch (ctrl) {  // the control must be a constant
+        case 0xB1:
+            lo = __builtin_amdgcn_update_dpp(0, lo, 0xB1, 0xF, 0xF, false);
+            hi = __builtin_amdgcn_update_dpp(0, hi, 0xB1, 0xF, 0xF, false);
+            break;
+        case 0x4E:
+            lo = __builtin_amdgcn_update_dpp(0, lo, 0x4E, 0xF, 0xF, false);
+            hi = __builtin_amdgcn_update_dpp(0, hi, 0x4E, 0xF, 0xF, false);
+            break;
+        case 0x141:
+            lo = __builtin_amdgcn_update_dpp(0, lo, 0x141, 0xF, 0xF, false);
+            hi = __builtin_amdgcn_update_dpp(0, hi, 0x141, 0xF, 0xF, false);
+            break;
+        default:
+            lo = __builtin_amdgcn_update_dpp(0, lo, 0x140, 0xF, 0xF, false);
+            hi = __builtin_amdgcn_update_dpp(0, hi, 0x140, 0xF, 0xF, false);
+            break;
+    }
+    return __builtin_bit_cast(double, (unsigned long long)(unsigned)hi << 32 | (unsigned)lo);
+}
+__device__ inline double sum8_f64(double v) {
+    v += dpp_f64(v, 0xB1);         // lane ^ 1
+    v += dpp_f64(v, 0x4E);         // lane ^ 2
+    return v + dpp_f64(v, 0x141);  // 7 - lane within the octet
+}
+__device__ inline double sum16_f64(double v) {
+    v = sum8_f64(v);
+    return v + dpp_f64(v, 0x140);  // 15 - lane within the row
+}
+
+// The reference's in-order double sum of squares of x[0..H), by one wave
+// (every lane returns it): the slow way, for rows the bound does not decide.
+__device__ inline double norm_sumsq_inorder(const float* x, int H) {
+    const int lane = threadIdx.x & 63;
+    double ss = 0.0;
+    for (int c = 0; c < H; c += 64) {
+        const float v = c + lane < H ? x[c + lane] : 0.0f;
+        const double t = (double)v * (double)v;
+        const int n = min(64, H - c);
+        for (int l = 0; l < n; ++l) ss += __shfl(t, l);
+    }
+    return ss;
 }
 
 // Barrier that orders LDS only: outstanding global loads stay in flight.

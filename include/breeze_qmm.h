@@ -126,6 +126,19 @@ int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64
  * i4_matmul_dev. */
 int i4_matmul_multi_dev(void* const* handles, int n, const float* dA, int M, float* const* dC, void* stream);
 
+/* The decoder's RMSNorm followed by the projections of its output, replacing
+ * rmsnorm(hn, h, w) and the i4_matmul calls on hn that follow it
+ * (kernel/qwen35_decoder.cpp:279 and 285-288, 405-407, 419-420):
+ *   hn = rmsnorm(dX[M, K], dNormW[K], eps),  dC[i][M, N_i] = hn * W_i.
+ * hn is bit-identical to i4_rmsnorm_dev's and every output to
+ * i4_matmul_dev's on it.  When the decode kernel quantizes the activation
+ * itself (M <= 8 with M <= 4 rows of K/32 <= 512/M blocks, e.g. up to three
+ * rows of K = 5120) and the handles share a device layout, the norm runs in
+ * the prologue of the one projection launch; otherwise it is its own launch
+ * first.  dHn (may be NULL) receives hn [M, K].  Returns as i4_matmul_dev. */
+int i4_rmsnorm_matmul_multi_dev(const float* dX, const float* dNormW, float eps, void* const* handles, int n, int M,
+                                float* const* dC, float* dHn, void* stream);
+
 /* Handle facts: out[0..7] = N, K, bits, scale group (blocks per distinct
  * scale, 0 = one per column), has_zero_points, has_corr_delta,
  * device bytes held, device ordinal.  Returns 0 or -1. */
