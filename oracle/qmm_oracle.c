@@ -230,26 +230,45 @@ ORC_API void orc_chain(const int32_t* cs, const float* sa, const float* sb, int 
 static int run_path(const int16_t* b, const float* sb, const int32_t* delta, int N, int K,
                     const float* A, int M, int hi_prec, float* C, int32_t* cs_out) {
     const int nblk = K / 32;
+    const int32_t mult = hi_prec ? 256 : 1;
     int16_t* q = malloc(sizeof(int16_t) * (size_t)M * K);
     float* sa = malloc(sizeof(float) * (size_t)M * nblk);
-    int32_t* cs = cs_out ? cs_out : malloc(sizeof(int32_t) * (size_t)M * N * nblk);
     int rc = -2;
-    if (q && sa && cs) {
+    if (q && sa) {
         orc_quantize(A, M, K, hi_prec, q, sa, NULL);
-        orc_block_dots(q, M, b, N, K, cs);
-        if (delta) {
-            const int32_t mult = hi_prec ? 256 : 1;
-            for (int m = 0; m < M; ++m)
-                for (int n = 0; n < N; ++n)
-                    for (int j = 0; j < nblk; ++j)
-                        cs[((size_t)m * N + n) * nblk + j] += mult * delta[(size_t)n * nblk + j];
+        if (cs_out) {
+            orc_block_dots(q, M, b, N, K, cs_out);
+            if (delta)
+                for (int m = 0; m < M; ++m)
+                    for (int n = 0; n < N; ++n)
+                        for (int j = 0; j < nblk; ++j)
+                            cs_out[((size_t)m * N + n) * nblk + j] += mult * delta[(size_t)n * nblk + j];
+            orc_chain(cs_out, sa, sb, M, N, nblk, C);
+        } else {
+            /* The same block integers and chain as orc_block_dots,
+             * the delta term and orc_chain, one output at a time (outputs
+             * are independent, so the threads change no bit). */
+#pragma omp parallel for schedule(static)
+            for (long long mn = 0; mn < (long long)M * N; ++mn) {
+                const int m = (int)(mn / N), n = (int)(mn % N);
+                float acc = 0.0f;
+                for (int j = 0; j < nblk; ++j) {
+                    const int16_t* x = q + (size_t)m * K + 32 * j;
+                    const int16_t* w = b + (size_t)n * K + 32 * j;
+                    int64_t s = 0;
+                    for (int i = 0; i < 32; ++i) s += (int64_t)x[i] * w[i];
+                    int32_t c = (int32_t)s;
+                    if (delta) c += mult * delta[(size_t)n * nblk + j];
+                    const float f = (float)c * sb[(size_t)n * nblk + j];
+                    acc = fmaf(sa[(size_t)m * nblk + j], f, acc);
+                }
+                C[mn] = acc;
+            }
         }
-        orc_chain(cs, sa, sb, M, N, nblk, C);
         rc = 0;
     }
     free(q);
     free(sa);
-    if (cs != cs_out) free(cs);
     return rc;
 }
 

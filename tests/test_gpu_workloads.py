@@ -4,9 +4,9 @@ Each workload's seeded inputs (oracle.make_config) go through the device
 entry point and are compared bit-for-bit with the C restatement of the
 reference arithmetic, in the reference's high-precision (two-pass INT16)
 activation mode that the workloads specify.  The LM head also checks the
-fused argmax index exactly; the prefill workload checks a row subset through
-the row-independence property (row m of an M-row call equals the same row
-computed alone, tests/test_cpu_packing.py:155-168 of the reference).
+fused argmax index exactly; the prefill workloads compare all 512 rows (the
+oracle computes its outputs on every core, one output per task, which
+changes no bit).
 """
 import numpy as np
 import pytest
@@ -75,6 +75,6 @@ def test_prefill_rows_bit_exact(gpu, hb, orc, hi_prec, name):
         got = _device_matmul(hb, gpu, h, d["A"], N)
     finally:
         hb.free(h)
-    rows = [0, 1, 127, 128, 300, 511]
-    want = orc.matmul(d["qweight"], d["scales"], None, N, K, bits, d["A"][rows], True)
-    assert bits_equal(got[rows], want)
+    want = orc.matmul(d["qweight"], d["scales"], None, N, K, bits, d["A"], True)
+    bad = np.nonzero(np.any(got.view(np.uint32) != want.view(np.uint32), axis=1))[0]
+    assert bad.size == 0, (name, bad[:10].tolist())
