@@ -475,3 +475,29 @@ def test_non_finite_and_extreme_activations(gpu, hb, orc, hi_prec, bits, explici
                     assert _nan_aware_equal(c_dev, want), (K, groups, hp, x.shape)
         finally:
             hb.free(h)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_decode_rows_from_global_records_with_argmax(gpu, hb, orc, hi_prec, bits):
+    """Three to eight rows whose records the decode prologue does not
+    quantize (K = 4640: 145 blocks, a partial last chunk) read their A
+    operands from the chunk-major records in global memory, all rows in one
+    workgroup; outputs bit-exact and the argmax of every row first-max
+    exact, several tiles per workgroup (N = 16 * 600)."""
+    N, K = 16 * 600, 4640
+    rng = np.random.default_rng(60 + bits)
+    qw, sc, _ = rng_weights(rng, N, K, bits)
+    h = hb.prepack(qw, sc, None, K, N, bits=bits)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for rows in (4, 5, 7, 8):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                A[rng.random(A.shape) < 0.01] *= 20.0
+                want = orc.matmul(qw, sc, None, N, K, bits, A, hp)
+                c, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+                gpu.cuda.synchronize()
+                assert bits_equal(c.cpu().numpy(), want), (hp, rows)
+                assert idx.cpu().tolist() == np.argmax(want, axis=1).tolist(), (hp, rows)
+    finally:
+        hb.free(h)
