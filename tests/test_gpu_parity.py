@@ -478,12 +478,12 @@ def test_non_finite_and_extreme_activations(gpu, hb, orc, hi_prec, bits, explici
 
 
 @pytest.mark.parametrize("bits", [4, 8])
-def test_decode_rows_from_global_records_with_argmax(gpu, hb, orc, hi_prec, bits):
-    """Three to eight rows whose records the decode prologue does not
-    quantize (K = 4640: 145 blocks, a partial last chunk) read their A
-    operands from the chunk-major records in global memory, all rows in one
-    workgroup; outputs bit-exact and the argmax of every row first-max
-    exact, several tiles per workgroup (N = 16 * 600)."""
+def test_decode_staged_rows_with_argmax(gpu, hb, orc, hi_prec, bits):
+    """Four to eight rows whose records come from the stand-alone quantizer
+    (K = 4640: 145 blocks, a partial last chunk; five to eight rows in two
+    row-group workgroups per tile range): outputs bit-exact and the argmax
+    of every row first-max exact, several tiles per workgroup
+    (N = 16 * 600)."""
     N, K = 16 * 600, 4640
     rng = np.random.default_rng(60 + bits)
     qw, sc, _ = rng_weights(rng, N, K, bits)
