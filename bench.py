@@ -353,7 +353,7 @@ def main():
         if name == "rmsnorm":
             m = int(r) if r else 1
             t = time_rmsnorm(hb, torch, m, args.steps, args.warmup)
-            print(json.dumps({"workload": f"RMSNorm M={m} H={RMSNORM_H} (in-order double sum, exact)",
+            print(json.dumps({"workload": f"RMSNorm M={m} H={RMSNORM_H} (bit-identical to the in-order double sum)",
                               "steps": args.steps, "us": round(t * 1e6, 3)}), flush=True)
             return
         if name not in workloads.LABELS:
@@ -395,7 +395,7 @@ def main():
             rows.append(entry)
             print(f"bench: {entry}", file=sys.stderr, flush=True)
         t = time_rmsnorm(hb, torch, 1, args.steps, args.warmup)
-        rows.append({"workload": f"RMSNorm M=1 H={RMSNORM_H} (in-order double sum, exact)", "us": round(t * 1e6, 2)})
+        rows.append({"workload": f"RMSNorm M=1 H={RMSNORM_H} (bit-identical to the in-order double sum)", "us": round(t * 1e6, 2)})
         for label in MULTI_SHAPES:
             for m in (1, 4):
                 r = time_multi(hb, torch, label, m, args.steps, args.warmup)

@@ -7,6 +7,7 @@ already using the previous library keeps its inode.
 import os
 import subprocess
 import sys
+import tempfile
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(os.path.dirname(PKG), "csrc")
@@ -59,35 +60,41 @@ def _run(cmd, verbose):
 
 def build(verbose=False):
     """Device code objects and host code in two passes (run side by side),
-    so device-only flags never reach the host compiler; then one link."""
+    so device-only flags never reach the host compiler; then one link.
+    Intermediates live in a temporary directory, and every compiler process
+    is reaped before it goes, so a failed build leaves nothing behind."""
     out = lib_path()
-    tag = f"{out}.{os.getpid()}"
-    tmp = f"{tag}.tmp"
+    tmp = f"{out}.{os.getpid()}.tmp"
     srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    fatbins = [f"{tag}.{i}.hipfb" for i in range(len(srcs))]
-    objs = [f"{tag}.{i}.o" for i in range(len(srcs))]
-    try:
-        procs = [(_run([HIPCC, "-x", "hip", *FLAGS, *DEVICE_FLAGS, "--offload-device-only", "-c", s, "-o", fb],
-                       verbose), s) for s, fb in zip(srcs, fatbins)]
+    running = []
+
+    def finish(procs, what):
         for p, s in procs:
             _, err = p.communicate()
             if p.returncode != 0:
-                raise RuntimeError(f"hipcc (device pass of {s}) failed ({p.returncode}):\n{err[-4000:]}")
-        procs = [(_run([HIPCC, "-x", "hip", *FLAGS, "--offload-host-only", "-Xclang", "-fcuda-include-gpubinary",
-                        "-Xclang", fb, "-c", s, "-o", o], verbose), s) for s, fb, o in zip(srcs, fatbins, objs)]
-        for p, s in procs:
-            _, err = p.communicate()
-            if p.returncode != 0:
-                raise RuntimeError(f"hipcc (host pass of {s}) failed ({p.returncode}):\n{err[-4000:]}")
-        p = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose)
-        _, err = p.communicate()
-        if p.returncode != 0:
-            raise RuntimeError(f"link failed ({p.returncode}):\n{err[-4000:]}")
-        os.replace(tmp, out)
-    finally:
-        for f in (tmp, *fatbins, *objs):
-            if os.path.exists(f):
-                os.unlink(f)
+                raise RuntimeError(f"hipcc ({what} of {s}) failed ({p.returncode}):\n{err[-4000:]}")
+
+    with tempfile.TemporaryDirectory(prefix="breeze_qmm_build_") as work:
+        fatbins = [os.path.join(work, f"{i}.hipfb") for i in range(len(srcs))]
+        objs = [os.path.join(work, f"{i}.o") for i in range(len(srcs))]
+        try:
+            running = [(_run([HIPCC, "-x", "hip", *FLAGS, *DEVICE_FLAGS, "--offload-device-only", "-c", s, "-o", fb],
+                             verbose), s) for s, fb in zip(srcs, fatbins)]
+            finish(running, "device pass")
+            running = [(_run([HIPCC, "-x", "hip", *FLAGS, "--offload-host-only", "-Xclang",
+                              "-fcuda-include-gpubinary", "-Xclang", fb, "-c", s, "-o", o], verbose), s)
+                       for s, fb, o in zip(srcs, fatbins, objs)]
+            finish(running, "host pass")
+            running = [(_run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp], verbose), "link")]
+            finish(running, "link")
+            os.replace(tmp, out)
+        finally:
+            for p, _ in running:
+                if p.poll() is None:
+                    p.kill()
+                p.communicate()
+            if os.path.exists(tmp):
+                os.unlink(tmp)
     return out
 
 
