@@ -28,7 +28,11 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--headline-only]
 
 --workload times one workload alone and prints its own JSON line (for
 profiling one kernel); the default run prints the contract line above.
-``--workload rmsnorm[:ROWS]`` times the decoder's exact RMSNorm at width 5120.
+``--workload rmsnorm[:ROWS]`` times the decoder's exact RMSNorm at width 5120,
+``--workload rmsnorm_worst[:ROWS]`` its one-wave fallback (rows that
+defeat the parallel in-order rebuild, with that rebuild forced), and
+``--workload multi[:ROWS]`` the decoder's projections of one activation (one
+launch, one launch per projection, and with the RMSNorm in front).
 """
 import argparse
 import json
@@ -270,15 +274,24 @@ def time_multi(hb, torch, label, rows, steps, warmup):
 RMSNORM_H = 5120
 
 
-def time_rmsnorm(hb, torch, rows, steps, warmup):
+def time_rmsnorm(hb, torch, rows, steps, warmup, worst=False):
     """Per-call time (s) of the decoder's exact RMSNorm (i4_rmsnorm_dev) on
     `rows` rows of width 5120 (the hidden size of the prefill and LM-head
     shapes), called through the C ABI with preallocated buffers and timed
-    like the matmul workloads."""
+    like the matmul workloads.  worst: rows whose partial sums all stay next
+    to a power of two (1.0, then 5119 terms of 2^-30), with the in-order sum
+    forced (BREEZE_HIP_NORM_EXACT=1), so every row takes the kernel's
+    fallback: one wave summing in element order."""
     import numpy as np
 
     rng = np.random.default_rng(7)
-    x = torch.from_numpy(rng.standard_normal((rows, RMSNORM_H)).astype(np.float32)).cuda()
+    if worst:
+        xa = np.full((rows, RMSNORM_H), 2.0 ** -30, np.float32)
+        xa[:, 0] = 1.0
+        os.environ["BREEZE_HIP_NORM_EXACT"] = "1"
+    else:
+        xa = rng.standard_normal((rows, RMSNORM_H)).astype(np.float32)
+    x = torch.from_numpy(xa).cuda()
     w = torch.from_numpy((1 + 0.1 * rng.standard_normal(RMSNORM_H)).astype(np.float32)).cuda()
     out = torch.empty_like(x)
     stream = torch.cuda.current_stream()
@@ -350,10 +363,13 @@ def main():
                 print(json.dumps({"workload": f"{label} M={m}", "us": {k: round(v * 1e6, 3) for k, v in res.items()}}),
                       flush=True)
             return
-        if name == "rmsnorm":
+        if name in ("rmsnorm", "rmsnorm_worst"):
             m = int(r) if r else 1
-            t = time_rmsnorm(hb, torch, m, args.steps, args.warmup)
-            print(json.dumps({"workload": f"RMSNorm M={m} H={RMSNORM_H} (bit-identical to the in-order double sum)",
+            worst = name == "rmsnorm_worst"
+            t = time_rmsnorm(hb, torch, m, args.steps, args.warmup, worst=worst)
+            what = ("in-order fallback of one wave, in-order sum forced" if worst
+                    else "bit-identical to the in-order double sum")
+            print(json.dumps({"workload": f"RMSNorm M={m} H={RMSNORM_H} ({what})",
                               "steps": args.steps, "us": round(t * 1e6, 3)}), flush=True)
             return
         if name not in workloads.LABELS:

@@ -320,7 +320,8 @@ int pick_pf_ct(int ntiles, int gy, int n_cu, const char* force) {
 // the "anchors" -- exact specials and the first tie after each -- need the
 // running sum: one wave walks them in order, with everything between two
 // anchors summed in parallel beforehand.  Rows with more than kNormMaxSpecial
-// specials are summed by one thread in element order.  Rows up to kNormStage
+// specials are summed in element order by wave 0 alone (one running sum,
+// 64 terms squared at a time).  Rows up to kNormStage
 // wide are staged in LDS and each thread holds its (at most kNormPer) terms
 // and their classes in registers; wider rows are read from memory per pass.
 constexpr int kNormThreads = 1024;
@@ -605,10 +606,10 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
                 S += (long long)seg[nspec];
                 if (tid == 0) ss_s = nspec ? __builtin_ldexp((double)S, e - 52) : 0.0;
             }
-        } else if (tid == 0) {
-            double acc = 0.0;
-            for (int j = 0; j < H; ++j) acc += (double)x[j] * (double)x[j];
-            ss_s = acc;
+        } else if (tid < 64) {
+            // Too many specials for the walk: wave 0 sums in element order.
+            const double acc = norm_sumsq_inorder(x, H);
+            if (tid == 0) ss_s = acc;
         }
     }
     __syncthreads();

@@ -326,13 +326,22 @@ __device__ inline double sum16_f64(double v) {
 // The reference's in-order double sum of squares of x[0..H), by one wave
 // (every lane returns it): the slow way, for rows the bound does not decide.
 __device__ inline double norm_sumsq_inorder(const float* x, int H) {
+    // Every lane of the wave holds the same running sum; the wave squares 64
+    // elements at a time (exactly, in double) and each term enters the sum
+    // in element order through v_readlane, so only the adds form the chain.
     const int lane = threadIdx.x & 63;
     double ss = 0.0;
-    for (int c = 0; c < H; c += 64) {
+    int c = 0;
+    for (; c + 64 <= H; c += 64) {
+        const float v = x[c + lane];
+        const long long tb = __builtin_bit_cast(long long, (double)v * (double)v);
+#pragma unroll
+        for (int l = 0; l < 64; ++l) ss += __builtin_bit_cast(double, readlane64(tb, l));
+    }
+    if (c < H) {
         const float v = c + lane < H ? x[c + lane] : 0.0f;
-        const double t = (double)v * (double)v;
-        const int n = min(64, H - c);
-        for (int l = 0; l < n; ++l) ss += __shfl(t, l);
+        const long long tb = __builtin_bit_cast(long long, (double)v * (double)v);
+        for (int l = 0; l < H - c; ++l) ss += __builtin_bit_cast(double, readlane64(tb, l));
     }
     return ss;
 }

@@ -8,7 +8,7 @@ shipped, and with BREEZE_HIP_NORM_EXACT=1, which always takes the in-order
 rebuild.  The rows stress what that rebuild depends on: exact ties of both
 parities, terms that round away, binade crossings, zeros, leading zeros,
 outliers, denormal and non-finite inputs, a row whose partial sums hug a
-power of two (the single-thread fallback), and a row whose mean is a float
+power of two (the one-wave fallback), and a row whose mean is a float
 rounding midpoint (the bound cannot decide it).  Widths straddle the
 kernel's one-to-two terms per thread step (1024/1025) and its staged /
 unstaged switch (8192/8193).
