@@ -2,5 +2,5 @@
 #include "prefill_kernel.h"
 
 namespace bq {
-template hipError_t launch_pf<4, false>(bool*, const PfArgs&, int, int, dim3, hipStream_t);
+template hipError_t launch_pf<4, false>(bool*, const PfArgs&, int, int, int, dim3, hipStream_t);
 }  // namespace bq

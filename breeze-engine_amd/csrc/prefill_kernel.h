@@ -6,18 +6,20 @@
 
 namespace bq {
 
-template <int BITS, bool HP, int SCM, int CT>
+template <int BITS, bool HP, int SCM, int CT, int RP>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
-    using L = PfLayout<CT, SCM, BITS>;
+    using L = PfLayout<CT, SCM, BITS, RP>;
     extern __shared__ __align__(16) char pf_lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int col = lane & 15, grp = lane >> 4;
-    // Wave w: row pair w&3 (two 16-row tiles) and column half w>>2, so each
-    // SIMD (waves w and w+4) holds one wave of each half.
-    const int rp = wave & 3, half = wave >> 2;
+    // Wave w: row pair w % RP (two 16-row tiles) and column part w / RP of
+    // the kParts parts; waves w and w + 4 share a SIMD.
+    constexpr int kParts = kPfWaves / RP;
+    static_assert(kPfWaves % RP == 0 && CT >= kParts, "every part holds a tile");
+    const int rp = wave % RP, part = wave / RP;
     const int t0 = blockIdx.x * CT;
-    const int rt0 = blockIdx.y * kPfWaves + 2 * rp;
+    const int rt0 = blockIdx.y * (2 * RP) + 2 * rp;
     const bool active = rt0 * 16 < a.M;
     const uint32_t lds0 = __builtin_amdgcn_readfirstlane(lds_address(pf_lds));
     const int nch = a.nch;
@@ -89,13 +91,24 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             gstep[k] = 64;
         }
     }
-    // This wave's two activation records per chunk.
-    const char* rec0 = a.R + (size_t)rt0 * nch * kRecBytes + 16 * lane;
-    const size_t rec_step = (size_t)nch * kRecBytes;  // next row tile
+    // The workgroup's 2 RP activation records per chunk, 3 DMA units each
+    // (bytes 0 and 1024 and the tail from 1152; the last two overlap), split
+    // over the waves: unit wave + 8 i, clamped, so a spare slot repeats the
+    // last unit's load (same bytes to the same place).
+    constexpr int kRecUnits = 6 * RP, kRecPerWave = (kRecUnits + kPfWaves - 1) / kPfWaves;
+    const char* rec0 = a.R + (size_t)blockIdx.y * (2 * RP) * nch * kRecBytes + 16 * lane;
+    uint32_t rec_src[kRecPerWave], rec_dst[kRecPerWave];
+#pragma unroll
+    for (int i = 0; i < kRecPerWave; ++i) {
+        const int u = min(wave + kPfWaves * i, kRecUnits - 1), r = u / 3, pt = u % 3;
+        const int off = pt == 0 ? 0 : pt == 1 ? 1024 : 1152;
+        rec_src[i] = (uint32_t)(r * nch * kRecBytes + off);
+        rec_dst[i] = (uint32_t)(L::kA + r * kRecBytes + off);
+    }
 
     // Load d of this wave's kDmaChunk loads of chunk c into the chunk region
-    // at LDS address cbase: the shared slots, then 3 per activation record.
-    constexpr int kDmaChunk = L::kPerWave + 6;
+    // at LDS address cbase: the shared slots, then its record units.
+    constexpr int kDmaChunk = L::kPerWave + kRecPerWave;
     // INT4: only chunk 0 of a stage (first) carries the stage's shared loads.
     auto dma_slot = [&](int c, uint32_t cbase, int d, bool first) {
         if (d < L::kPerWave) {
@@ -108,10 +121,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                 dma16(src0[d] + (size_t)sg * step[d] + g * gstep[d], (to_raw[d] ? lds0 : cbase) + x0s[d]);
             }
         } else {
-            const int e = d - L::kPerWave, r = e / 3, part = e % 3;
-            const int off = part == 0 ? 0 : part == 1 ? 1024 : 1152;
-            dma16(rec0 + r * rec_step + (size_t)c * kRecBytes + off,
-                  cbase + (uint32_t)(L::kA + (2 * rp + r) * kRecBytes + off));
+            const int e = d - L::kPerWave;
+            dma16(rec0 + rec_src[e] + (size_t)c * kRecBytes, cbase + rec_dst[e]);
         }
     };
     auto issue_chunk = [&](int c, uint32_t cbase, bool first) {
@@ -205,9 +216,10 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     auto run32 = [&](auto ctw_tag, int toff) {
         constexpr int CTW = decltype(ctw_tag)::value;
         constexpr int NG = CTW / 2;
+        constexpr int NG1 = NG > 0 ? NG : 1;  // array extents (a part of one tile has no group)
         constexpr bool ODD = (CTW & 1) != 0;
         const int c32 = lane & 31, kh = lane >> 5;
-        float sbg[NG], sbo = 0.0f;
+        float sbg[NG1], sbo = 0.0f;
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             sbg[g] = 0.0f;
@@ -221,7 +233,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             sbo = reinterpret_cast<const float*>(a.S)[(size_t)min(t0 + toff + CTW - 1, a.ntiles - 1) * a.ngrp * 16 + col];
             asm volatile("" ::"v"(sbo));
         }
-        float acc[NG][16], acco[2][4];
+        float acc[NG1][16], acco[2][4];
 #pragma unroll
         for (int g = 0; g < NG; ++g)
 #pragma unroll
@@ -298,9 +310,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                     sbo2[0] = sbo2[1] = sbo;
                 }
             };
-            v4i bq[NG][2];  // B operand per group and block
-            int2 wsg[NG];
-            float sbv[NG][2];
+            v4i bq[NG1][2];  // B operand per group and block
+            int2 wsg[NG1];
+            float sbv[NG1][2];
             auto load_group = [&](int g) {
                 if (g >= NG) return;
                 const int t = toff + 2 * g + (c32 >> 4);
@@ -326,7 +338,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             auto bopo = [&](int b) -> uint64_t {
                 return b == 0 ? ((uint64_t)bwo.y << 32 | bwo.x) : ((uint64_t)bwo.w << 32 | bwo.z);
             };
-            v16i h32[NGB], d32[NGB];
+            v16i h32[NGB > 0 ? NGB : 1], d32[NGB > 0 ? NGB : 1];
             v4i ho[2][2], dov[2][2];
             const v16i z16 = {};
             auto step_h = [&](int s) {
@@ -474,18 +486,26 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             }
         }
     };
-    if (half == 0) run32(std::integral_constant<int, (CT + 1) / 2>{}, 0);
-    else run32(std::integral_constant<int, CT / 2>{}, (CT + 1) / 2);
+    // Part q: tiles [q CTB + min(q, CTR), ...), CTB + 1 of them for q < CTR.
+    constexpr int CTB = CT / kParts, CTR = CT % kParts;
+    const int toff = part * CTB + min(part, CTR);
+    if constexpr (CTR > 0) {
+        if (part < CTR) {
+            run32(std::integral_constant<int, CTB + 1>{}, toff);
+            return;
+        }
+    }
+    run32(std::integral_constant<int, CTB>{}, toff);
 }
 
 
-template <int BITS, bool HP, int SCM, int CT>
+template <int BITS, bool HP, int SCM, int CT, int RP>
 hipError_t launch_pf_t(bool* pf_attr, const PfArgs& p, dim3 grid, hipStream_t st) {
-    using L = PfLayout<CT, SCM, BITS>;
-    auto kern = prefill_kernel<BITS, HP, SCM, CT>;
+    using L = PfLayout<CT, SCM, BITS, RP>;
+    auto kern = prefill_kernel<BITS, HP, SCM, CT, RP>;
     int slot = 0;
-    while (kPfCts[slot] != CT) ++slot;
-    const int key = (HP ? 1 : 0) | SCM << 1 | slot << 3 | (BITS == 4 ? 32 : 0);
+    while (kPfCfgs[slot].rp != RP || kPfCfgs[slot].ct != CT) ++slot;
+    const int key = (HP ? 1 : 0) | SCM << 1 | slot << 3 | (BITS == 4 ? 128 : 0);
     if (!pf_attr[key]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, L::kBytes);
@@ -496,21 +516,32 @@ hipError_t launch_pf_t(bool* pf_attr, const PfArgs& p, dim3 grid, hipStream_t st
     return hipGetLastError();
 }
 
+// One case per entry of kPfCfgs.
 template <int BITS, bool HP, int SCM>
-hipError_t launch_pf_scm(bool* pf_attr, const PfArgs& p, int ct, dim3 grid, hipStream_t st) {
-    switch (ct) {
-        case 17: return launch_pf_t<BITS, HP, SCM, 17>(pf_attr, p, grid, st);
-        case 16: return launch_pf_t<BITS, HP, SCM, 16>(pf_attr, p, grid, st);
-        case 8: return launch_pf_t<BITS, HP, SCM, 8>(pf_attr, p, grid, st);
-        default: return launch_pf_t<BITS, HP, SCM, 4>(pf_attr, p, grid, st);
+hipError_t launch_pf_scm(bool* pf_attr, const PfArgs& p, int rp, int ct, dim3 grid, hipStream_t st) {
+    switch (rp * 100 + ct) {
+        case 417: return launch_pf_t<BITS, HP, SCM, 17, 4>(pf_attr, p, grid, st);
+        case 416: return launch_pf_t<BITS, HP, SCM, 16, 4>(pf_attr, p, grid, st);
+        case 413: return launch_pf_t<BITS, HP, SCM, 13, 4>(pf_attr, p, grid, st);
+        case 412: return launch_pf_t<BITS, HP, SCM, 12, 4>(pf_attr, p, grid, st);
+        case 409: return launch_pf_t<BITS, HP, SCM, 9, 4>(pf_attr, p, grid, st);
+        case 408: return launch_pf_t<BITS, HP, SCM, 8, 4>(pf_attr, p, grid, st);
+        case 405: return launch_pf_t<BITS, HP, SCM, 5, 4>(pf_attr, p, grid, st);
+        case 404: return launch_pf_t<BITS, HP, SCM, 4, 4>(pf_attr, p, grid, st);
+        case 216: return launch_pf_t<BITS, HP, SCM, 16, 2>(pf_attr, p, grid, st);
+        case 208: return launch_pf_t<BITS, HP, SCM, 8, 2>(pf_attr, p, grid, st);
+        case 204: return launch_pf_t<BITS, HP, SCM, 4, 2>(pf_attr, p, grid, st);
+        case 116: return launch_pf_t<BITS, HP, SCM, 16, 1>(pf_attr, p, grid, st);
+        case 108: return launch_pf_t<BITS, HP, SCM, 8, 1>(pf_attr, p, grid, st);
+        default: return hipErrorInvalidValue;
     }
 }
 
 template <int BITS, bool HP>
-hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int ct, dim3 grid, hipStream_t st) {
-    if (scm == 2) return launch_pf_scm<BITS, HP, 2>(pf_attr, p, ct, grid, st);
-    if (scm == 1) return launch_pf_scm<BITS, HP, 1>(pf_attr, p, ct, grid, st);
-    return launch_pf_scm<BITS, HP, 0>(pf_attr, p, ct, grid, st);
+hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int rp, int ct, dim3 grid, hipStream_t st) {
+    if (scm == 2) return launch_pf_scm<BITS, HP, 2>(pf_attr, p, rp, ct, grid, st);
+    if (scm == 1) return launch_pf_scm<BITS, HP, 1>(pf_attr, p, rp, ct, grid, st);
+    return launch_pf_scm<BITS, HP, 0>(pf_attr, p, rp, ct, grid, st);
 }
 
 }  // namespace bq

@@ -278,25 +278,43 @@ __global__ __launch_bounds__(256) void quantize_rec_kernel(const float* __restri
     }
 }
 
-// Column tiles per workgroup: the instantiated widths, and the choice that
-// minimizes (workgroup rounds) x (tiles per workgroup) at one workgroup per
-// CU.  `force` (the BREEZE_HIP_PREFILL_CT environment variable) selects an
-// instantiated width instead, for tests and tuning.
-
-int pick_pf_ct(int ntiles, int gy, int n_cu, const char* force) {
+// Row pairs per prefill workgroup: 32 rows for up to 32 rows, 64 for up to
+// 64, otherwise 128.  `force` (BREEZE_HIP_PREFILL_RP) selects 1, 2 or 4 for
+// tests.
+int pick_pf_rp(int M, const char* force) {
     if (force) {
         const int v = std::atoi(force);
-        for (int ct : kPfCts)
-            if (ct == v) return ct;
+        if (v == 1 || v == 2 || v == 4) return v;
     }
-    int best = kPfCts[0];
+    return M <= 32 ? 1 : M <= 64 ? 2 : 4;
+}
+
+// Column tiles per workgroup for rp row pairs: among the instantiated
+// widths, the one that minimizes (workgroup rounds at one workgroup per CU)
+// x (tiles on the busiest SIMD, whose two waves hold column parts s / rp and
+// (s + 4) / rp).  `force` (BREEZE_HIP_PREFILL_CT) selects an instantiated
+// width for rp instead, for tests and tuning.
+int pick_pf_ct(int ntiles, int gy, int rp, int n_cu, const char* force) {
+    if (force) {
+        const int v = std::atoi(force);
+        for (const PfCfg& c : kPfCfgs)
+            if (c.rp == rp && c.ct == v) return v;
+    }
+    int best = 0;
     long best_cost = -1;
-    for (int ct : kPfCts) {
-        const long wgs = (long)((ntiles + ct - 1) / ct) * gy;
-        const long cost = (wgs + n_cu - 1) / n_cu * ct;
+    for (const PfCfg& c : kPfCfgs) {
+        if (c.rp != rp) continue;
+        const int parts = kPfWaves / rp, ctb = c.ct / parts, ctr = c.ct % parts;
+        int simd = 0;
+        for (int sm = 0; sm < 4; ++sm) {
+            const int q0 = sm / rp, q1 = (sm + 4) / rp;
+            simd = std::max(simd, 2 * ctb + (q0 < ctr) + (q1 < ctr));
+        }
+        const long wgs = (long)((ntiles + c.ct - 1) / c.ct) * gy;
+        const long cost = (wgs + n_cu - 1) / n_cu * simd;
         if (best_cost < 0 || cost < best_cost) {
             best_cost = cost;
-            best = ct;
+            best = c.ct;
         }
     }
     return best;
@@ -717,7 +735,7 @@ struct Workspace {
     hipStream_t stream = nullptr;
     int n_cu = 0;
     bool attr_set[1024] = {};
-    bool pf_attr[64] = {};
+    bool pf_attr[256] = {};
 };
 
 constexpr int kMaxDevices = 64;
@@ -1100,7 +1118,9 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     if (mp && mp->norm && !fused) return kNotPairable;
     // Prefill GEMM: more than 8 rows without a legacy corr.
     const bool pre = !dec && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
-    const int Mpad = (M + kPfRows - 1) / kPfRows * kPfRows;
+    const int pf_rp = pick_pf_rp(M, std::getenv("BREEZE_HIP_PREFILL_RP"));
+    const int pf_rows = 32 * pf_rp;  // rows per prefill workgroup
+    const int Mpad = (M + pf_rows - 1) / pf_rows * pf_rows;
     const int nch_rec = (h->nblk + 1) / 2;  // record chunks of two blocks
     if (pre) {
         // Records in MFMA operand order for the prefill GEMM.
@@ -1222,12 +1242,15 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
             set_err("internal: INT4 handle with per-block scales has no zero points");
             return -5;
         }
-        const int gy = Mpad / kPfRows;
-        const int ct = pick_pf_ct(p.ntiles, gy, device_cus(w, dev), std::getenv("BREEZE_HIP_PREFILL_CT"));
+        const int gy = Mpad / pf_rows;
+        const int ct = pick_pf_ct(p.ntiles, gy, pf_rp, device_cus(w, dev), std::getenv("BREEZE_HIP_PREFILL_CT"));
         const dim3 grid((unsigned)((p.ntiles + ct - 1) / ct), (unsigned)gy);
-        if (h->bits == 8) e = hp ? launch_pf<8, true>(w.pf_attr, p, scm, ct, grid, st) : launch_pf<8, false>(w.pf_attr, p, scm, ct, grid, st);
-        else e = hp ? launch_pf<4, true>(w.pf_attr, p, scm, ct, grid, st) : launch_pf<4, false>(w.pf_attr, p, scm, ct, grid, st);
-        e = hipGetLastError();
+        if (h->bits == 8)
+            e = hp ? launch_pf<8, true>(w.pf_attr, p, scm, pf_rp, ct, grid, st)
+                   : launch_pf<8, false>(w.pf_attr, p, scm, pf_rp, ct, grid, st);
+        else
+            e = hp ? launch_pf<4, true>(w.pf_attr, p, scm, pf_rp, ct, grid, st)
+                   : launch_pf<4, false>(w.pf_attr, p, scm, pf_rp, ct, grid, st);
     } else {
         const dim3 grid(a.ntiles, (M + kRowsPerWG - 1) / kRowsPerWG);
         if (h->bits == 8) e = hp ? launch_rows_bits<8, true>(a, grid, dots, st)

@@ -408,10 +408,14 @@ constexpr int kLdsMax = 160 * 1024;
 
 // ------------------------------------------------------------------ prefill GEMM (M > 8)
 //
-// One workgroup of 8 waves computes 128 rows x 16*CT columns over all of K.
-// Wave w owns rows 32 (w & 3) .. +31 and column half w >> 2 (the first
-// (CT+1)/2 tiles or the other CT/2), so each SIMD holds one wave of each
-// half.  Per 32-block, H = sum(h*b) comes from one MFMA, (H << 8) + 128*S is
+// One workgroup of 8 waves computes 32 RP rows (RP = 1, 2 or 4 row pairs of
+// 16-row tiles) x 16*CT columns over all of K.  Wave w owns row pair w % RP
+// and column part w / RP of the 8 / RP parts (CT / parts tiles each, the
+// first CT % parts parts one more); waves w and w + 4 share a SIMD.  With
+// RP = 4 the parts are two halves: the C4 shape's 512 rows fill the CUs
+// with 128-row workgroups, while fewer rows use 32- or 64-row workgroups
+// and split the columns over more waves instead of leaving waves without
+// rows.  Per 32-block, H = sum(h*b) comes from one MFMA, (H << 8) + 128*S is
 // the accumulator input of the l-byte MFMA, which then holds the exact block
 // integer cs, and the lane folds acc = fma(s_a, f32(cs) * s_b, acc) in block
 // order.  Pairs of tiles run on v_mfma_i32_32x32x32_i8, an odd last tile on
@@ -421,8 +425,9 @@ constexpr int kLdsMax = 160 * 1024;
 // 16 bytes per lane to LDS address M0 + 16*lane) through a ring of
 // kPfStages stages.  A stage holds one chunk (two blocks): the CT weight
 // tiles (1 KB each; the decode layout is the MFMA B operand), their weight
-// sums and scales (the shared part, loaded by all waves together), and each
-// wave's activation record.  The compiler does not see these loads: every
+// sums and scales (the shared part, loaded by all waves together), and the
+// workgroup's 2 RP activation records (also split over all waves).  The
+// compiler does not see these loads: every
 // wave waits for its own with an explicit vmcnt, then the workgroup barrier
 // publishes the stage.
 //
@@ -435,7 +440,7 @@ constexpr int kLdsMax = 160 * 1024;
 // (column, block) for the two-pass product and the scales in the INT8
 // chunk layout.  A second barrier publishes the expanded stage.
 
-constexpr int kPfWaves = 8, kPfRows = 16 * kPfWaves;
+constexpr int kPfWaves = 8;
 // Ring of kPfStages stages of kPfChunks chunks each.
 constexpr int kPfStages = 2, kPfChunks = 2;
 // Activation record per (16-row tile, chunk): [block 2][lane 64][h 8 B, l 8 B]
@@ -456,16 +461,16 @@ struct PfArgs {
 
 // SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
 // One chunk's LDS region: [CT weight tiles, 1 KB each][weight sums, 128 B
-// per tile][block or group scales][8 activation records].  INT4 adds the raw
-// area after the two stages: group scales (SCM 1, 64 B per tile) or block
+// per tile][block or group scales][2 RP activation records].  INT4 adds the
+// raw area after the two stages: group scales (SCM 1, 64 B per tile) or block
 // scales then zero points (SCM 2, 256 + 64 B per tile), in whole KB.
-template <int CT, int SCM, int BITS>
+template <int CT, int SCM, int BITS, int RP>
 struct PfLayout {
     static constexpr int kWS = CT * 1024;
     static constexpr int kSB = kWS + CT * 128;
     static constexpr int kShared = kSB + (SCM == 2 ? CT * 128 : SCM == 1 ? CT * 64 : 0);
     static constexpr int kA = kShared;
-    static constexpr int kChunk = kA + kPfWaves * kRecBytes;
+    static constexpr int kChunk = kA + 2 * RP * kRecBytes;
     static constexpr int kStage = kPfChunks * kChunk;
     static constexpr int kRawZ = CT * 256;  // SCM 2: zero points after the block scales
     static constexpr int kRawUsed = BITS == 8 ? 0 : SCM == 2 ? CT * 320 : SCM == 1 ? CT * 64 : 0;
@@ -492,7 +497,14 @@ __device__ inline void dma16(const void* src, uint32_t lds) {
 __host__ __device__ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
 
 
-constexpr int kPfCts[] = {17, 16, 8, 4};
+// Instantiated (row pairs, column tiles) per workgroup.  Every column part
+// has at least one tile (CT >= 8 / RP).
+struct PfCfg {
+    int rp, ct;
+};
+constexpr PfCfg kPfCfgs[] = {{4, 17}, {4, 16}, {4, 13}, {4, 12}, {4, 9}, {4, 8}, {4, 5},
+                             {4, 4},  {2, 16}, {2, 8},  {2, 4},  {1, 16}, {1, 8}};
+constexpr int kPfNumCfgs = sizeof(kPfCfgs) / sizeof(kPfCfgs[0]);
 
 // Launchers, one explicit instantiation per (bits, activation mode) in the
 // kernel units dec_w*.hip and pf_w*.hip.  attr_set / pf_attr: this device's
@@ -501,6 +513,6 @@ template <int BITS, bool HP>
 hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, bool p64, bool fused,
                            bool extra, hipStream_t st);
 template <int BITS, bool HP>
-hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int ct, dim3 grid, hipStream_t st);
+hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int rp, int ct, dim3 grid, hipStream_t st);
 
 }  // namespace bq

@@ -313,16 +313,28 @@ def test_argmax_first_max_semantics(gpu, hb, hi_prec):
         hb.free(h)
 
 
-@pytest.mark.parametrize("scales", ["channel", "group", "block"])
-@pytest.mark.parametrize("ct", ["auto", "17", "16", "8", "4"])
-def test_prefill_gemm_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
-    """The M > 8 INT8 GEMM against the oracle: per-column, per-group (4 blocks)
-    and per-block scales; every column-tile width, with a partial last column
-    group (19 tiles); an odd block count (33, so the last chunk and the last
-    scale group are partial); row counts around the 128-row workgroup; and
-    activations with x20 outliers for the hi/lo split."""
-    if ct != "auto":
+# Prefill workgroup shapes (row pairs : column tiles), as instantiated.
+PF_CFGS = ["auto", "4:17", "4:16", "4:13", "4:12", "4:9", "4:8", "4:5", "4:4", "2:16", "2:8", "2:4", "1:16", "1:8"]
+PF_ROWS = (9, 33, 70, 130, 300)
+
+
+def _force_pf(monkeypatch, cfg):
+    if cfg != "auto":
+        rp, ct = cfg.split(":")
+        monkeypatch.setenv("BREEZE_HIP_PREFILL_RP", rp)
         monkeypatch.setenv("BREEZE_HIP_PREFILL_CT", ct)
+
+
+@pytest.mark.parametrize("scales", ["channel", "group", "block"])
+@pytest.mark.parametrize("cfg", PF_CFGS)
+def test_prefill_gemm_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, cfg):
+    """The M > 8 INT8 GEMM against the oracle: per-column, per-group (4 blocks)
+    and per-block scales; every workgroup shape (32, 64 or 128 rows, every
+    column-tile width), with a partial last column group (19 tiles); an odd
+    block count (33, so the last chunk and the last scale group are
+    partial); row counts around the 32-, 64- and 128-row workgroups; and
+    activations with x20 outliers for the hi/lo split."""
+    _force_pf(monkeypatch, cfg)
     N, K = 304, 1056
     rng = np.random.default_rng(11)
     qw, sc, _ = rng_weights(rng, N, K, 8)
@@ -334,7 +346,7 @@ def test_prefill_gemm_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
     try:
         for hp in (True, False):
             hb.set_hi_prec(hp)
-            for rows in (9, 130, 300):
+            for rows in PF_ROWS:
                 A = rng.normal(size=(rows, K)).astype(np.float32)
                 A[rng.random(A.shape) < 0.01] *= 20.0
                 want = orc.matmul(qw, sc, None, N, K, 8, A, hp)
@@ -346,16 +358,15 @@ def test_prefill_gemm_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
 
 
 @pytest.mark.parametrize("scales", ["channel", "group4", "group8", "block", "zeros"])
-@pytest.mark.parametrize("ct", ["auto", "17", "16", "8", "4"])
-def test_prefill_gemm_int4_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, ct):
+@pytest.mark.parametrize("cfg", PF_CFGS)
+def test_prefill_gemm_int4_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales, cfg):
     """The M > 8 GEMM on INT4 weights (nibbles expanded to signed bytes
     n - zp in LDS) against the oracle: per-column scales, groups of one and
     two 4-block chunks, per-block scales (default zero point 8) and explicit
-    zero points 0..15; every column-tile width with a partial last column
+    zero points 0..15; every workgroup shape with a partial last column
     group (19 tiles); 33 and 35 blocks, so the last 4-block chunk holds one
     or three blocks."""
-    if ct != "auto":
-        monkeypatch.setenv("BREEZE_HIP_PREFILL_CT", ct)
+    _force_pf(monkeypatch, cfg)
     N = 304
     rng = np.random.default_rng(12)
     for K in (1056, 1120):
@@ -373,7 +384,7 @@ def test_prefill_gemm_int4_bit_exact(gpu, hb, orc, hi_prec, monkeypatch, scales,
             assert info["scale_group"] == {"channel": 0, "group4": 4, "group8": 8, "block": 1, "zeros": 1}[scales], info
             for hp in (True, False):
                 hb.set_hi_prec(hp)
-                for rows in (9, 130, 300):
+                for rows in PF_ROWS:
                     A = rng.normal(size=(rows, K)).astype(np.float32)
                     A[rng.random(A.shape) < 0.01] *= 20.0
                     want = orc.matmul(qw, sc, qz, N, K, 4, A, hp)

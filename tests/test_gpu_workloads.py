@@ -64,10 +64,13 @@ def test_lm_head_logits_and_argmax(gpu, hb, orc, hi_prec):
     assert idx.tolist() == np.argmax(want, axis=1).tolist()
 
 
-@pytest.mark.parametrize("name", ["w8_prefill", "w4_prefill"])
-def test_prefill_rows_bit_exact(gpu, hb, orc, hi_prec, name):
+@pytest.mark.parametrize("name,rows", [("w8_prefill", None), ("w4_prefill", None), ("w8_prefill", 16),
+                                       ("w4_prefill", 100)])
+def test_prefill_rows_bit_exact(gpu, hb, orc, hi_prec, name, rows):
+    """All 512 rows, and the first 16 or 100 rows alone (32-row workgroups,
+    and 128-row workgroups at another column width)."""
     from oracle import oracle
-    d = oracle.make_config(name)
+    d = oracle.make_config(name, rows)
     N, K, bits = d["N"], d["K"], d["bits"]
     hb.set_hi_prec(True)
     h = hb.prepack(d["qweight"], d["scales"], None, K, N, bits=bits)
@@ -77,4 +80,4 @@ def test_prefill_rows_bit_exact(gpu, hb, orc, hi_prec, name):
         hb.free(h)
     want = orc.matmul(d["qweight"], d["scales"], None, N, K, bits, d["A"], True)
     bad = np.nonzero(np.any(got.view(np.uint32) != want.view(np.uint32), axis=1))[0]
-    assert bad.size == 0, (name, bad[:10].tolist())
+    assert bad.size == 0, (name, rows, bad[:10].tolist())
