@@ -6,9 +6,10 @@
 
 namespace bq {
 
-template <int BITS, bool HP, int SCM, int CT, int RP>
+template <int BITS, bool HP, int SCM, int CT, int RP, int S>
 __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
-    using L = PfLayout<CT, SCM, BITS, RP>;
+    using L = PfLayout<CT, SCM, BITS, RP, S>;
+    static_assert(S == 2 || S == 3, "ring depth");
     extern __shared__ __align__(16) char pf_lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -51,7 +52,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             } else {
                 const int y = (u - CT) * 1024 + 16 * lane;
                 to_raw[k] = true;
-                x0s[k] = (uint32_t)(L::kRawOff + (u - CT) * 1024);
+                x0s[k] = (uint32_t)((u - CT) * 1024);  // within the stage's raw area
                 src0[k] = a.S;  // padding lanes: any valid source
                 step[k] = 0;
                 if (SCM == 2 && y < L::kRawZ) {
@@ -109,8 +110,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     // Load d of this wave's kDmaChunk loads of chunk c into the chunk region
     // at LDS address cbase: the shared slots, then its record units.
     constexpr int kDmaChunk = L::kPerWave + kRecPerWave;
-    // INT4: only chunk 0 of a stage (first) carries the stage's shared loads.
-    auto dma_slot = [&](int c, uint32_t cbase, int d, bool first) {
+    // INT4: only chunk 0 of a stage (first) carries the stage's shared loads;
+    // raw is the LDS address of the stage's raw area.
+    auto dma_slot = [&](int c, uint32_t cbase, int d, bool first, uint32_t raw) {
         if (d < L::kPerWave) {
             if (BITS == 8) {
                 const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
@@ -118,35 +120,41 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             } else if (first) {
                 const int sg = c >> 1;
                 const size_t g = SCM == 1 ? (size_t)((4 * sg) >> a.sc_shift) : 0;
-                dma16(src0[d] + (size_t)sg * step[d] + g * gstep[d], (to_raw[d] ? lds0 : cbase) + x0s[d]);
+                dma16(src0[d] + (size_t)sg * step[d] + g * gstep[d], (to_raw[d] ? raw : cbase) + x0s[d]);
             }
         } else {
             const int e = d - L::kPerWave;
             dma16(rec0 + rec_src[e] + (size_t)c * kRecBytes, cbase + rec_dst[e]);
         }
     };
-    auto issue_chunk = [&](int c, uint32_t cbase, bool first) {
-#pragma unroll
-        for (int d = 0; d < kDmaChunk; ++d) dma_slot(c, cbase, d, first);
-    };
+    // Raw area of stage g (INT4).
+    auto raw_base = [&](int g) { return lds0 + (uint32_t)(L::kRawOff + (g % (S - 1)) * L::kRaw); };
+    // With more than two stages every stage issues the same loads per wave
+    // (chunks past the end repeat the last chunk's, into a slot nobody
+    // reads), so the wait at a stage's start counts the loads issued after
+    // it exactly.  Two stages wait for all loads and skip those chunks (the
+    // loads kept the allocator from fitting the widest shapes' registers).
+    constexpr int kStageLoads = BITS == 8 ? kPfChunks * kDmaChunk : kDmaChunk + (kPfChunks - 1) * kRecPerWave;
     auto issue_stage = [&](int g, int buf) {
         const uint32_t sbase = lds0 + (uint32_t)(buf * L::kStage);
 #pragma unroll
         for (int cc = 0; cc < kPfChunks; ++cc) {
-            const int c = g * kPfChunks + cc;
-            if (c < nch) issue_chunk(c, sbase + (uint32_t)(cc * L::kChunk), cc == 0);
+            const int c = min(g * kPfChunks + cc, nch - 1);
+            if (S == 2 && g * kPfChunks + cc >= nch) continue;
+#pragma unroll
+            for (int d = 0; d < kDmaChunk; ++d) dma_slot(c, sbase + (uint32_t)(cc * L::kChunk), d, cc == 0, raw_base(g));
         }
     };
 
-    // INT4: expands stage buffer buf in place (all threads; a workgroup
+    // INT4: expands stage g (buffer buf) in place from its raw area (all threads; a workgroup
     // barrier must follow).  Wave w takes tiles w, w + 8, ...; lane l holds
     // weight lane l of the tile (column l & 15, k-octet l >> 4), so the LDS
     // reads and writes are linear.  The nibble sums of a column's four
     // octets (one per 16-lane row) meet by row swaps.
-    auto expand = [&](int buf) {
+    auto expand = [&](int g, int buf) {
         if constexpr (BITS == 4) {
             char* sb = pf_lds + buf * L::kStage;
-            const char* raw = pf_lds + L::kRawOff;
+            const char* raw = pf_lds + L::kRawOff + (g % (S - 1)) * L::kRaw;
             const int c = lane & 15, o = lane >> 4, cc = o & 1;
             for (int t = wave; t < CT; t += kPfWaves) {
                 const int wl = t * 1024 + 16 * lane;
@@ -243,9 +251,10 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) acco[r][i] = 0.0f;
 
-        // dma_tag: 0 no loads, 1 or 2 the loads of chunk 0 or 1 of the next
-        // stage (c_next, at LDS nbase).
-        auto compute = [&](const char* cp, auto nb_tag, auto dma_tag, int c_next, uint32_t nbase) {
+        // dma_tag: 0 no loads, 1 or 2 the loads of chunk 0 or 1 of the stage
+        // S - 1 ahead (chunk c_next, at LDS nbase; nraw: that buffer's raw
+        // area).
+        auto compute = [&](const char* cp, auto nb_tag, auto dma_tag, int c_next, uint32_t nbase, uint32_t nraw) {
             constexpr int NB = decltype(nb_tag)::value;
             constexpr bool DMA = decltype(dma_tag)::value != 0;
             constexpr bool FIRST = decltype(dma_tag)::value == 1;
@@ -407,7 +416,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             for (int s = 0; s < NS; ++s) {
                 if (s < NGB && s % NB == 0) load_group(s / NB + kAhead);
                 if (s == NGB - 1) load_odd();
-                if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s, FIRST);
+                if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s, FIRST, nraw);
                 step_h(s + 1);
                 step_e(s);
                 step_d(s + 1);
@@ -415,7 +424,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             }
             if (DMA) {
 #pragma unroll
-                for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d, FIRST);
+                for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d, FIRST, nraw);
             }
         };
 
@@ -425,42 +434,61 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
         constexpr std::integral_constant<int, 1> dma0{};
         constexpr std::integral_constant<int, 2> dma1{};
         constexpr std::integral_constant<int, 0> no_dma{};
+        // Ring of S stage buffers: stage g lives in buffer g % S.  The first
+        // S - 1 stages are issued up front; computing stage g issues stage
+        // g + S - 1 (chunks clamped to the last one).  At the start of stage
+        // g the loads of the stages after it that are already issued may
+        // stay in flight.
         issue_stage(0, 0);
+        if (S > 2) issue_stage(1, 1);
         for (int g = 0; g + 1 < nst; ++g) {
-            __builtin_amdgcn_s_waitcnt(vm_wait(0));
+            const int ahead = min(g + S - 2, nst - 1) - g;  // stages issued after g (uniform)
+            if (S > 2 && ahead > 0) __builtin_amdgcn_s_waitcnt(vm_wait(kStageLoads));
+            else __builtin_amdgcn_s_waitcnt(vm_wait(0));
             lds_barrier();
+            const int buf = g % S;
             if (BITS == 4) {
-                expand(g & 1);
+                expand(g, buf);
                 lds_barrier();
             }
-            const uint32_t nbase = lds0 + (uint32_t)(((g + 1) & 1) * L::kStage);
-            const int cn = (g + 1) * kPfChunks;
-            if (active) {
-                const char* sp = pf_lds + (g & 1) * L::kStage;
-                compute(sp, two, dma0, cn, nbase);
-                compute(sp + L::kChunk, two, dma1, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk);
-            } else {
-                issue_stage(g + 1, (g + 1) & 1);
+            const int gn = g + S - 1, bn = gn % S;  // stage issued now, and its buffer
+            const uint32_t nbase = lds0 + (uint32_t)(bn * L::kStage);
+            const int cn = min(gn * kPfChunks, nch - 1);
+            // With two stages gn = g + 1 < nst always: a straight-line body
+            // (a branch here makes the allocator copy the accumulators).
+            if (S == 2 || gn < nst) {
+                if (active) {
+                    const char* sp = pf_lds + buf * L::kStage;
+                    compute(sp, two, dma0, cn, nbase, raw_base(gn));
+                    compute(sp + L::kChunk, two, dma1, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk,
+                            raw_base(gn));
+                } else {
+                    issue_stage(gn, bn);
+                }
+            } else if (S > 2 && active) {
+                const char* sp = pf_lds + buf * L::kStage;
+                compute(sp, two, no_dma, 0, 0u, 0u);
+                compute(sp + L::kChunk, two, no_dma, 0, 0u, 0u);
             }
         }
         __builtin_amdgcn_s_waitcnt(vm_wait(0));
         lds_barrier();
         if (BITS == 4) {
-            expand((nst - 1) & 1);
+            expand(nst - 1, (nst - 1) % S);
             lds_barrier();
         }
         if (!active) return;
         {
-            const char* sp = pf_lds + ((nst - 1) & 1) * L::kStage;
+            const char* sp = pf_lds + ((nst - 1) % S) * L::kStage;
             const int c0 = (nst - 1) * kPfChunks;
             if (c0 + 1 < nch) {
-                compute(sp, two, no_dma, 0, 0u);
-                if (odd) compute(sp + L::kChunk, one, no_dma, 0, 0u);
-                else compute(sp + L::kChunk, two, no_dma, 0, 0u);
+                compute(sp, two, no_dma, 0, 0u, 0u);
+                if (odd) compute(sp + L::kChunk, one, no_dma, 0, 0u, 0u);
+                else compute(sp + L::kChunk, two, no_dma, 0, 0u, 0u);
             } else if (odd) {
-                compute(sp, one, no_dma, 0, 0u);
+                compute(sp, one, no_dma, 0, 0u, 0u);
             } else {
-                compute(sp, two, no_dma, 0, 0u);
+                compute(sp, two, no_dma, 0, 0u, 0u);
             }
         }
 #pragma unroll
@@ -499,10 +527,10 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
 }
 
 
-template <int BITS, bool HP, int SCM, int CT, int RP>
+template <int BITS, bool HP, int SCM, int CT, int RP, int S>
 hipError_t launch_pf_t(bool* pf_attr, const PfArgs& p, dim3 grid, hipStream_t st) {
-    using L = PfLayout<CT, SCM, BITS, RP>;
-    auto kern = prefill_kernel<BITS, HP, SCM, CT, RP>;
+    using L = PfLayout<CT, SCM, BITS, RP, S>;
+    auto kern = prefill_kernel<BITS, HP, SCM, CT, RP, S>;
     int slot = 0;
     while (kPfCfgs[slot].rp != RP || kPfCfgs[slot].ct != CT) ++slot;
     const int key = (HP ? 1 : 0) | SCM << 1 | slot << 3 | (BITS == 4 ? 128 : 0);
@@ -516,23 +544,23 @@ hipError_t launch_pf_t(bool* pf_attr, const PfArgs& p, dim3 grid, hipStream_t st
     return hipGetLastError();
 }
 
-// One case per entry of kPfCfgs.
+// One case per entry of kPfCfgs (row pairs, column tiles, ring stages).
 template <int BITS, bool HP, int SCM>
 hipError_t launch_pf_scm(bool* pf_attr, const PfArgs& p, int rp, int ct, dim3 grid, hipStream_t st) {
     switch (rp * 100 + ct) {
-        case 417: return launch_pf_t<BITS, HP, SCM, 17, 4>(pf_attr, p, grid, st);
-        case 416: return launch_pf_t<BITS, HP, SCM, 16, 4>(pf_attr, p, grid, st);
-        case 413: return launch_pf_t<BITS, HP, SCM, 13, 4>(pf_attr, p, grid, st);
-        case 412: return launch_pf_t<BITS, HP, SCM, 12, 4>(pf_attr, p, grid, st);
-        case 409: return launch_pf_t<BITS, HP, SCM, 9, 4>(pf_attr, p, grid, st);
-        case 408: return launch_pf_t<BITS, HP, SCM, 8, 4>(pf_attr, p, grid, st);
-        case 405: return launch_pf_t<BITS, HP, SCM, 5, 4>(pf_attr, p, grid, st);
-        case 404: return launch_pf_t<BITS, HP, SCM, 4, 4>(pf_attr, p, grid, st);
-        case 216: return launch_pf_t<BITS, HP, SCM, 16, 2>(pf_attr, p, grid, st);
-        case 208: return launch_pf_t<BITS, HP, SCM, 8, 2>(pf_attr, p, grid, st);
-        case 204: return launch_pf_t<BITS, HP, SCM, 4, 2>(pf_attr, p, grid, st);
-        case 116: return launch_pf_t<BITS, HP, SCM, 16, 1>(pf_attr, p, grid, st);
-        case 108: return launch_pf_t<BITS, HP, SCM, 8, 1>(pf_attr, p, grid, st);
+        case 417: return launch_pf_t<BITS, HP, SCM, 17, 4, 2>(pf_attr, p, grid, st);
+        case 416: return launch_pf_t<BITS, HP, SCM, 16, 4, 2>(pf_attr, p, grid, st);
+        case 413: return launch_pf_t<BITS, HP, SCM, 13, 4, 2>(pf_attr, p, grid, st);
+        case 412: return launch_pf_t<BITS, HP, SCM, 12, 4, 2>(pf_attr, p, grid, st);
+        case 409: return launch_pf_t<BITS, HP, SCM, 9, 4, 2>(pf_attr, p, grid, st);
+        case 408: return launch_pf_t<BITS, HP, SCM, 8, 4, 2>(pf_attr, p, grid, st);
+        case 405: return launch_pf_t<BITS, HP, SCM, 5, 4, 2>(pf_attr, p, grid, st);
+        case 404: return launch_pf_t<BITS, HP, SCM, 4, 4, 2>(pf_attr, p, grid, st);
+        case 216: return launch_pf_t<BITS, HP, SCM, 16, 2, 2>(pf_attr, p, grid, st);
+        case 208: return launch_pf_t<BITS, HP, SCM, 8, 2, 3>(pf_attr, p, grid, st);
+        case 204: return launch_pf_t<BITS, HP, SCM, 4, 2, 3>(pf_attr, p, grid, st);
+        case 116: return launch_pf_t<BITS, HP, SCM, 16, 1, 2>(pf_attr, p, grid, st);
+        case 108: return launch_pf_t<BITS, HP, SCM, 8, 1, 3>(pf_attr, p, grid, st);
         default: return hipErrorInvalidValue;
     }
 }

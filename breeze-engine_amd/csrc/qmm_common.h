@@ -422,8 +422,10 @@ constexpr int kLdsMax = 160 * 1024;
 // v_mfma_i32_16x16x32_i8.
 //
 // Operands reach LDS by direct global->LDS loads (global_load_lds_dwordx4,
-// 16 bytes per lane to LDS address M0 + 16*lane) through a ring of
-// kPfStages stages.  A stage holds one chunk (two blocks): the CT weight
+// 16 bytes per lane to LDS address M0 + 16*lane) through a ring of S stages
+// of two chunks (S = 2, or 3 for the 32- and 64-row shapes, whose short
+// stages would not cover a load's latency).  A chunk (two blocks) holds the
+// CT weight
 // tiles (1 KB each; the decode layout is the MFMA B operand), their weight
 // sums and scales (the shared part, loaded by all waves together), and the
 // workgroup's 2 RP activation records (also split over all waves).  The
@@ -441,8 +443,8 @@ constexpr int kLdsMax = 160 * 1024;
 // chunk layout.  A second barrier publishes the expanded stage.
 
 constexpr int kPfWaves = 8;
-// Ring of kPfStages stages of kPfChunks chunks each.
-constexpr int kPfStages = 2, kPfChunks = 2;
+// Chunks per ring stage.
+constexpr int kPfChunks = 2;
 // Activation record per (16-row tile, chunk): [block 2][lane 64][h 8 B, l 8 B]
 // in MFMA A-operand order (lane: row lane&15, k-octet lane>>4), then the
 // block scales [block 2][row 16] float.
@@ -461,10 +463,12 @@ struct PfArgs {
 
 // SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
 // One chunk's LDS region: [CT weight tiles, 1 KB each][weight sums, 128 B
-// per tile][block or group scales][2 RP activation records].  INT4 adds the
-// raw area after the two stages: group scales (SCM 1, 64 B per tile) or block
-// scales then zero points (SCM 2, 256 + 64 B per tile), in whole KB.
-template <int CT, int SCM, int BITS, int RP>
+// per tile][block or group scales][2 RP activation records].  INT4 adds S - 1
+// raw areas after the S stages (stage g uses area g % (S - 1): only the next
+// stage waits for its expansion while the one after it loads): group scales
+// (SCM 1, 64 B per tile) or block scales then zero points (SCM 2, 256 + 64 B
+// per tile), in whole KB.
+template <int CT, int SCM, int BITS, int RP, int S>
 struct PfLayout {
     static constexpr int kWS = CT * 1024;
     static constexpr int kSB = kWS + CT * 128;
@@ -475,12 +479,12 @@ struct PfLayout {
     static constexpr int kRawZ = CT * 256;  // SCM 2: zero points after the block scales
     static constexpr int kRawUsed = BITS == 8 ? 0 : SCM == 2 ? CT * 320 : SCM == 1 ? CT * 64 : 0;
     static constexpr int kRaw = (kRawUsed + 1023) / 1024 * 1024;
-    static constexpr int kRawOff = kPfStages * kStage;
+    static constexpr int kRawOff = S * kStage;  // raw area r at kRawOff + r * kRaw
     // DMA units of 1 KB per stage (INT8: per chunk): INT8 the chunk's shared
     // part, INT4 the CT raw tiles and the raw area.
     static constexpr int kUnits = BITS == 8 ? (kShared + 1023) / 1024 : CT + kRaw / 1024;
     static constexpr int kPerWave = (kUnits + kPfWaves - 1) / kPfWaves;
-    static constexpr int kBytes = kRawOff + kRaw;
+    static constexpr int kBytes = kRawOff + (S - 1) * kRaw;
     static_assert(kShared % 64 == 0 && kBytes <= 160 * 1024, "layout");
 };
 
@@ -500,10 +504,10 @@ __host__ __device__ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) <
 // Instantiated (row pairs, column tiles) per workgroup.  Every column part
 // has at least one tile (CT >= 8 / RP).
 struct PfCfg {
-    int rp, ct;
+    int rp, ct, st;  // row pairs, column tiles, ring stages
 };
-constexpr PfCfg kPfCfgs[] = {{4, 17}, {4, 16}, {4, 13}, {4, 12}, {4, 9}, {4, 8}, {4, 5},
-                             {4, 4},  {2, 16}, {2, 8},  {2, 4},  {1, 16}, {1, 8}};
+constexpr PfCfg kPfCfgs[] = {{4, 17, 2}, {4, 16, 2}, {4, 13, 2}, {4, 12, 2}, {4, 9, 2}, {4, 8, 2}, {4, 5, 2},
+                             {4, 4, 2},  {2, 16, 2}, {2, 8, 3},  {2, 4, 3},  {1, 16, 2}, {1, 8, 3}};
 constexpr int kPfNumCfgs = sizeof(kPfCfgs) / sizeof(kPfCfgs[0]);
 
 // Launchers, one explicit instantiation per (bits, activation mode) in the
