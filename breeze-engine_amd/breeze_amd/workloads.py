@@ -24,9 +24,9 @@ LABELS = {
     "w8_gemv": "W8 GEMV M=1 K=4096 N=4096, per-channel scales",
     "w4_gemv": "W4 GEMV M=1 K=4096 N=12288, group-128 scales",
     "w4_decode": "W4 decode M={M} K=12288 N=4096, group-128 scales, 1% x20 outliers",
-    "w8_prefill": "W8 prefill M=512 K=5120 N=17408, per-channel scales",
+    "w8_prefill": "W8 prefill M={M} K=5120 N=17408, per-channel scales",
     "w8_lmhead": "W8 LM head M=1 K=5120 N=151936 + argmax, per-channel scales",
-    "w4_prefill": "W4 prefill M=512 K=5120 N=17408, group-128 scales",
+    "w4_prefill": "W4 prefill M={M} K=5120 N=17408, group-128 scales",
 }
 
 

@@ -19,6 +19,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     constexpr int kParts = kPfWaves / RP;
     static_assert(kPfWaves % RP == 0 && CT >= kParts, "every part holds a tile");
     const int rp = wave % RP, part = wave / RP;
+    // Part q: tiles [q CTB + min(q, CTR), ...), CTB + 1 of them for q < CTR.
+    constexpr int CTB = CT / kParts, CTR = CT % kParts;
+    const int part_t0 = part * CTB + min(part, CTR), part_nt = CTB + (part < CTR ? 1 : 0);
     const int t0 = blockIdx.x * CT;
     const int rt0 = blockIdx.y * (2 * RP) + 2 * rp;
     const bool active = rt0 * 16 < a.M;
@@ -128,7 +131,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
         }
     };
     // Raw area of stage g (INT4).
-    auto raw_base = [&](int g) { return lds0 + (uint32_t)(L::kRawOff + (g % (S - 1)) * L::kRaw); };
+    auto raw_base = [&](int g) { return lds0 + (uint32_t)(L::kRawOff + (g % L::kNRaw) * L::kRaw); };
     // With more than two stages every stage issues the same loads per wave
     // (chunks past the end repeat the last chunk's, into a slot nobody
     // reads), so the wait at a stage's start counts the loads issued after
@@ -146,17 +149,23 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
         }
     };
 
-    // INT4: expands stage g (buffer buf) in place from its raw area (all threads; a workgroup
-    // barrier must follow).  Wave w takes tiles w, w + 8, ...; lane l holds
+    // INT4: expands stage g (buffer buf) in place from its raw area (with more
+    // than one row pair all threads share the tiles and a workgroup barrier
+    // must follow).  Wave w takes tiles w, w + 8, ... (with one row pair, the
+    // tiles of its column part); lane l holds
     // weight lane l of the tile (column l & 15, k-octet l >> 4), so the LDS
     // reads and writes are linear.  The nibble sums of a column's four
     // octets (one per 16-lane row) meet by row swaps.
     auto expand = [&](int g, int buf) {
         if constexpr (BITS == 4) {
             char* sb = pf_lds + buf * L::kStage;
-            const char* raw = pf_lds + L::kRawOff + (g % (S - 1)) * L::kRaw;
+            const char* raw = pf_lds + L::kRawOff + (g % L::kNRaw) * L::kRaw;
             const int c = lane & 15, o = lane >> 4, cc = o & 1;
-            for (int t = wave; t < CT; t += kPfWaves) {
+            // One row pair: each wave expands the tiles of its own column
+            // part, which no other wave reads, so no barrier has to follow.
+            const int t_beg = RP == 1 ? part_t0 : wave, t_end = RP == 1 ? part_t0 + part_nt : CT;
+            const int t_step = RP == 1 ? 1 : kPfWaves;
+            for (int t = t_beg; t < t_end; t += t_step) {
                 const int wl = t * 1024 + 16 * lane;
                 const uint4 w = *reinterpret_cast<const uint4*>(sb + wl);
                 const uint32_t z = SCM == 2 ? *reinterpret_cast<const uint32_t*>(raw + L::kRawZ + t * 64 + 4 * c)
@@ -449,7 +458,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             const int buf = g % S;
             if (BITS == 4) {
                 expand(g, buf);
-                lds_barrier();
+                if (RP > 1) lds_barrier();
+                else asm volatile("" ::: "memory");
             }
             const int gn = g + S - 1, bn = gn % S;  // stage issued now, and its buffer
             const uint32_t nbase = lds0 + (uint32_t)(bn * L::kStage);
@@ -475,7 +485,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
         lds_barrier();
         if (BITS == 4) {
             expand(nst - 1, (nst - 1) % S);
-            lds_barrier();
+            if (RP > 1) lds_barrier();
+            else asm volatile("" ::: "memory");
         }
         if (!active) return;
         {
@@ -514,16 +525,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             }
         }
     };
-    // Part q: tiles [q CTB + min(q, CTR), ...), CTB + 1 of them for q < CTR.
-    constexpr int CTB = CT / kParts, CTR = CT % kParts;
-    const int toff = part * CTB + min(part, CTR);
     if constexpr (CTR > 0) {
         if (part < CTR) {
-            run32(std::integral_constant<int, CTB + 1>{}, toff);
+            run32(std::integral_constant<int, CTB + 1>{}, part_t0);
             return;
         }
     }
-    run32(std::integral_constant<int, CTB>{}, toff);
+    run32(std::integral_constant<int, CTB>{}, part_t0);
 }
 
 

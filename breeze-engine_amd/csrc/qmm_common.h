@@ -463,9 +463,12 @@ struct PfArgs {
 
 // SCM: scale layout: 0 one per column, 1 per group of >= 2 blocks, 2 per block.
 // One chunk's LDS region: [CT weight tiles, 1 KB each][weight sums, 128 B
-// per tile][block or group scales][2 RP activation records].  INT4 adds S - 1
-// raw areas after the S stages (stage g uses area g % (S - 1): only the next
-// stage waits for its expansion while the one after it loads): group scales
+// per tile][block or group scales][2 RP activation records].  INT4 adds kNRaw
+// raw areas after the S stages, stage g using area g % kNRaw: S - 1 when a
+// barrier follows the expansion (only the next stage waits for its expansion
+// while the one after it loads), S with one row pair, whose waves expand
+// their own tiles with no barrier after it (a wave may load stage g + S - 1
+// while another still expands stage g).  A raw area holds group scales
 // (SCM 1, 64 B per tile) or block scales then zero points (SCM 2, 256 + 64 B
 // per tile), in whole KB.
 template <int CT, int SCM, int BITS, int RP, int S>
@@ -480,11 +483,12 @@ struct PfLayout {
     static constexpr int kRawUsed = BITS == 8 ? 0 : SCM == 2 ? CT * 320 : SCM == 1 ? CT * 64 : 0;
     static constexpr int kRaw = (kRawUsed + 1023) / 1024 * 1024;
     static constexpr int kRawOff = S * kStage;  // raw area r at kRawOff + r * kRaw
+    static constexpr int kNRaw = RP == 1 ? S : S - 1;
     // DMA units of 1 KB per stage (INT8: per chunk): INT8 the chunk's shared
     // part, INT4 the CT raw tiles and the raw area.
     static constexpr int kUnits = BITS == 8 ? (kShared + 1023) / 1024 : CT + kRaw / 1024;
     static constexpr int kPerWave = (kUnits + kPfWaves - 1) / kPfWaves;
-    static constexpr int kBytes = kRawOff + (S - 1) * kRaw;
+    static constexpr int kBytes = kRawOff + kNRaw * kRaw;
     static_assert(kShared % 64 == 0 && kBytes <= 160 * 1024, "layout");
 };
 
