@@ -12,7 +12,8 @@ namespace bq {
 // rest of the arguments come from the struct as the code reaches them.
 // Tiles per workgroup group: the first rem_t groups own base_t + 1 tiles, the
 // rest base_t (ntiles = base_t * NG + rem_t).  misc = sc_shift | RG << 8 |
-// pair_xcd << 10 | phases per tile << 16.  PAIR: gate and up projections
+// xcd << 11 | phases per tile << 16 (RG row groups of 4, up to 4; xcd: the
+// RG workgroups of one tile range share an XCD).  PAIR: gate and up projections
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
 
@@ -33,8 +34,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     a.ngrp = pngrp;
     a.nblk4 = (pnblk + 3) / 4 * 4;
     a.sc_shift = misc & 31;
-    a.RG = (misc >> 8) & 3;
-    a.pair_xcd = (misc >> 10) & 1;
+    a.RG = (misc >> 8) & 7;
+    a.pair_xcd = (misc >> 11) & 1;
     constexpr bool PAIR = FUSE == kFusePair, NORM = FUSE == kFuseNormMulti;
     constexpr bool MULTI = FUSE == kFuseMulti || NORM;
     constexpr int JG = BITS == 8 ? 2 : 4;
@@ -50,12 +51,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         g = blockIdx.x;
         rg = 0;
     } else if (a.pair_xcd) {
-        const int b = blockIdx.x;
-        g = (b >> 4) * 8 + (b & 7);
-        rg = (b >> 3) & 1;
+        // Workgroups are dealt to the 8 XCDs in turn: the RG row groups of
+        // tile range g are blocks 8 (RG (g / 8) + rg) + g % 8, one XCD.
+        const int b = blockIdx.x, q = b >> 3;
+        g = (q / a.RG) * 8 + (b & 7);
+        rg = q % a.RG;
     } else {
-        g = blockIdx.x >> 1;
-        rg = blockIdx.x & 1;
+        g = blockIdx.x / a.RG;
+        rg = blockIdx.x % a.RG;
     }
     const int m0 = rg * 4;
     const int Mr = min(4, a.M - m0);
@@ -647,7 +650,7 @@ hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hi
     }
     const void* act = FUSED ? static_cast<const void*>(a.A) : static_cast<const void*>(a.Aq);
     const int npw = (a.nbg + kProducers - 1) / kProducers;
-    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 10 | npw << 16;
+    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 11 | npw << 16;
     const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
     kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, base_t, a.nblk, a.M, a.nbg, rem_t, a.NG, a.ngrp, misc, a);
     return hipGetLastError();

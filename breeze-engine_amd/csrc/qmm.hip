@@ -1010,6 +1010,21 @@ constexpr int kFusedMaxBlocks = kQuantPasses * 128;  // row-blocks the prologue 
 // LDS bytes of the decode kernel, or 0 if the activation records of a row
 // group do not fit (in LDS, or in the prologue's 6-uint4-per-thread record
 // copy).
+// Most rows the decode kernel takes (row groups of 4, the workgroups of one
+// tile range on one XCD) before the prefill GEMM does.  Measured (us, 12 /
+// 16 rows, GEMM -> decode): W4 K=12288 N=4096 119 -> 21 / 120 -> 22, W8
+// K=5120 N=5120 40 -> 17 / 40 -> 18, W4 K=5120 N=17408 55 -> 28 / 55 -> 34;
+// only W8 at 1088 tiles lost at 16 rows (42 -> 46), so wide W8 stops at 12.
+// BREEZE_HIP_DEC_ROWS sets the limit (1..kDecMaxRows) for tests and tuning.
+constexpr int kDecMaxRows = 16;
+int dec_max_rows(int bits, int ntiles, const char* force) {
+    if (force) {
+        const int v = std::atoi(force);
+        if (v >= 1 && v <= kDecMaxRows) return v;
+    }
+    return bits == 8 && ntiles >= 1024 ? 12 : kDecMaxRows;
+}
+
 int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG, bool p64 = false) {
     if (Mr_max * a.nblk > kFusedMaxBlocks && Mr_max * a.nblk * 4 > 6 * kDecWaves * 64) return 0;
     const int total = dec_lds(Mr_max, a.nblk, JG, p64).total;
@@ -1100,9 +1115,10 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     a.C = dC;
     a.Cs = dCs;
 
-    // Decode kernel for M <= 8 (one or two row groups of 4); the rows kernel
-    // serves larger M, the block-integer export and shapes whose activation
-    // records do not fit in LDS.  The decode kernel quantizes small
+    // Decode kernel for M <= dec_rows (row groups of 4: up to 8 rows, up to
+    // 16 where that is set below); the prefill GEMM and the rows kernel serve
+    // larger M, the rows kernel the block-integer export and shapes whose
+    // activation records do not fit in LDS.  The decode kernel quantizes small
     // activations itself; larger ones go through the stand-alone quantizer
     // once instead of once per workgroup.
     const int Mr_max = std::min(M, 4);
@@ -1110,7 +1126,8 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // layout fits in LDS.
     const int lds_p64 = (M <= 2 && !dots) ? plan_dec_lds(a, Mr_max, JG, true) : 0;
     const bool p64 = lds_p64 > 0;
-    const int lds = p64 ? lds_p64 : (M <= 8 && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
+    const int dec_rows = (h2 || mp) ? 8 : dec_max_rows(h->bits, a.ntiles, std::getenv("BREEZE_HIP_DEC_ROWS"));
+    const int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     const bool dec = lds > 0;
     if ((h2 || mp) && !dec) return kNotPairable;
     if (mp && (h->extra || dIdx)) return kNotPairable;
@@ -1176,7 +1193,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
             a.NG = std::min(a.ntiles, n_cu);
             a.pair_xcd = 0;
         } else {
-            const int ng = std::min(a.ntiles, std::max(1, n_cu / 2));
+            const int ng = std::min(a.ntiles, std::max(1, n_cu / a.RG));
             a.pair_xcd = ng % 8 == 0 ? 1 : 0;
             a.NG = ng;
         }
@@ -1200,10 +1217,11 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
                     return -4;
                 }
                 unsigned int* t = nullptr;
-                if (!hip_ok(hipMalloc(&t, 9 * sizeof(unsigned long long)), "argmax workspace")) return -4;
+                if (!hip_ok(hipMalloc(&t, (1 + kDecMaxRows) * sizeof(unsigned long long)), "argmax workspace"))
+                    return -4;
                 // Cleared on st itself: a non-blocking stream does not wait
                 // for work on the null stream.
-                fill_u32_kernel<<<1, 64, 0, st>>>(t, 18, 0u);
+                fill_u32_kernel<<<1, 64, 0, st>>>(t, 2 * (1 + kDecMaxRows), 0u);
                 if (!hip_ok(hipGetLastError(), "argmax workspace clear")) {
                     w.retired.push_back(t);
                     return -4;
@@ -1644,7 +1662,7 @@ int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64
     if (dIdx && M > 0) {
         // The decode argmax merges into this state and needs it zero; a
         // kernel clears it (a graph may capture this call).
-        fill_u32_kernel<<<1, 64, 0, st>>>(s.ticket, 18, 0u);
+        fill_u32_kernel<<<1, 64, 0, st>>>(s.ticket, 2 * (1 + kDecMaxRows), 0u);
         if (!hip_ok(hipGetLastError(), "argmax state clear")) return -5;
     }
     return run(w, s, h, dA, M, dC, nullptr, dIdx, st);

@@ -168,9 +168,9 @@ def test_legacy_corr_is_honoured(gpu, hb, orc, hi_prec, bits):
     try:
         for hp in (False, True):
             hb.set_hi_prec(hp)
-            # 5 rows: the decode kernel; 9 and 17: the rows kernel's corr
-            # delta in row chunks of 8 (quantized_matmul.cpp:542-550).
-            for rows in (5, 9, 17):
+            # 5 and 9 rows: the decode kernel; 17 and 33: the rows kernel's
+            # corr delta in row chunks of 8 (quantized_matmul.cpp:542-550).
+            for rows in (5, 9, 17, 33):
                 A = rng.normal(size=(rows, K)).astype(np.float32)
                 want = orc.matmul_legacy(B, scale, zp, corr, N, K, bits, A, hp)
                 assert bits_equal(hb.matmul(h, A, N), want), (hp, rows)
@@ -182,8 +182,8 @@ def test_legacy_corr_is_honoured(gpu, hb, orc, hi_prec, bits):
 def test_legacy_int4_signed_zero_points(gpu, hb, orc, hi_prec, zp_lo, zp_hi):
     """Legacy INT4 handles keep signed int8 zero points from -112 up
     (b = nibble - zp never wraps there) with a consistent corr, so they stay
-    INT4 with explicit zero points: the decode kernel (1, 3, 8 rows) and the
-    prefill GEMM's in-LDS nibble expansion (9, 17, 130 rows), whose per-byte
+    INT4 with explicit zero points: the decode kernel (1, 3, 8, 9 rows) and
+    the prefill GEMM's in-LDS nibble expansion (17, 130 rows), whose per-byte
     n - zp must not borrow across bytes for negative zp.  33 blocks: a
     partial last 4-block chunk."""
     N, K = 64, 1056
@@ -319,6 +319,8 @@ PF_ROWS = (9, 33, 70, 130, 300)
 
 
 def _force_pf(monkeypatch, cfg):
+    # Rows 9-16 would take the decode kernel: keep them on the GEMM here.
+    monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "8")
     if cfg != "auto":
         rp, ct = cfg.split(":")
         monkeypatch.setenv("BREEZE_HIP_PREFILL_RP", rp)
@@ -512,3 +514,30 @@ def test_decode_staged_rows_with_argmax(gpu, hb, orc, hi_prec, bits):
                 assert idx.cpu().tolist() == np.argmax(want, axis=1).tolist(), (hp, rows)
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
+def test_decode_three_and_four_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros):
+    """9 to 16 rows through the decode kernel (three or four workgroups of 4
+    rows per tile range, on one XCD when the range count allows; the limit
+    forced to 16), outputs and argmax against the oracle: K = 4608 (staged
+    records, 40 tiles: row groups placed on one XCD) and K = 96 (the prologue
+    quantizes; 20 tiles: the plain block order)."""
+    monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "16")
+    rng = np.random.default_rng(31)
+    for K, N in ((4608, 640), (96, 320)):
+        qw, sc, qz = rng_weights(rng, N, K, bits, explicit_zeros=explicit_zeros)
+        h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+        try:
+            for hp in (True, False):
+                hb.set_hi_prec(hp)
+                for rows in (9, 12, 13, 16):
+                    A = rng.normal(size=(rows, K)).astype(np.float32)
+                    A[rng.random(A.shape) < 0.01] *= 20.0
+                    want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
+                    got, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+                    gpu.cuda.synchronize()
+                    assert bits_equal(got.cpu().numpy(), want), (K, hp, rows)
+                    assert idx.cpu().numpy().tolist() == np.argmax(want, axis=1).tolist(), (K, hp, rows)
+        finally:
+            hb.free(h)

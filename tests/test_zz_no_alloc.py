@@ -39,7 +39,7 @@ def _reference_call(hb, torch, h, A, N, argmax):
     return c.cpu().numpy(), None
 
 
-@pytest.mark.parametrize("case", ["fused", "staged", "argmax", "prefill", "prefill_argmax"])
+@pytest.mark.parametrize("case", ["fused", "staged", "argmax", "row_groups_argmax", "prefill", "prefill_argmax"])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_noalloc_matches_allocating_entry(gpu, hb, hi_prec, case, bits):
     torch = gpu
@@ -47,8 +47,9 @@ def test_noalloc_matches_allocating_entry(gpu, hb, hi_prec, case, bits):
         "fused": (512, 256, (3, 1), False),
         "staged": (4608, 256, (8, 4), False),
         "argmax": (1024, 16 * 600, (2, 1), True),
+        "row_groups_argmax": (1024, 16 * 320, (16, 12), True),
         "prefill": (1056, 304, (130, 20), False),
-        "prefill_argmax": (640, 16 * 300, (12, 9), True),
+        "prefill_argmax": (640, 16 * 300, (40, 17), True),
     }[case]
     rng = np.random.default_rng(sum(map(ord, case)) + bits)
     qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, bits == 4)
