@@ -1,4 +1,4 @@
-// prefill_kernel.h -- the prefill GEMM (M > 8) and its launcher,
+// prefill_kernel.h -- the prefill GEMM (rows past the decode kernel's) and its launcher,
 // instantiated per (bits, activation mode) by pf_w{4,8}_{hp,lp}.hip.
 #pragma once
 

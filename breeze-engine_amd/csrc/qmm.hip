@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void wsum_kernel(const uint4* __restrict__ W, 
     WS[i * 2 + 1] = 128 * s1;
 }
 
-// ------------------------------------------------------------------ generic rows kernel (M > 8)
+// ------------------------------------------------------------------ generic rows kernel (legacy corr past the decode rows, block-integer export)
 //
 // One workgroup per (16-column tile, 8-row chunk), all of K: waves compute a
 // segment of f values into LDS, then one lane per (m, n) folds them in order.
@@ -1115,10 +1115,11 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     a.C = dC;
     a.Cs = dCs;
 
-    // Decode kernel for M <= dec_rows (row groups of 4: up to 8 rows, up to
-    // 16 where that is set below); the prefill GEMM and the rows kernel serve
-    // larger M, the rows kernel the block-integer export and shapes whose
-    // activation records do not fit in LDS.  The decode kernel quantizes small
+    // Decode kernel for M <= dec_rows (row groups of 4: up to 16 rows, 12 for
+    // wide INT8 handles, 8 for the paired and multi-projection calls); the
+    // prefill GEMM and the rows kernel serve larger M, the rows kernel the
+    // block-integer export and shapes whose activation records do not fit in
+    // LDS.  The decode kernel quantizes small
     // activations itself; larger ones go through the stand-alone quantizer
     // once instead of once per workgroup.
     const int Mr_max = std::min(M, 4);

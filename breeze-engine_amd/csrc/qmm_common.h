@@ -160,12 +160,12 @@ __device__ inline v4i mfma64(const uint4& a, const uint4& b) {
 }
 
 
-// ------------------------------------------------------------------ decode GEMV (M <= 8)
+// ------------------------------------------------------------------ decode GEMV (up to 16 rows)
 //
 // One workgroup of 16 waves per CU owns a contiguous range of 16-column
-// tiles for up to 4 activation rows (M 5..8: one workgroup per row group of
-// 4, the pair placed on the same XCD so the second read of every weight
-// chunk hits its L2).  Waves 0..14 produce: a tile's K range is cut into
+// tiles for up to 4 activation rows (5 to 16 rows: one workgroup per row
+// group of 4, the row groups of a tile range placed on the same XCD so the
+// later reads of every weight chunk hit its L2).  Waves 0..14 produce: a tile's K range is cut into
 // phases of 15 chunks and producer w takes chunk 15p + w of phase p, so
 // every producer streams its weights in K order and the chunks of a phase
 // arrive together.  Per phase each producer runs the MFMA and the in-lane
@@ -406,7 +406,7 @@ constexpr int kDecRing = 2;
 
 constexpr int kLdsMax = 160 * 1024;
 
-// ------------------------------------------------------------------ prefill GEMM (M > 8)
+// ------------------------------------------------------------------ prefill GEMM (more rows)
 //
 // One workgroup of 8 waves computes 32 RP rows (RP = 1, 2 or 4 row pairs of
 // 16-row tiles) x 16*CT columns over all of K.  Wave w owns row pair w % RP
