@@ -11,9 +11,10 @@ namespace bq {
 // preload, 14 SGPRs), so those loads do not wait for a kernarg fetch; the
 // rest of the arguments come from the struct as the code reaches them.
 // Tiles per workgroup group: the first rem_t groups own base_t + 1 tiles, the
-// rest base_t (ntiles = base_t * NG + rem_t).  misc = sc_shift | RG << 8 |
-// xcd << 11 | phases per tile << 16 (RG row groups of 4, up to 4; xcd: the
-// RG workgroups of one tile range share an XCD).  PAIR: gate and up projections
+// rest base_t (ntiles = base_t * NG + rem_t).  misc = sc_shift | log2(4 / RS)
+// << 5 | RG << 8 | xcd << 12 | phases per tile << 16 (RG row groups of RS
+// rows, RS 4 or 2, RG up to 8; xcd: the RG workgroups of one tile range
+// share an XCD).  PAIR: gate and up projections
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
 
@@ -34,8 +35,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     a.ngrp = pngrp;
     a.nblk4 = (pnblk + 3) / 4 * 4;
     a.sc_shift = misc & 31;
-    a.RG = (misc >> 8) & 7;
-    a.pair_xcd = (misc >> 11) & 1;
+    a.RS = 4 >> ((misc >> 5) & 1);
+    a.RG = (misc >> 8) & 15;
+    a.pair_xcd = (misc >> 12) & 1;
     constexpr bool PAIR = FUSE == kFusePair, NORM = FUSE == kFuseNormMulti;
     constexpr bool MULTI = FUSE == kFuseMulti || NORM;
     constexpr int JG = BITS == 8 ? 2 : 4;
@@ -60,8 +62,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         g = blockIdx.x / a.RG;
         rg = blockIdx.x % a.RG;
     }
-    const int m0 = rg * 4;
-    const int Mr = min(4, a.M - m0);
+    const int m0 = rg * a.RS;
+    const int Mr = min(a.RS, a.M - m0);
 
     // Activation loads, ahead of all other set-up in program order: at kernel
     // start the prologue's instructions are fetched cold, and timestamps put
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int npw = misc >> 16;                // phases per tile: ceil(nbg / 15)
     const int U = nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
 
-    const DecLds lay = dec_lds(min(a.M, 4), a.nblk, JG, P64);
+    const DecLds lay = dec_lds(min(a.M, a.RS), a.nblk, JG, P64);
     uint8_t* recs = smem + lay.recs;
     float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
     int* sq_l = reinterpret_cast<int*>(smem + lay.sq);
@@ -650,7 +652,7 @@ hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hi
     }
     const void* act = FUSED ? static_cast<const void*>(a.A) : static_cast<const void*>(a.Aq);
     const int npw = (a.nbg + kProducers - 1) / kProducers;
-    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 11 | npw << 16;
+    const int misc = a.sc_shift | (a.RS == 2 ? 1 : 0) << 5 | a.RG << 8 | a.pair_xcd << 12 | npw << 16;
     const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
     kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, base_t, a.nblk, a.M, a.nbg, rem_t, a.NG, a.ngrp, misc, a);
     return hipGetLastError();

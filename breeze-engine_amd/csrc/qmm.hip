@@ -715,7 +715,7 @@ struct Scratch {
     size_t rec_cap = 0;
     unsigned long long* parts = nullptr;  // argmax partial keys
     size_t parts_cap = 0;
-    unsigned int* ticket = nullptr;  // decode argmax: ticket counter, then 8 row keys; zero between calls
+    unsigned int* ticket = nullptr;  // decode argmax: ticket counter, then kDecMaxRows row keys; zero between calls
     float* gate = nullptr;           // gate projection of the unpaired gate/up path
     size_t gate_cap = 0;
     float* hn = nullptr;  // normalized rows when the norm runs as its own launch
@@ -762,14 +762,14 @@ Scratch* scratch_for(Workspace& w, hipStream_t st) {
 // process ends.  Host code never passes the array's name to a kernel (on the
 // host it is only a stand-in for the symbol): each device's own address of
 // it comes from hipGetSymbolAddress, once per device with that device
-// current, and is kept in g_noalloc_ptr.  Layout per call: [0, 256) the
-// decode argmax state (ticket and 8 row keys, cleared by a fill kernel on
+// current, and is kept in g_noalloc_ptr.  Layout per call: [0, 512) the
+// decode argmax state (ticket and up to 32 row keys, cleared by a fill kernel on
 // every call that uses it), then the activation records of this call (the
 // stand-alone quantizer's records, scales and sums, or the prefill
 // records), then the argmax partials.  Calls that overlap on one device
 // share the array and race.
 constexpr size_t kNoAllocBytes = 16u << 20;
-constexpr size_t kNoAllocState = 256;
+constexpr size_t kNoAllocState = 512;
 static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
 uint8_t* g_noalloc_ptr[kMaxDevices];
 
@@ -1010,19 +1010,25 @@ constexpr int kFusedMaxBlocks = kQuantPasses * 128;  // row-blocks the prologue 
 // LDS bytes of the decode kernel, or 0 if the activation records of a row
 // group do not fit (in LDS, or in the prologue's 6-uint4-per-thread record
 // copy).
-// Most rows the decode kernel takes (row groups of 4, the workgroups of one
-// tile range on one XCD) before the prefill GEMM does.  Measured (us, 12 /
-// 16 rows, GEMM -> decode): W4 K=12288 N=4096 119 -> 21 / 120 -> 22, W8
-// K=5120 N=5120 40 -> 17 / 40 -> 18, W4 K=5120 N=17408 55 -> 28 / 55 -> 34;
-// only W8 at 1088 tiles lost at 16 rows (42 -> 46), so wide W8 stops at 12.
-// BREEZE_HIP_DEC_ROWS sets the limit (1..kDecMaxRows) for tests and tuning.
-constexpr int kDecMaxRows = 16;
+// Most rows the decode kernel takes (row groups, the workgroups of one tile
+// range on one XCD) before the prefill GEMM does.  Measured GEMM -> decode
+// (us): at 12 / 16 rows W4 K=12288 N=4096 119 -> 21 / 120 -> 22, W8
+// K=5120 N=5120 40 -> 17 / 40 -> 18; at 20 / 32 rows W4 K=12288 N=4096
+// 119 -> 28 / 120 -> 37, W8 K=12288 N=4096 87 -> 43 / 88 -> 50, W4 K=4096
+// N=12288 44 -> 29 / 44 -> 42, W4 K=5120 N=17408 56 -> 42 / 56 -> 63, W8
+// K=4096 N=12288 34 -> 40 / 35 -> 51, W8 K=5120 N=17408 at 16 rows 42 -> 46.
+// The GEMM gains with the column tiles it can spread over the CUs, the
+// decode kernel loses with every row group re-reading the weights, so the
+// limit falls with the width, and with INT8 (twice the bytes per weight).
+// BREEZE_HIP_DEC_ROWS sets it (1..kDecMaxRows) for tests and tuning.
+constexpr int kDecMaxRows = 32, kDecMaxGroups = 8;
 int dec_max_rows(int bits, int ntiles, const char* force) {
     if (force) {
         const int v = std::atoi(force);
         if (v >= 1 && v <= kDecMaxRows) return v;
     }
-    return bits == 8 && ntiles >= 1024 ? 12 : kDecMaxRows;
+    if (bits == 8) return ntiles >= 1024 ? 12 : ntiles > 512 ? 16 : 32;
+    return ntiles > 768 ? 24 : 32;
 }
 
 int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG, bool p64 = false) {
@@ -1122,13 +1128,24 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // LDS.  The decode kernel quantizes small
     // activations itself; larger ones go through the stand-alone quantizer
     // once instead of once per workgroup.
-    const int Mr_max = std::min(M, 4);
+    int Mr_max = std::min(M, 4);
     // One or two rows: block pairs per MFMA (P64) when its larger record
     // layout fits in LDS.
     const int lds_p64 = (M <= 2 && !dots) ? plan_dec_lds(a, Mr_max, JG, true) : 0;
     const bool p64 = lds_p64 > 0;
     const int dec_rows = (h2 || mp) ? 8 : dec_max_rows(h->bits, a.ntiles, std::getenv("BREEZE_HIP_DEC_ROWS"));
-    const int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
+    int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
+    // Rows per row group: 4, or 2 where four rows of records do not fit
+    // (long K: the staged copy holds 1536 row-blocks, so two rows reach K =
+    // 24576).  Eight row groups at most.
+    int rs = 4;
+    if (!lds && M > 2 && M <= std::min(dec_rows, 2 * kDecMaxGroups) && !dots && !h2 && !mp) {
+        lds = plan_dec_lds(a, 2, JG);
+        if (lds) {
+            rs = 2;
+            Mr_max = 2;
+        }
+    }
     const bool dec = lds > 0;
     if ((h2 || mp) && !dec) return kNotPairable;
     if (mp && (h->extra || dIdx)) return kNotPairable;
@@ -1189,7 +1206,8 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
             a.norm_exact = ex && ex[0] == '1';
         }
         const int n_cu = device_cus(w, dev);
-        a.RG = (M + 3) / 4;
+        a.RS = rs;
+        a.RG = (M + rs - 1) / rs;
         if (a.RG == 1) {
             a.NG = std::min(a.ntiles, n_cu);
             a.pair_xcd = 0;
@@ -1222,7 +1240,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
                     return -4;
                 // Cleared on st itself: a non-blocking stream does not wait
                 // for work on the null stream.
-                fill_u32_kernel<<<1, 64, 0, st>>>(t, 2 * (1 + kDecMaxRows), 0u);
+                fill_u32_kernel<<<(2 * (1 + kDecMaxRows) + 63) / 64, 64, 0, st>>>(t, 2 * (1 + kDecMaxRows), 0u);
                 if (!hip_ok(hipGetLastError(), "argmax workspace clear")) {
                     w.retired.push_back(t);
                     return -4;
@@ -1663,7 +1681,7 @@ int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64
     if (dIdx && M > 0) {
         // The decode argmax merges into this state and needs it zero; a
         // kernel clears it (a graph may capture this call).
-        fill_u32_kernel<<<1, 64, 0, st>>>(s.ticket, 2 * (1 + kDecMaxRows), 0u);
+        fill_u32_kernel<<<(2 * (1 + kDecMaxRows) + 63) / 64, 64, 0, st>>>(s.ticket, 2 * (1 + kDecMaxRows), 0u);
         if (!hip_ok(hipGetLastError(), "argmax state clear")) return -5;
     }
     return run(w, s, h, dA, M, dC, nullptr, dIdx, st);

@@ -517,13 +517,13 @@ def test_decode_staged_rows_with_argmax(gpu, hb, orc, hi_prec, bits):
 
 
 @pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
-def test_decode_three_and_four_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros):
-    """9 to 16 rows through the decode kernel (three or four workgroups of 4
+def test_decode_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros):
+    """9 to 32 rows through the decode kernel (three to eight workgroups of 4
     rows per tile range, on one XCD when the range count allows; the limit
-    forced to 16), outputs and argmax against the oracle: K = 4608 (staged
+    forced to 32), outputs and argmax against the oracle: K = 4608 (staged
     records, 40 tiles: row groups placed on one XCD) and K = 96 (the prologue
     quantizes; 20 tiles: the plain block order)."""
-    monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "16")
+    monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "32")
     rng = np.random.default_rng(31)
     for K, N in ((4608, 640), (96, 320)):
         qw, sc, qz = rng_weights(rng, N, K, bits, explicit_zeros=explicit_zeros)
@@ -531,7 +531,7 @@ def test_decode_three_and_four_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bi
         try:
             for hp in (True, False):
                 hb.set_hi_prec(hp)
-                for rows in (9, 12, 13, 16):
+                for rows in (9, 12, 13, 16, 20, 25, 32):
                     A = rng.normal(size=(rows, K)).astype(np.float32)
                     A[rng.random(A.shape) < 0.01] *= 20.0
                     want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
@@ -541,3 +541,28 @@ def test_decode_three_and_four_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bi
                     assert idx.cpu().numpy().tolist() == np.argmax(want, axis=1).tolist(), (K, hp, rows)
         finally:
             hb.free(h)
+
+
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
+def test_decode_two_row_groups_long_k(gpu, hb, orc, hi_prec, bits, explicit_zeros):
+    """K = 17408 (544 blocks): four rows of records exceed the decode
+    kernel's staged copy, so 3 to 16 rows run as workgroups of 2 rows (the
+    MLP down projection at decode batch sizes), outputs and argmax against
+    the oracle, default routing."""
+    rng = np.random.default_rng(37)
+    K, N = 17408, 320
+    qw, sc, qz = rng_weights(rng, N, K, bits, explicit_zeros=explicit_zeros)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for rows in (3, 4, 7, 8, 12, 16):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                A[rng.random(A.shape) < 0.01] *= 20.0
+                want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
+                got, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+                gpu.cuda.synchronize()
+                assert bits_equal(got.cpu().numpy(), want), (hp, rows)
+                assert idx.cpu().numpy().tolist() == np.argmax(want, axis=1).tolist(), (hp, rows)
+    finally:
+        hb.free(h)
