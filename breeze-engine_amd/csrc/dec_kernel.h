@@ -13,7 +13,7 @@ namespace bq {
 // Tiles per workgroup group: the first rem_t groups own base_t + 1 tiles, the
 // rest base_t (ntiles = base_t * NG + rem_t).  misc = sc_shift | log2(4 / RS)
 // << 5 | RG << 8 | xcd << 12 | phases per tile << 16 (RG row groups of RS
-// rows, RS 4 or 2, RG up to 8; xcd: the RG workgroups of one tile range
+// rows, RS 4, 2 or 1, RG up to 8; xcd: the RG workgroups of one tile range
 // share an XCD).  PAIR: gate and up projections
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
@@ -35,7 +35,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     a.ngrp = pngrp;
     a.nblk4 = (pnblk + 3) / 4 * 4;
     a.sc_shift = misc & 31;
-    a.RS = 4 >> ((misc >> 5) & 1);
+    a.RS = 4 >> ((misc >> 5) & 3);
     a.RG = (misc >> 8) & 15;
     a.pair_xcd = (misc >> 12) & 1;
     constexpr bool PAIR = FUSE == kFusePair, NORM = FUSE == kFuseNormMulti;
@@ -652,7 +652,7 @@ hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hi
     }
     const void* act = FUSED ? static_cast<const void*>(a.A) : static_cast<const void*>(a.Aq);
     const int npw = (a.nbg + kProducers - 1) / kProducers;
-    const int misc = a.sc_shift | (a.RS == 2 ? 1 : 0) << 5 | a.RG << 8 | a.pair_xcd << 12 | npw << 16;
+    const int misc = a.sc_shift | (a.RS == 1 ? 2 : a.RS == 2 ? 1 : 0) << 5 | a.RG << 8 | a.pair_xcd << 12 | npw << 16;
     const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
     kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, base_t, a.nblk, a.M, a.nbg, rem_t, a.NG, a.ngrp, misc, a);
     return hipGetLastError();

@@ -1135,15 +1135,17 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     const bool p64 = lds_p64 > 0;
     const int dec_rows = (h2 || mp) ? 8 : dec_max_rows(h->bits, a.ntiles, std::getenv("BREEZE_HIP_DEC_ROWS"));
     int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
-    // Rows per row group: 4, or 2 where four rows of records do not fit
-    // (long K: the staged copy holds 1536 row-blocks, so two rows reach K =
-    // 24576).  Eight row groups at most.
+    // Rows per row group: 4, or 2 or 1 where four rows of records do not
+    // fit (long K: the staged copy holds 1536 row-blocks, so two rows reach
+    // K = 24576 and one row K = 49152).  Eight row groups at most.
     int rs = 4;
-    if (!lds && M > 2 && M <= std::min(dec_rows, 2 * kDecMaxGroups) && !dots && !h2 && !mp) {
-        lds = plan_dec_lds(a, 2, JG);
+    for (int r = 2; r >= 1 && !lds; r >>= 1) {
+        if (r >= Mr_max) continue;  // that plan did not fit
+        if (M > std::min(dec_rows, r * kDecMaxGroups) || dots || h2 || mp) break;
+        lds = plan_dec_lds(a, r, JG);
         if (lds) {
-            rs = 2;
-            Mr_max = 2;
+            rs = r;
+            Mr_max = r;
         }
     }
     const bool dec = lds > 0;

@@ -217,7 +217,7 @@ struct GemvArgs {
     const int32_t* D2;
     int M, N, K, nblk, nblk4, nbg, nblk_pad, sc_shift, ngrp, flags;
     int ntiles, NG, RG, pair_xcd;
-    int RS;  // rows per row group: 4, or 2 where four rows of records do not fit in LDS
+    int RS;  // rows per row group: 4, or 2 or 1 where four rows of records do not fit
     // Multi-projection launch: up to kMaxSeg weight sets of one layout (all
     // but N alike) whose 16-column tiles are concatenated in order; segment
     // k owns tiles [seg_end[k - 1], seg_end[k]) and writes segC[k], a

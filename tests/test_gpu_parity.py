@@ -566,3 +566,27 @@ def test_decode_two_row_groups_long_k(gpu, hb, orc, hi_prec, bits, explicit_zero
                 assert idx.cpu().numpy().tolist() == np.argmax(want, axis=1).tolist(), (hp, rows)
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_decode_one_row_groups_longer_k(gpu, hb, orc, hi_prec, bits):
+    """K = 26624 (832 blocks): even two rows of records exceed the decode
+    kernel's staged copy, so 2 to 8 rows run as workgroups of one row; more
+    rows take the GEMM.  Outputs and argmax against the oracle."""
+    rng = np.random.default_rng(41)
+    K, N = 26624, 160
+    qw, sc, qz = rng_weights(rng, N, K, bits)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for rows in (1, 2, 3, 8, 9):
+                A = rng.normal(size=(rows, K)).astype(np.float32)
+                A[rng.random(A.shape) < 0.01] *= 20.0
+                want = orc.matmul(qw, sc, qz, N, K, bits, A, hp)
+                got, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+                gpu.cuda.synchronize()
+                assert bits_equal(got.cpu().numpy(), want), (hp, rows)
+                assert idx.cpu().numpy().tolist() == np.argmax(want, axis=1).tolist(), (hp, rows)
+    finally:
+        hb.free(h)
