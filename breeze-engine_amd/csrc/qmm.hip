@@ -1121,8 +1121,8 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     a.C = dC;
     a.Cs = dCs;
 
-    // Decode kernel for M <= dec_rows (row groups of 4: up to 16 rows, 12 for
-    // wide INT8 handles, 8 for the paired and multi-projection calls); the
+    // Decode kernel for M <= dec_rows (row groups: up to 32 rows, fewer for
+    // wide handles, 16 for the paired and multi-projection calls); the
     // prefill GEMM and the rows kernel serve larger M, the rows kernel the
     // block-integer export and shapes whose activation records do not fit in
     // LDS.  The decode kernel quantizes small
@@ -1133,7 +1133,10 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // layout fits in LDS.
     const int lds_p64 = (M <= 2 && !dots) ? plan_dec_lds(a, Mr_max, JG, true) : 0;
     const bool p64 = lds_p64 > 0;
-    const int dec_rows = (h2 || mp) ? 8 : dec_max_rows(h->bits, a.ntiles, std::getenv("BREEZE_HIP_DEC_ROWS"));
+    // The paired and multi-projection calls take row groups of 4, at most 16
+    // rows.
+    const int dec_rows = std::min((h2 || mp) ? 16 : kDecMaxRows,
+                                  dec_max_rows(h->bits, a.ntiles, std::getenv("BREEZE_HIP_DEC_ROWS")));
     int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     // Rows per row group: 4, or 2 or 1 where four rows of records do not
     // fit (long K: the staged copy holds 1536 row-blocks, so two rows reach

@@ -107,9 +107,9 @@ int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* 
  * forbid it.  All of its device scratch is one static 16 MiB array per
  * device, so a call whose activation records do not fit is refused (-4,
  * i4_last_error() says why): about 72 bytes per row and 32-block of K when
- * the decode kernel stages its records (up to 16 rows, M*K above 16384), and
+ * the decode kernel stages its records (up to 32 rows, M*K above 16384), and
  * about 68 bytes per 32-block of K per row, rows rounded up to 32, 64 or 128, for
- * more than 8 rows.  Calls that overlap on one device share the array and
+ * the rows the prefill GEMM takes.  Calls that overlap on one device share the array and
  * race: serialize them.  Outputs are those of i4_matmul_dev /
  * i4_matmul_argmax_dev, bit for bit. */
 int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream);

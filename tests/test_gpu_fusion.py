@@ -50,21 +50,21 @@ def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, bits, expl
             assert hb.handle_info(hg)["scale_group"] == 4
         for hp in (False, True):
             hb.set_hi_prec(hp)
-            A = (rng.normal(size=(9, K)) * 2).astype(np.float32)
+            A = (rng.normal(size=(20, K)) * 2).astype(np.float32)
             g = orc.matmul(qg, sg, zg, N, K, bits, A, hp)
             u = orc.matmul(qu, su, zu, N, K, bits, A, hp)
             want = _silu_mul(g, u)
             fused = {}
-            for rows in (1, 2, 3, 5, 8):
+            for rows in (1, 2, 3, 5, 8, 12, 16):
                 got = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A[:rows]).cuda(), N).cpu().numpy()
                 np.testing.assert_allclose(got, want[:rows], rtol=1e-6, atol=1e-30, err_msg=f"{rows} rows")
                 fused[rows] = got
-            # Nine rows take the two-launch fallback: same bits as one-launch rows.
-            got9 = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A).cuda(), N).cpu().numpy()
+            # Twenty rows take the two-launch fallback: same bits as one-launch rows.
+            got20 = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A).cuda(), N).cpu().numpy()
             torch.cuda.synchronize()
-            assert bits_equal(got9[:8], fused[8]), hp
-            assert bits_equal(got9[:1], fused[1]), hp
-            np.testing.assert_allclose(got9, want, rtol=1e-6, atol=1e-30)
+            assert bits_equal(got20[:16], fused[16]), hp
+            assert bits_equal(got20[:1], fused[1]), hp
+            np.testing.assert_allclose(got20, want, rtol=1e-6, atol=1e-30)
     finally:
         hb.free(hg)
         hb.free(hu)

@@ -3,8 +3,8 @@ against the oracle, bit for bit: the Qwen3.5-27B decoder's in_qkv, in_z,
 in_b, in_a (kernel/qwen35_decoder.cpp:285-288; K = 5120, N = 10240, 6144,
 48, 48) and q, k, v (334-336; N = 12288, 1024, 1024), odd widths whose
 segment boundaries fall inside workgroups, a partial last chunk, one to
-eight rows (one and two row groups), and the shapes that fall back to one
-launch per projection (mixed bits, explicit zero points, more than 8
+sixteen rows (one to four row groups), and the shapes that fall back to one
+launch per projection (mixed bits, explicit zero points, more than 16
 rows)."""
 import numpy as np
 import pytest
@@ -39,7 +39,7 @@ def test_multi_projection_bit_exact(gpu, hb, orc, hi_prec, shape, bits):
     try:
         for hp in (True, False):
             hb.set_hi_prec(hp)
-            for M in (1, 2, 3, 5, 8):
+            for M in (1, 2, 3, 5, 8, 12, 16):
                 A = rng.normal(size=(M, K)).astype(np.float32)
                 A[rng.random(A.shape) < 0.01] *= 20.0
                 print(f"multi {shape} bits={bits} hp={hp} M={M}", flush=True)
@@ -53,7 +53,7 @@ def test_multi_projection_bit_exact(gpu, hb, orc, hi_prec, shape, bits):
             hb.free(h)
 
 
-@pytest.mark.parametrize("case", ["mixed_bits", "explicit_zeros", "rows_12", "single"])
+@pytest.mark.parametrize("case", ["mixed_bits", "explicit_zeros", "rows_20", "single"])
 def test_multi_projection_fallbacks(gpu, hb, orc, hi_prec, case):
     """Shapes one decode launch does not take run one launch per projection
     and give the same bits."""
@@ -68,7 +68,7 @@ def test_multi_projection_fallbacks(gpu, hb, orc, hi_prec, case):
         specs = [(4, 512, False)]
     else:
         specs = [(8, 256, False), (8, 96, False), (8, 32, False)]
-    M = 12 if case == "rows_12" else 4
+    M = 20 if case == "rows_20" else 4
     ws = [rng_weights(rng, N, K, b, np.float32, z) for b, N, z in specs]
     hs = [hb.prepack(qw, sc, qz, K, N, bits=b) for (qw, sc, qz), (b, N, _) in zip(ws, specs)]
     try:

@@ -3,10 +3,12 @@
 hn = rmsnorm(x, w, eps) (kernel/qwen35_decoder.cpp:134-140) and each
 projection of hn.  The Qwen3.5-27B in_qkv/in_z/in_b/in_a shapes (K = 5120)
 at one to three rows take the fused launch, four and eight rows the
-norm-then-projections fallback; rows from the RMSNorm parity set (ties,
-vanishing terms, outliers, denormals, a mean on a float rounding midpoint
-that the bound leaves to the in-order sum) at K = 4096; each case as shipped
-and with BREEZE_HIP_NORM_EXACT=1 (every row through the in-order sum)."""
+norm-then-projections fallback (a row group's 4 x 160 blocks exceed the
+512 row-blocks the prologue quantizes); rows from the RMSNorm parity set
+(ties, vanishing terms, outliers, denormals, a mean on a float rounding
+midpoint that the bound leaves to the in-order sum) at K = 4096, one at a
+time and all together (row groups of 4, fused); each case as shipped and
+with BREEZE_HIP_NORM_EXACT=1 (every row through the in-order sum)."""
 import numpy as np
 import pytest
 
@@ -84,6 +86,17 @@ def test_norm_in_prologue_adversarial_rows(gpu, hb, orc, hi_prec, monkeypatch, m
                 if np.all(np.isfinite(hn_ref)):
                     assert bits_equal(outs[0].cpu().numpy(), orc.matmul(*w4, None, 64, K, 4, hn_ref, True)), (r, eps)
                     assert bits_equal(outs[1].cpu().numpy(), orc.matmul(*w8, None, 32, K, 8, hn_ref, True)), (r, eps)
+            # All the rows at once: four row groups of 4, each normalizing its
+            # own rows in the prologue of the one launch.
+            with np.errstate(all="ignore"):
+                hn_ref = orc.rmsnorm(rows, ln, eps)
+            outs, hn = hb.rmsnorm_matmul_multi(torch.from_numpy(rows).cuda(), torch.from_numpy(ln).cuda(),
+                                               float(eps), [h4, h8], [64, 32], want_hn=True)
+            torch.cuda.synchronize()
+            assert _same(hn.cpu().numpy(), hn_ref), ("all rows", eps)
+            fin = np.all(np.isfinite(hn_ref), axis=1)
+            assert bits_equal(outs[0].cpu().numpy()[fin], orc.matmul(*w4, None, 64, K, 4, hn_ref[fin], True)), eps
+            assert bits_equal(outs[1].cpu().numpy()[fin], orc.matmul(*w8, None, 32, K, 8, hn_ref[fin], True)), eps
     finally:
         hb.free(h4)
         hb.free(h8)
