@@ -18,7 +18,7 @@ namespace bq {
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
 
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64, int PW>
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64>
 __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
                                                              int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
                                                              int pNG, int pngrp, int misc, GemvArgs args) {
@@ -506,16 +506,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // goes first, since weight requests issued beside it slowed it down
     // (three and four rows: 11.8 -> 11.3 us).
     Unit<JG, EXTRA> ring[R];
-    // Window: the first PW units, loaded with the ring's first R at kernel
-    // start, so the weights stream while the activations arrive and are
-    // quantized; the ring takes over from unit PW.
-    Unit<JG, EXTRA> win[PW > 0 ? PW : 1];
     if (!FUSED) {
         store_acts();
         __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int d = 0; d < PW; ++d) load_unit(win[d]);
 #pragma unroll
     for (int d = 0; d < R; ++d) load_unit(ring[d]);
     __builtin_amdgcn_sched_barrier(0);
@@ -616,13 +610,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         }
     };
 
-#pragma unroll
-    for (int d = 0; d < PW; ++d) {
-        consume(win[d], d & 1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (d < U) lds_barrier();  // uniform over the workgroup
-    }
-    for (int u0 = PW; u0 < U; u0 += R) {
+    for (int u0 = 0; u0 < U; u0 += R) {
 #pragma unroll
         for (int d = 0; d < R; ++d) {
             const bool live = u0 + d < U;  // uniform over the workgroup
@@ -634,16 +622,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     }
 }
 
-// Window depths instantiated for handles without per-block metadata and
-// without the gate/up pairing (index into attribute keys: position + 1).
-constexpr int kDecWindows[] = {3, 7};
-
-template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64, int PW>
+template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64>
 hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hipStream_t st) {
-    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, FUSE, P64, PW>;
-    const int wsel = PW == 0 ? 0 : PW == kDecWindows[0] ? 1 : 2;
+    auto kern = dec_kernel<BITS, HP, FUSED, EXTRA, R, FUSE, P64>;
     const int key = (BITS == 8 ? 1 : 0) | (HP ? 2 : 0) | (FUSED ? 4 : 0) | (EXTRA ? 8 : 0) | ((R / 2 - 1) << 4) |
-                    (P64 ? 32 : 0) | FUSE << 6 | wsel << 8;
+                    (P64 ? 32 : 0) | FUSE << 6;
     if (!attr_set[key]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
@@ -658,48 +641,23 @@ hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hi
     return hipGetLastError();
 }
 
-// Window depth: the deepest instantiated one that the workgroup with the
-// fewest units fills together with the ring (units past a workgroup's end
-// would only re-read its last chunk).  Off unless BREEZE_HIP_DEC_PW names an
-// instantiated depth: issuing the window's units costs ~20 scalar
-// instructions each on the CU's one scalar unit, shared by all sixteen
-// waves, and every decode workload measured slower with it.
-inline int pick_dec_window(const GemvArgs& a, int R) {
-    const char* f = std::getenv("BREEZE_HIP_DEC_PW");
-    if (!f) return 0;
-    const int v = std::atoi(f);
-    for (int w : kDecWindows)
-        if (w == v) return v;
-    return 0;
-}
-
 template <int BITS, bool HP, bool FUSED, bool EXTRA, bool P64>
 hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, hipStream_t st) {
     if (fuse == kFusePair)
-        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePair, P64, 0>(attr_set, a, grid, lds, st);
+        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePair, P64>(attr_set, a, grid, lds, st);
     if constexpr (!EXTRA) {
         if (fuse == kFuseMulti)
-            return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseMulti, P64, 0>(attr_set, a, grid, lds, st);
+            return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseMulti, P64>(attr_set, a, grid, lds, st);
         if constexpr (FUSED) {
             if (fuse == kFuseNormMulti)
-                return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseNormMulti, P64, 0>(attr_set, a, grid, lds,
-                                                                                              st);
+                return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseNormMulti, P64>(attr_set, a, grid, lds, st);
         } else if (fuse == kFuseNormMulti) {
             return hipErrorInvalidValue;  // the host normalizes first when the prologue does not quantize
-        }
-        switch (pick_dec_window(a, kDecRing)) {
-            case kDecWindows[0]:
-                return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, kDecWindows[0]>(attr_set, a,
-                                                                                                       grid, lds, st);
-            case kDecWindows[1]:
-                return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, kDecWindows[1]>(attr_set, a,
-                                                                                                       grid, lds, st);
-            default: break;
         }
     } else if (fuse >= kFuseMulti) {
         return hipErrorInvalidValue;  // the host sends per-block-metadata handles one by one
     }
-    return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64, 0>(attr_set, a, grid, lds, st);
+    return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePlain, P64>(attr_set, a, grid, lds, st);
 }
 
 template <int BITS, bool HP, bool FUSED, bool EXTRA>

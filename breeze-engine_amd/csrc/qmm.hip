@@ -734,7 +734,7 @@ struct Workspace {
     size_t hA_cap = 0, hC_cap = 0;
     hipStream_t stream = nullptr;
     int n_cu = 0;
-    bool attr_set[1024] = {};
+    bool attr_set[256] = {};  // decode kernel variants with the kernel attribute set
     bool pf_attr[256] = {};
 };
 
