@@ -266,7 +266,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
         auto compute = [&](const char* cp, auto nb_tag, auto dma_tag, int c_next, uint32_t nbase, uint32_t nraw) {
             constexpr int NB = decltype(nb_tag)::value;
             constexpr bool DMA = decltype(dma_tag)::value != 0;
-            constexpr bool FIRST = decltype(dma_tag)::value == 1;
+            constexpr bool BOTH = decltype(dma_tag)::value == 3;  // both chunks of the next stage
+            constexpr bool FIRST = decltype(dma_tag)::value == 1 || BOTH;
+            const int c_next2 = min(c_next + 1, nch - 1);
             constexpr int kAhead = 1;            // groups read ahead
             constexpr int NGB = NG * NB;         // group steps
             constexpr int NS = NGB + (ODD ? NB : 0);
@@ -426,6 +428,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                 if (s < NGB && s % NB == 0) load_group(s / NB + kAhead);
                 if (s == NGB - 1) load_odd();
                 if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s, FIRST, nraw);
+                if (BOTH && s >= kDmaChunk && s < 2 * kDmaChunk)
+                    dma_slot(c_next2, nbase + (uint32_t)L::kChunk, s - kDmaChunk, false, nraw);
                 step_h(s + 1);
                 step_e(s);
                 step_d(s + 1);
@@ -434,6 +438,11 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             if (DMA) {
 #pragma unroll
                 for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d, FIRST, nraw);
+                if (BOTH) {
+#pragma unroll
+                    for (int d = (NS > kDmaChunk ? NS - kDmaChunk : 0); d < kDmaChunk; ++d)
+                        dma_slot(c_next2, nbase + (uint32_t)L::kChunk, d, false, nraw);
+                }
             }
         };
 
@@ -443,6 +452,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
         constexpr std::integral_constant<int, 1> dma0{};
         constexpr std::integral_constant<int, 2> dma1{};
         constexpr std::integral_constant<int, 0> no_dma{};
+        constexpr std::integral_constant<int, 3> dma01{};
         // Ring of S stage buffers: stage g lives in buffer g % S.  The first
         // S - 1 stages are issued up front; computing stage g issues stage
         // g + S - 1 (chunks clamped to the last one).  At the start of stage
@@ -469,9 +479,16 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             if (S == 2 || gn < nst) {
                 if (active) {
                     const char* sp = pf_lds + buf * L::kStage;
-                    compute(sp, two, dma0, cn, nbase, raw_base(gn));
-                    compute(sp + L::kChunk, two, dma1, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk,
-                            raw_base(gn));
+                    if (S == 2) {
+                        // Both chunks' loads during the first chunk: the
+                        // second chunk's have a whole chunk to land.
+                        compute(sp, two, dma01, cn, nbase, raw_base(gn));
+                        compute(sp + L::kChunk, two, no_dma, 0, 0u, 0u);
+                    } else {
+                        compute(sp, two, dma0, cn, nbase, raw_base(gn));
+                        compute(sp + L::kChunk, two, dma1, min(cn + 1, nch - 1), nbase + (uint32_t)L::kChunk,
+                                raw_base(gn));
+                    }
                 } else {
                     issue_stage(gn, bn);
                 }
