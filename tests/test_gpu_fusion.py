@@ -6,7 +6,7 @@ Both projections are the exact path (bit-identical to the oracle), so the
 result is compared with the oracle's projections through float32 SiLU and
 product: the only difference allowed is exp's last-place rounding (the
 device expf against numpy's), bounded here at 1e-6 relative.  The one-launch
-path (M <= 8, handles of the same layout) and the two-launch fallback use the
+path (M <= 16, handles of the same layout) and the two-launch fallback use the
 same device arithmetic and must agree bit for bit."""
 import numpy as np
 import pytest
