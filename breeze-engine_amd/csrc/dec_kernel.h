@@ -1,4 +1,4 @@
-// dec_kernel.h -- the decode GEMV kernel (up to 16 rows) and its launcher,
+// dec_kernel.h -- the decode GEMV kernel (up to 32 rows) and its launcher,
 // instantiated per (bits, activation mode) by dec_w{4,8}_{hp,lp}.hip.
 #pragma once
 
