@@ -256,26 +256,29 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
 template <bool HP>
 __global__ __launch_bounds__(256) void quantize_rec_kernel(const float* __restrict__ A, int M, int K, int nblk,
                                                            int nch, int Mpad, uint8_t* __restrict__ R) {
-    const int gtid = blockIdx.x * 256 + threadIdx.x;
-    const int blk = gtid >> 3, e = gtid & 7;
+    // A wave per (16-row tile, block j): lane (r, o) = (lane >> 2, lane & 3)
+    // quantizes k-octet o of row r, the 4 lanes of a row one block, and
+    // writes the octet's 16-byte record slot [8 h bytes | 8 l bytes].  The
+    // wave's 64 slots are the block's whole 1 KB part of the record.
+    const int g = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int o = lane & 3, r = lane >> 2;
     const int nb2 = 2 * nch;
-    const int m = blk / nb2, j = blk - m * nb2;
-    const bool inside = m < Mpad;
+    const int mt = g / nb2, j = g - mt * nb2, m = 16 * mt + r;
+    if (mt * 16 >= Mpad) return;  // whole waves only: the quad reductions need all lanes
     const bool valid = m < M && j < nblk;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (valid) v = *reinterpret_cast<const float4*>(A + (size_t)m * K + 32 * j + 4 * e);
-    float s;
-    int sum;
-    uint32_t p0, p1;
-    quant8<HP>(v, s, sum, p0, p1);
-    if (inside) {
-        uint8_t* rec = R + ((size_t)(m >> 4) * nch + (j >> 1)) * kRecBytes;
-        const int b = j & 1, r = m & 15;
-        uint8_t* p = rec + b * 1024 + ((e >> 1) * 16 + r) * 16 + (e & 1) * 4;
-        *reinterpret_cast<uint32_t*>(p) = p0;
-        *reinterpret_cast<uint32_t*>(p + 8) = p1;
-        if (e == 0) *reinterpret_cast<float*>(rec + kRecA + (b * 16 + r) * 4) = s;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (valid) {
+        const float* src = A + (size_t)m * K + 32 * j + 8 * o;
+        v0 = *reinterpret_cast<const float4*>(src);
+        v1 = *reinterpret_cast<const float4*>(src + 4);
     }
+    float s;
+    uint2 ph, pl;
+    quant4x8<HP>(v0, v1, s, ph, pl);
+    uint8_t* rec = R + ((size_t)mt * nch + (j >> 1)) * kRecBytes;
+    const int b = j & 1;
+    *reinterpret_cast<uint4*>(rec + b * 1024 + (o * 16 + r) * 16) = make_uint4(ph.x, ph.y, pl.x, pl.y);
+    if (o == 0) *reinterpret_cast<float*>(rec + kRecA + (b * 16 + r) * 4) = s;
 }
 
 // Row pairs per prefill workgroup: 32 rows for up to 32 rows, 64 for up to
@@ -1170,7 +1173,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         // Records in MFMA operand order for the prefill GEMM.
         if (!grow(w, st, &s.rec, &s.rec_cap, (size_t)(Mpad / 16) * nch_rec * kRecBytes, "workspace alloc", s.fixed))
             return -4;
-        const size_t threads = (size_t)Mpad * nch_rec * 2 * 8;
+        const size_t threads = (size_t)(Mpad / 16) * nch_rec * 2 * 64;  // a wave per (16 rows, block)
         const unsigned qb = (unsigned)((threads + 255) / 256);
         if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);
         else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);

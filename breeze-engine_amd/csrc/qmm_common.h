@@ -126,6 +126,48 @@ __device__ inline void quant8(float4 v, float& s_out, int& sum_out, uint32_t& p0
     p1 = w1;
 }
 
+// The same quantization with 4 lanes a block, 8 consecutive k per lane (lane
+// q of the quad holds k = 8q..8q+7), for the prefill records: the block
+// scale in every lane of the quad, and this lane's 8 bytes of record part 0
+// (ph) and part 1 (pl).  Every step is quant8's, element for element, so
+// the results are the same bits.  All 64 lanes of the wave must call it.
+template <bool HP>
+__device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, uint2& pl) {
+    const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float ab[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ab[i] = fabsf(__builtin_canonicalizef(x[i]));
+    float amax = fmaxf(fmaxf(fmaxf(fmaxf(ab[0], ab[1]), 0.0f), fmaxf(ab[2], ab[3])),
+                       fmaxf(fmaxf(ab[4], ab[5]), fmaxf(ab[6], ab[7])));
+    int am = __float_as_int(amax);  // >= +0: integer order is float order
+    am = max(am, dpp_xor1(am));
+    am = max(am, dpp_xor2(am));
+    amax = __int_as_float(am);
+    constexpr int qmax = HP ? 32767 : 127;
+    const float s = amax / (float)qmax;
+    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+    uint32_t w0[2] = {0u, 0u}, w1[2] = {0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float prod = x[i] * inv;
+        int q = 0;
+        if (__builtin_isfinite(prod)) {
+            q = (int)rintf(prod);
+            q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
+        }
+        if (HP) {
+            const uint32_t u = (uint32_t)(q + 32768);
+            w0[i >> 2] |= (((u >> 8) ^ 0x80u) & 0xFFu) << (8 * (i & 3));
+            w1[i >> 2] |= (((u & 0xFFu) ^ 0x80u) & 0xFFu) << (8 * (i & 3));
+        } else {
+            w0[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+        }
+    }
+    s_out = s;
+    ph = make_uint2(w0[0], w0[1]);
+    pl = make_uint2(w1[0], w1[1]);
+}
+
 __device__ inline uint64_t unpack_b(const uint4& w, int jb, int bits) {
     if (bits == 8) {
         const uint32_t lo = jb == 0 ? w.x : w.z, hi = jb == 0 ? w.y : w.w;
