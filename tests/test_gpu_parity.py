@@ -462,23 +462,27 @@ def _special_rows(rng, K):
 
 
 @pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
-def test_non_finite_and_extreme_activations(gpu, hb, orc, hi_prec, bits, explicit_zeros):
+def test_non_finite_and_extreme_activations(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros):
     """Activation blocks with NaNs (quiet and signaling: skipped by the block
     max), infinities (the row becomes NaN), denormals, signed zeros, values
     near the float maximum and tiny normals, through every quantizer: the
     decode kernel's own (one row; 16 and 256 row-blocks), the stand-alone
-    decode quantizer (4 rows of K = 4608) and the records for M > 8 (all
-    nine rows at once).  Outputs match the oracle bit for bit outside NaNs."""
+    decode quantizer (4 rows of K = 4608), the decode kernel's row groups
+    (all nine rows at once) and the prefill GEMM's records (the nine rows
+    again with the decode kernel held to 8 rows).  Outputs match the oracle
+    bit for bit outside NaNs."""
     rng = np.random.default_rng(91 + bits)
     N = 48
-    for K, groups in ((512, "single"), (8192, "single"), (4608, "four"), (512, "all")):
+    for K, groups in ((512, "single"), (8192, "single"), (4608, "four"), (512, "all"), (512, "gemm")):
+        if groups == "gemm":
+            monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "8")
         qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
         h = hb.prepack(qw, sc, qz, K, N, bits=bits)
         try:
             A = _special_rows(rng, K)
             batches = {"single": [A[i:i + 1] for i in range(len(A))],
                        "four": [A[0:4], A[4:8]],
-                       "all": [A]}[groups]
+                       "all": [A], "gemm": [A]}[groups]
             for hp in (False, True):
                 hb.set_hi_prec(hp)
                 for x in batches:
