@@ -168,9 +168,10 @@ def test_legacy_corr_is_honoured(gpu, hb, orc, hi_prec, bits):
     try:
         for hp in (False, True):
             hb.set_hi_prec(hp)
-            # 5 and 9 rows: the decode kernel; 17 and 33: the rows kernel's
-            # corr delta in row chunks of 8 (quantized_matmul.cpp:542-550).
-            for rows in (5, 9, 17, 33):
+            # 5, 9 and 17 rows: the decode kernel (up to 32 rows here); 33
+            # and 40: the rows kernel's corr delta in row chunks of 8
+            # (quantized_matmul.cpp:542-550).
+            for rows in (5, 9, 17, 33, 40):
                 A = rng.normal(size=(rows, K)).astype(np.float32)
                 want = orc.matmul_legacy(B, scale, zp, corr, N, K, bits, A, hp)
                 assert bits_equal(hb.matmul(h, A, N), want), (hp, rows)
@@ -182,8 +183,8 @@ def test_legacy_corr_is_honoured(gpu, hb, orc, hi_prec, bits):
 def test_legacy_int4_signed_zero_points(gpu, hb, orc, hi_prec, zp_lo, zp_hi):
     """Legacy INT4 handles keep signed int8 zero points from -112 up
     (b = nibble - zp never wraps there) with a consistent corr, so they stay
-    INT4 with explicit zero points: the decode kernel (1, 3, 8, 9 rows) and
-    the prefill GEMM's in-LDS nibble expansion (17, 130 rows), whose per-byte
+    INT4 with explicit zero points: the decode kernel (1, 3, 8, 9, 17 rows)
+    and the prefill GEMM's in-LDS nibble expansion (33, 130 rows), whose per-byte
     n - zp must not borrow across bytes for negative zp.  33 blocks: a
     partial last 4-block chunk."""
     N, K = 64, 1056
@@ -202,7 +203,7 @@ def test_legacy_int4_signed_zero_points(gpu, hb, orc, hi_prec, zp_lo, zp_hi):
         assert info["bits"] == 4 and not info["has_corr_delta"], info
         for hp in (True, False):
             hb.set_hi_prec(hp)
-            for rows in (1, 3, 8, 9, 17, 130):
+            for rows in (1, 3, 8, 9, 17, 33, 130):
                 A = rng.normal(size=(rows, K)).astype(np.float32)
                 A[rng.random(A.shape) < 0.01] *= 20.0
                 want = orc.matmul_legacy(B, scale, zp, corr, N, K, 4, A, hp)

@@ -72,7 +72,8 @@ def test_noalloc_matches_allocating_entry(gpu, hb, hi_prec, case, bits):
 @pytest.mark.parametrize("bits", [4, 8])
 def test_noalloc_legacy_corr_rows_kernel(gpu, hb, orc, hi_prec, bits):
     """A legacy handle whose corr disagrees with its weights takes the rows
-    kernel for more than 8 rows (staged records in the fixed scratch)."""
+    kernel past the decode kernel's 32 rows (staged records in the fixed
+    scratch)."""
     torch = gpu
     N, K, nblk = 48, 384, 12
     rng = np.random.default_rng(31 + bits)
@@ -85,7 +86,7 @@ def test_noalloc_legacy_corr_rows_kernel(gpu, hb, orc, hi_prec, bits):
     assert h, hb.last_error()
     try:
         hb.set_hi_prec(True)
-        for m in (17, 9):
+        for m in (40, 33):
             A = rng.normal(size=(m, K)).astype(np.float32)
             got, _ = _noalloc(hb, torch, h, A, N, False)
             want, _ = _reference_call(hb, torch, h, A, N, False)
