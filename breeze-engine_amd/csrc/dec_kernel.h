@@ -72,30 +72,36 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // 32-float blocks, and the staged scale and sum rows (pitch nblk4) are
     // contiguous too: a block index is an offset, with no row/column split.
     const int nb_rows = Mr * a.nblk;
-    uint4 av[kQuantPasses];
-    uint4 wn[NORM ? kQuantPasses : 1];  // NORM: the norm weights of those elements
+    // Lane q = tid & 3 of a quad holds k = 8q..8q+7 of its block: two uint4
+    // per pass, in named registers (arrays indexed under the passes' early
+    // exits were placed in scratch).
+    static_assert(kQuantPasses == 2, "the prologue spells out two passes");
+    Oct av0, av1;
+    Oct wn0, wn1;  // NORM: the norm weights of those elements
     uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
     if (FUSED) {
         if (nb_rows > kQuantEarlyBlocks || wave < 8) {
-            const float* arow = a.A + (size_t)m0 * a.K + 4 * (tid & 7);
+            const float* arow = a.A + (size_t)m0 * a.K + 8 * (tid & 3);
             const bool all = nb_rows > kQuantEarlyBlocks;
-            const int qb = all ? 128 : 64;  // blocks per pass
-            const int npass_ld = all ? (nb_rows + 127) >> 7 : (nb_rows + 63) >> 6;
-#pragma unroll
-            for (int p = 0; p < kQuantPasses; ++p) {
-                if (p >= npass_ld) break;
-                const int blk = min(p * qb + (tid >> 3), nb_rows - 1);
-                av[p] = *reinterpret_cast<const uint4*>(arow + 32 * blk);
-            }
+            const int qb = all ? 256 : 128;  // blocks per pass
+            const bool two = all && nb_rows > 256;
+            auto ld = [&](int p, Oct& v) {
+                const int blk = min(p * qb + (tid >> 2), nb_rows - 1);
+                v.x = *reinterpret_cast<const uint4*>(arow + 32 * blk);
+                v.y = *reinterpret_cast<const uint4*>(arow + 32 * blk + 4);
+            };
+            ld(0, av0);
+            if (two) ld(1, av1);
             if (NORM) {
-#pragma unroll
-                for (int p = 0; p < kQuantPasses; ++p) {
-                    if (p >= npass_ld) break;
-                    const int blk = min(p * qb + (tid >> 3), nb_rows - 1);
+                auto ldw = [&](int p, Oct& v) {
+                    const int blk = min(p * qb + (tid >> 2), nb_rows - 1);
                     const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk);
-                    wn[NORM ? p : 0] =
-                        *reinterpret_cast<const uint4*>(a.normW + 32 * (blk - m * a.nblk) + 4 * (tid & 7));
-                }
+                    const float* wrow = a.normW + 32 * (blk - m * a.nblk) + 8 * (tid & 3);
+                    v.x = *reinterpret_cast<const uint4*>(wrow);
+                    v.y = *reinterpret_cast<const uint4*>(wrow + 4);
+                };
+                ldw(0, wn0);
+                if (two) ldw(1, wn1);
             }
         }
     } else {
@@ -230,12 +236,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     auto store_acts = [&]() {
         if (FUSED) {
             const bool all = nb_rows > kQuantEarlyBlocks;
-            const int qb = all ? 128 : 64;  // blocks per pass
-            const int npass = all ? (nb_rows + 127) >> 7 : wave < 8 ? (nb_rows + 63) >> 6 : 0;
+            const int qb = all ? 256 : 128;  // blocks per pass
+            const int npass = all ? (nb_rows + 255) >> 8 : wave < 8 ? 1 : 0;  // 0, 1 or 2
             // NORM: the decoder's RMSNorm of each row first, hn = (x * inv) * w
             // with inv = 1 / sqrtf((float)(ss / K) + eps)
             // (kernel/qwen35_decoder.cpp:134-140), bit for bit.  The block
-            // sums of squares (4 terms in a lane, an 8-lane DPP sum) go to
+            // sums of squares (two runs of 4 terms in a lane, their sum, a
+            // 4-lane DPP sum: the 8-lane sum of 4-term runs, pair by pair) go to
             // the idle phase buffer, every wave adds up each row's (a lane
             // run of at most 8, a 16-lane DPP sum, the 4 row sums: at most
             // 20 roundings a term) and norm_mean_from_bound decides the
@@ -246,19 +253,23 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             float inv_r[NORM ? 4 : 1];
             if constexpr (NORM) {
                 double* nsq = reinterpret_cast<double*>(fbuf);
-#pragma unroll
-                for (int p = 0; p < kQuantPasses; ++p) {
-                    if (p >= npass) break;
-                    const int blk = p * qb + (tid >> 3);
-                    const float x0 = __uint_as_float(av[p].x), x1 = __uint_as_float(av[p].y);
-                    const float x2 = __uint_as_float(av[p].z), x3 = __uint_as_float(av[p].w);
-                    double t = (double)x0 * (double)x0;
-                    t += (double)x1 * (double)x1;
-                    t += (double)x2 * (double)x2;
-                    t += (double)x3 * (double)x3;
-                    t = sum8_f64(t);
-                    if ((tid & 7) == 0 && blk < nb_rows) nsq[blk] = t;
-                }
+                auto sumsq = [&](int p, const Oct& v) {
+                    const int blk = p * qb + (tid >> 2);
+                    auto run4 = [](const uint4& u) {
+                        const float x0 = __uint_as_float(u.x), x1 = __uint_as_float(u.y);
+                        const float x2 = __uint_as_float(u.z), x3 = __uint_as_float(u.w);
+                        double t = (double)x0 * (double)x0;
+                        t += (double)x1 * (double)x1;
+                        t += (double)x2 * (double)x2;
+                        return t + (double)x3 * (double)x3;
+                    };
+                    double t = run4(v.x) + run4(v.y);
+                    t += dpp_f64(t, 0xB1);  // lane ^ 1
+                    t += dpp_f64(t, 0x4E);  // lane ^ 2
+                    if ((tid & 3) == 0 && blk < nb_rows) nsq[blk] = t;
+                };
+                if (npass > 0) sumsq(0, av0);
+                if (npass > 1) sumsq(1, av1);
                 lds_barrier();
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -277,50 +288,55 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     inv_r[r] = 1.0f / sqrtf(mean + a.norm_eps);
                 }
             }
-#pragma unroll
-            for (int p = 0; p < kQuantPasses; ++p) {
-                if (p >= npass) break;
-                const int blk = p * qb + (tid >> 3), e = tid & 7;
+            auto qpass = [&](int p, const Oct& v, const Oct& w) {
+                const int blk = p * qb + (tid >> 2), e = tid & 3;
                 float s;
                 int sum;
-                uint32_t p0, p1;
-                float4 xq = make_float4(__uint_as_float(av[p].x), __uint_as_float(av[p].y),
-                                        __uint_as_float(av[p].z), __uint_as_float(av[p].w));
+                uint2 ph, pl;
+                float4 x0 = make_float4(__uint_as_float(v.x.x), __uint_as_float(v.x.y), __uint_as_float(v.x.z),
+                                        __uint_as_float(v.x.w));
+                float4 x1 = make_float4(__uint_as_float(v.y.x), __uint_as_float(v.y.y), __uint_as_float(v.y.z),
+                                        __uint_as_float(v.y.w));
                 if constexpr (NORM) {
                     const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk);
                     const float inv = m == 0 ? inv_r[0] : m == 1 ? inv_r[1] : m == 2 ? inv_r[2] : inv_r[3];
-                    xq = make_float4(xq.x * inv * __uint_as_float(wn[p].x), xq.y * inv * __uint_as_float(wn[p].y),
-                                     xq.z * inv * __uint_as_float(wn[p].z), xq.w * inv * __uint_as_float(wn[p].w));
-                    if (a.normOut && g == 0 && blk < nb_rows)
-                        *reinterpret_cast<float4*>(a.normOut + (size_t)m0 * a.K + 32 * blk + 4 * e) = xq;
+                    auto nrm = [&](const float4& x, const uint4& w) {
+                        return make_float4(x.x * inv * __uint_as_float(w.x), x.y * inv * __uint_as_float(w.y),
+                                           x.z * inv * __uint_as_float(w.z), x.w * inv * __uint_as_float(w.w));
+                    };
+                    x0 = nrm(x0, w.x);
+                    x1 = nrm(x1, w.y);
+                    if (a.normOut && g == 0 && blk < nb_rows) {
+                        float* o = a.normOut + (size_t)m0 * a.K + 32 * blk + 8 * e;
+                        *reinterpret_cast<float4*>(o) = x0;
+                        *reinterpret_cast<float4*>(o + 4) = x1;
+                    }
                 }
-                quant8<HP>(xq, s, sum, p0, p1);
+                quant4x8<HP>(x0, x1, s, ph, pl, sum);
                 if (blk < nb_rows) {
                     const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk), j = blk - m * a.nblk;
                     if (P64) {
-                        // Lane e holds bytes 4(e&1).. of k-octet e>>1: the
-                        // slot's zero half, then the octet.
-                        uint32_t* sh = reinterpret_cast<uint32_t*>(recs + m * lay.rec_pitch + j * 128 +
-                                                                   (e >> 1) * 16) + (e & 1);
-                        sh[0] = 0u;
-                        sh[2] = p0;
-                        sh[16] = 0u;  // l octets, 64 B further
-                        sh[18] = p1;
+                        // Lane e holds k-octet e: its slot is the zero
+                        // half, then the octet.
+                        uint4* sh = reinterpret_cast<uint4*>(recs + m * lay.rec_pitch + j * 128 + e * 16);
+                        sh[0] = make_uint4(0u, 0u, ph.x, ph.y);
+                        sh[4] = make_uint4(0u, 0u, pl.x, pl.y);  // l octets, 64 B further
                     } else {
                         // [chunk][h, l][k-octet][block of the chunk] of 8
                         // bytes: a lane's A operands for a chunk are 8 JG
                         // contiguous bytes.
-                        uint8_t* rec = recs + m * lay.rec_pitch + (j / JG) * (JG * 64) + (e >> 1) * (JG * 8) +
-                                       (j % JG) * 8 + 4 * (e & 1);
-                        *reinterpret_cast<uint32_t*>(rec) = p0;
-                        *reinterpret_cast<uint32_t*>(rec + JG * 32) = p1;
+                        uint8_t* rec = recs + m * lay.rec_pitch + (j / JG) * (JG * 64) + e * (JG * 8) + (j % JG) * 8;
+                        *reinterpret_cast<uint2*>(rec) = ph;
+                        *reinterpret_cast<uint2*>(rec + JG * 32) = pl;
                     }
                     if (e == 0) {
                         sa_l[m * lay.sa_pitch + j] = s;
                         sq_l[m * lay.sa_pitch + j] = (EXTRA ? -1 : -8) * sum;
                     }
                 }
-            }
+            };
+            if (npass > 0) qpass(0, av0, wn0);
+            if (npass > 1) qpass(1, av1, wn1);
         } else {
             // Rows land at the padded LDS pitches.
             const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;

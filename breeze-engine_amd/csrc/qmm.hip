@@ -1008,7 +1008,7 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
     a.ntiles = h->N / 16;
 }
 
-constexpr int kFusedMaxBlocks = kQuantPasses * 128;  // row-blocks the prologue quantizes
+constexpr int kFusedMaxBlocks = kQuantPasses * 256;  // row-blocks the prologue quantizes
 constexpr int kNormFusedMaxBlocks = 3 * 128;  // with the RMSNorm in the prologue
 
 // LDS bytes of the decode kernel, or 0 if the activation records of a row

@@ -129,10 +129,11 @@ __device__ inline void quant8(float4 v, float& s_out, int& sum_out, uint32_t& p0
 // The same quantization with 4 lanes a block, 8 consecutive k per lane (lane
 // q of the quad holds k = 8q..8q+7), for the prefill records: the block
 // scale in every lane of the quad, and this lane's 8 bytes of record part 0
-// (ph) and part 1 (pl).  Every step is quant8's, element for element, so
-// the results are the same bits.  All 64 lanes of the wave must call it.
+// (ph) and part 1 (pl), and sum(q) over the block in every lane of the quad.
+// Every step is quant8's, element for element, so the results are the same
+// bits.  All 64 lanes of the wave must call it.
 template <bool HP>
-__device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, uint2& pl) {
+__device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, uint2& pl, int& sum_out) {
     const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     float ab[8];
 #pragma unroll
@@ -147,6 +148,7 @@ __device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, u
     const float s = amax / (float)qmax;
     const float inv = s > 0.0f ? 1.0f / s : 0.0f;
     uint32_t w0[2] = {0u, 0u}, w1[2] = {0u, 0u};
+    int sum = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const float prod = x[i] * inv;
@@ -155,6 +157,7 @@ __device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, u
             q = (int)rintf(prod);
             q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
         }
+        sum += q;
         if (HP) {
             const uint32_t u = (uint32_t)(q + 32768);
             w0[i >> 2] |= (((u >> 8) ^ 0x80u) & 0xFFu) << (8 * (i & 3));
@@ -166,6 +169,13 @@ __device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, u
     s_out = s;
     ph = make_uint2(w0[0], w0[1]);
     pl = make_uint2(w1[0], w1[1]);
+    sum += dpp_xor1(sum);
+    sum_out = sum + dpp_xor2(sum);
+}
+template <bool HP>
+__device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, uint2& pl) {
+    int sum;
+    quant4x8<HP>(v0, v1, s_out, ph, pl, sum);
 }
 
 __device__ inline uint64_t unpack_b(const uint4& w, int jb, int bits) {
@@ -230,12 +240,12 @@ __device__ inline v4i mfma64(const uint4& a, const uint4& b) {
 constexpr int kDecWaves = 16;
 constexpr int kChainWave = kDecWaves - 1;
 constexpr int kProducers = kDecWaves - 1;
-// The quantizing prologue (8 lanes per 32-block) runs on the first eight
-// waves when two passes of 64 blocks cover the activations: the last waves
-// of a workgroup start up to ~0.3 us after the first, and the prologue
+// The quantizing prologue (4 lanes per 32-block, quant4x8) runs on the first
+// eight waves when one pass of 128 blocks covers the activations: the last
+// waves of a workgroup start up to ~0.3 us after the first, and the prologue
 // barrier waits for the slowest quantizer.  More blocks take all sixteen
-// waves (at most kQuantPasses passes of 128).
-constexpr int kQuantEarlyBlocks = 128, kQuantPasses = 4;
+// waves (at most kQuantPasses passes of 256).
+constexpr int kQuantEarlyBlocks = 128, kQuantPasses = 2;
 
 struct GemvArgs {
     const uint4* W;
@@ -287,6 +297,11 @@ constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3;
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
 // (explicit zero points, legacy corr, scale groups smaller than a chunk)
 // carry materialized per-block arrays so every load is unconditional.
+// Eight consecutive activation floats of one lane (k = 8q..8q+7 of a block).
+struct Oct {
+    uint4 x, y;
+};
+
 template <int JG, bool EXTRA>
 struct Unit {
     uint4 w;
