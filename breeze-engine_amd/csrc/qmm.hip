@@ -121,26 +121,31 @@ __global__ void repack_kernel(const uint8_t* __restrict__ raw, uint4* __restrict
 
 // ------------------------------------------------------------------ quantize
 
-// Stand-alone activation quantizer: 8 lanes per (row, block).  Records go
+// Stand-alone activation quantizer: 4 lanes per (row, block), 8 k each
+// (quant4x8).  Records go
 // to Aq [M][nblk][64 B]; scale and sum(q) to Sa/Sq [M][nblk4].
 template <bool HP>
 __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ A, int M, int K,
                                                        int nblk, int nblk4, uint8_t* __restrict__ Aq,
                                                        float* __restrict__ Sa, int* __restrict__ Sq) {
     const int gtid = blockIdx.x * 256 + threadIdx.x;
-    const int blk = gtid >> 3, e = gtid & 7;
+    const int blk = gtid >> 2, e = gtid & 3;
     const bool valid = blk < M * nblk;
     const int m = valid ? blk / nblk : 0, j = valid ? blk - m * nblk : 0;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (valid) v = *reinterpret_cast<const float4*>(A + (size_t)m * K + 32 * j + 4 * e);
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (valid) {
+        const float* x = A + (size_t)m * K + 32 * j + 8 * e;
+        v0 = *reinterpret_cast<const float4*>(x);
+        v1 = *reinterpret_cast<const float4*>(x + 4);
+    }
     float s;
     int sum;
-    uint32_t p0, p1;
-    quant8<HP>(v, s, sum, p0, p1);
+    uint2 ph, pl;
+    quant4x8<HP>(v0, v1, s, ph, pl, sum);
     if (valid) {
         uint8_t* rec = Aq + ((size_t)m * nblk + j) * 64;
-        *reinterpret_cast<uint32_t*>(rec + 4 * e) = p0;
-        *reinterpret_cast<uint32_t*>(rec + 32 + 4 * e) = p1;
+        *reinterpret_cast<uint2*>(rec + 8 * e) = ph;
+        *reinterpret_cast<uint2*>(rec + 32 + 8 * e) = pl;
         if (e == 0) {
             Sa[(size_t)m * nblk4 + j] = s;
             Sq[(size_t)m * nblk4 + j] = sum;
@@ -251,7 +256,7 @@ __global__ __launch_bounds__(kRowWaves * 64) void rows_kernel(GemvArgs a) {
     if (!DOTS && cm < Mc) a.C[(size_t)(m0 + cm) * a.N + t * 16 + ccol] = acc;
 }
 
-// Activation records for the prefill GEMM: 8 lanes per (row, block) over
+// Activation records for the prefill GEMM: 4 lanes per (row, block) over
 // Mpad rows and 2*nch blocks; padding rows and blocks quantize zeros.
 template <bool HP>
 __global__ __launch_bounds__(256) void quantize_rec_kernel(const float* __restrict__ A, int M, int K, int nblk,
@@ -1159,9 +1164,9 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     if ((h2 || mp) && !dec) return kNotPairable;
     if (mp && (h->extra || dIdx)) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
-    // The norm in the prologue pays for itself up to three passes (M = 3 at
-    // K = 5120, 480 row-blocks: 19.0 us against 17.4 us for the norm kernel
-    // then the projections; M = 2, 320 row-blocks: even).
+    // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
+    // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the
+    // norm kernel then the projections; M = 2, 320 row-blocks: even).
     if (mp && mp->norm && !(fused && Mr_max * h->nblk <= kNormFusedMaxBlocks)) return kNotPairable;
     // Prefill GEMM: more than 8 rows without a legacy corr.
     const bool pre = !dec && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
@@ -1180,7 +1185,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
     } else if (!fused) {
         if (!ensure_quant(w, s, st, M, h->nblk4)) return -4;
-        const size_t threads = (size_t)M * h->nblk * 8;
+        const size_t threads = (size_t)M * h->nblk * 4;
         const unsigned qb = (unsigned)((threads + 255) / 256);
         if (hp) quantize_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, s.aq, s.sa, s.sq);
         else quantize_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk4, s.aq, s.sa, s.sq);

@@ -66,75 +66,20 @@ __host__ __device__ inline size_t blk_index(int n, int j, int nbg, int JG) {
 
 __device__ inline int dpp_xor1(int v) { return __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); }
 __device__ inline int dpp_xor2(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); }
-__device__ inline int dpp_mirror8(int v) { return __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false); }
 
-// max over the 8 lanes of an aligned lane octet.  Inputs are +0 or more and
-// never NaN, so their bit patterns order as the floats do.
-__device__ inline float max8(float xf) {
-    int x = __float_as_int(xf);
-    x = max(x, dpp_xor1(x));
-    x = max(x, dpp_xor2(x));
-    return __int_as_float(max(x, dpp_mirror8(x)));
-}
-
-__device__ inline int sum8(int x) {
-    x += dpp_xor1(x);
-    x += dpp_xor2(x);
-    return x + dpp_mirror8(x);
-}
-
-// Quantizes one 32-block with 8 lanes, 4 consecutive k per lane (lane e of
-// the octet holds k = 4e..4e+3).  All 64 lanes of the wave must call it.
-// Returns the block scale and sum(q) in every lane of the octet, and this
-// lane's 4 bytes of record part 0 and part 1.
+// Quantizes one 32-block (quantize_A / quantize_A_i16 of one block,
+// kernel/quantized_matmul.cpp:215-258) with 4 lanes, 8 consecutive k per
+// lane (lane q of the quad holds k = 8q..8q+7).  Returns the block scale
+// and sum(q) in every lane of the quad, and this lane's 8 bytes of record
+// part 0 (ph: the INT8 values, or the high bytes in the two-pass mode) and
+// part 1 (pl: the low bytes).  All 64 lanes of the wave must call it.
 template <bool HP>
-__device__ inline void quant8(float4 v, float& s_out, int& sum_out, uint32_t& p0, uint32_t& p1) {
-    const float x[4] = {v.x, v.y, v.z, v.w};
+__device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, uint2& pl, int& sum_out) {
+    const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     // amax over the block from +0 with NaNs skipped, as the reference's
     // `a > amax ? a : amax` does.  fmaxf returns the other operand of a quiet
     // NaN; canonicalizing first makes every NaN quiet, and the +0 operand
     // keeps a lane whose values are all NaN at 0.
-    const float a0 = fabsf(__builtin_canonicalizef(x[0])), a1 = fabsf(__builtin_canonicalizef(x[1]));
-    const float a2 = fabsf(__builtin_canonicalizef(x[2])), a3 = fabsf(__builtin_canonicalizef(x[3]));
-    float amax = fmaxf(fmaxf(fmaxf(a0, a1), 0.0f), fmaxf(a2, a3));
-    amax = max8(amax);
-    constexpr int qmax = HP ? 32767 : 127;
-    const float s = amax / (float)qmax;
-    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-    int sum = 0;
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float prod = x[i] * inv;
-        int q = 0;
-        if (__builtin_isfinite(prod)) {
-            q = (int)rintf(prod);
-            q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
-        }
-        sum += q;
-        if (HP) {
-            const uint32_t u = (uint32_t)(q + 32768);
-            w0 |= (((u >> 8) ^ 0x80u) & 0xFFu) << (8 * i);
-            w1 |= (((u & 0xFFu) ^ 0x80u) & 0xFFu) << (8 * i);
-        } else {
-            w0 |= ((uint32_t)q & 0xFFu) << (8 * i);
-        }
-    }
-    s_out = s;
-    sum_out = sum8(sum);
-    p0 = w0;
-    p1 = w1;
-}
-
-// The same quantization with 4 lanes a block, 8 consecutive k per lane (lane
-// q of the quad holds k = 8q..8q+7), for the prefill records: the block
-// scale in every lane of the quad, and this lane's 8 bytes of record part 0
-// (ph) and part 1 (pl), and sum(q) over the block in every lane of the quad.
-// Every step is quant8's, element for element, so the results are the same
-// bits.  All 64 lanes of the wave must call it.
-template <bool HP>
-__device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, uint2& pl, int& sum_out) {
-    const float x[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
     float ab[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) ab[i] = fabsf(__builtin_canonicalizef(x[i]));

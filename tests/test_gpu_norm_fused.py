@@ -3,8 +3,8 @@
 hn = rmsnorm(x, w, eps) (kernel/qwen35_decoder.cpp:134-140) and each
 projection of hn.  The Qwen3.5-27B in_qkv/in_z/in_b/in_a shapes (K = 5120)
 at one and two rows take the fused launch, three, four and eight rows the
-norm-then-projections fallback (past 384 row-blocks, three prologue
-passes, the norm runs as its own launch); rows from the RMSNorm parity set
+norm-then-projections fallback (past 384 row-blocks the norm runs as its
+own launch); rows from the RMSNorm parity set
 (ties, vanishing terms, outliers, denormals, a mean on a float rounding
 midpoint that the bound leaves to the in-order sum) at K = 4096 one at a
 time, and all together at K = 3072 (row groups of 4 x 96 blocks, fused);
