@@ -1,0 +1,332 @@
+// dec8_kernel.h -- the decode GEMV for five to eight rows: one workgroup per
+// tile range serves all eight rows, so every weight chunk crosses from L2 to
+// a CU once.  Instantiated per (bits, activation mode) by dec_w{4,8}_{hp,lp}.hip.
+#pragma once
+
+#include "qmm_common.h"
+
+namespace bq {
+
+// Waves 0..13 produce, waves 14 and 15 fold (one activation row of each
+// output lane's pair each).  A tile's K range is cut into phases of 14
+// chunks; producer w takes chunk 14p + w of phase p.
+//
+// MFMA A operand (v_mfma_i32_16x16x32_i8): row 2m + s is record part s of
+// activation row m (the h and l bytes of the two-pass mode; the INT8 values
+// and zeros with INT8 activations), so output lane (col, grp) holds the
+// part-0 and part-1 dots of rows 2 grp and 2 grp + 1.  The records come
+// through the producer's register ring from a buffer the stand-alone
+// quantizer writes in that operand order ([chunk][JG / 2][64 lanes][16 B]),
+// not through LDS: eight rows of K = 12288 are 192 KB.  The bias term
+// 128 * sum(b) of the two-pass product, which the four-row kernel takes from
+// two constant A rows, is summed in the lane: udot8 of the lane's nibbles
+// (INT4) or udot4 of its raw bytes (INT8), then over the chunk's four
+// k-octet lane groups with permlane swaps, two blocks to a dword.
+constexpr int kP8 = 14;
+constexpr int kRows8 = 8;
+
+// LDS: block scales and (INT4) -zp * sum(q) of the eight rows, row pitch
+// padded 16 B past a multiple of 256 B (the four rows a fold or epilogue
+// reads together fall on different banks), then the phase buffer
+// [2 buffers][2 rows][64 lanes][dec_pitch(JG)] of f values.
+struct Dec8Lds {
+    int sa_pitch;         // elements per row
+    int sa, sq, fbuf, total;  // byte offsets, bytes used
+};
+__host__ __device__ inline Dec8Lds dec8_lds(int nblk, int JG) {
+    Dec8Lds l;
+    l.sa_pitch = ((nblk + 3) / 4 * 4 + 59) / 64 * 64 + 4;
+    int off = 0;
+    l.sa = lds_take(off, kRows8 * l.sa_pitch * 4);
+    l.sq = lds_take(off, kRows8 * l.sa_pitch * 4);
+    l.fbuf = lds_take(off, 2 * 2 * 64 * dec_pitch(JG) * 4);
+    l.total = off;
+    return l;
+}
+
+// Per-lane record bytes of one chunk: JG blocks of 8 bytes.
+template <int JG>
+struct Unit8 {
+    uint4 w;
+    uint4 a[JG / 2];
+    float sc;
+    int c;  // chunk to compute; nbg or more: none (past the end)
+};
+
+// Sum over the four k-octet lane groups (lanes col + 16 q) of a dword of two
+// 16-bit partial sums; every lane of a column receives it.
+__device__ inline uint32_t octet_sum2(uint32_t p) {
+    const auto s32 = __builtin_amdgcn_permlane32_swap(p, p, false, false);
+    const uint32_t y = s32[0] + s32[1];
+    const auto s16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
+    return s16[0] + s16[1];
+}
+
+// Leading arguments in SGPRs at wave launch (kernarg preload), as in
+// dec_kernel.  misc = sc_shift | phases per tile << 16.  Tiles: the first
+// rem_t workgroups own base_t + 1, the rest base_t.
+template <int BITS, bool HP>
+__global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, const float* pS, const uint4* pR,
+                                                              int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
+                                                              int pngrp, int misc, GemvArgs args) {
+    constexpr int JG = BITS == 8 ? 2 : 4;
+    constexpr int NA = JG / 2;
+    constexpr int PP = dec_pitch(JG);
+    constexpr int R = kDecRing;
+    typedef float fvec __attribute__((ext_vector_type(JG)));
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nblk = pnblk, M = pM, nbg = pnbg;
+    const int nblk4 = (nblk + 3) / 4 * 4;
+    const int sc_shift = misc & 31, npw = misc >> 16;
+
+    // Block scales and sums of q first (at most two uint4 per thread per
+    // array: M * nblk4 <= 8192).
+    const int nmeta = M * nblk4 / 4;
+    const uint4* gsa = reinterpret_cast<const uint4*>(args.Sa);
+    const uint4* gsq = reinterpret_cast<const uint4*>(args.Sq);
+    const int mi0 = min(tid, nmeta - 1), mi1 = min(tid + 1024, nmeta - 1);
+    const bool two_meta = nmeta > 1024;
+    uint4 ma0 = gsa[mi0], ma1 = ma0, mq0 = make_uint4(0u, 0u, 0u, 0u), mq1 = mq0;
+    if (two_meta) ma1 = gsa[mi1];
+    if (BITS == 4) {
+        mq0 = gsq[mi0];
+        if (two_meta) mq1 = gsq[mi1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    const int g = blockIdx.x;
+    const int t_begin = g * pbase_t + min(g, prem_t);
+    const int nT = pbase_t + (g < prem_t ? 1 : 0);
+    const int U = nT * npw;  // phases of this workgroup
+
+    const Dec8Lds lay = dec8_lds(nblk, JG);
+    float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
+    int* sq_l = reinterpret_cast<int*>(smem + lay.sq);
+    float* fbuf = reinterpret_cast<float*>(smem + lay.fbuf);  // [2][2][64][PP]
+    const int col = lane & 15, grp = lane >> 4;
+
+    // Rows land at the padded pitch; sums of q premultiplied by -8 (the
+    // default zero point).  Threads past the end rewrite the last element.
+    auto store_meta = [&]() {
+        const int pad = (lay.sa_pitch - nblk4) >> 2;
+        auto put = [&](int i, const uint4& va, const uint4& vq) {
+            const int e = 4 * i;
+            int m = 0;
+#pragma unroll
+            for (int r = 1; r < kRows8; ++r) m += e >= r * nblk4;
+            const int d = i + m * pad;
+            reinterpret_cast<uint4*>(sa_l)[d] = va;
+            if (BITS == 4) {
+                const uint32_t f = 0xFFFFFFF8u;  // -8
+                reinterpret_cast<uint4*>(sq_l)[d] = make_uint4(f * vq.x, f * vq.y, f * vq.z, f * vq.w);
+            }
+        };
+        put(mi0, ma0, mq0);
+        if (two_meta) put(mi1, ma1, mq1);
+    };
+
+    // Load cursor (as in dec_kernel): chunk ld_c of local tile ld_t, ld_rem
+    // units before the tile ends; past the end ld_c is out of range and the
+    // loads re-read the last tile.  A load with no work in a tile's short
+    // last phase reads the chunk this producer loads in the next tile (L2
+    // warm-up), or on the last tile the tile's last chunk.
+    int ld_c = wave, ld_rem = npw, ld_t = 0;
+    uint32_t ld_w = (uint32_t)t_begin * nbg * 64;
+    uint32_t ld_s = (uint32_t)t_begin * pngrp * 16;
+    const int pf_c = nbg + kP8 + wave;
+    const bool pf = npw >= 2 && wave + kP8 < nbg;
+    int ld_idle = (pf && nT > 1) ? pf_c : nbg - 1;
+    auto load_unit = [&](Unit8<JG>& p) {
+        const int c = min(ld_c, nbg - 1);
+        const int cw = ld_c < nbg ? ld_c : ld_idle;
+        uint32_t wi = ld_w + cw * 64 + lane;
+        uint32_t si = ld_s + (uint32_t)((c * JG) >> sc_shift) * 16 + col;
+        uint32_t ri = (uint32_t)c * (NA * 64) + lane;
+        asm("" : "+v"(wi), "+v"(si), "+v"(ri));
+        p.w = pW[wi];
+#pragma unroll
+        for (int h = 0; h < NA; ++h) p.a[h] = pR[ri + 64 * h];
+        p.sc = pS[si];
+        p.c = ld_c;
+        ld_c += kP8;
+        if (--ld_rem == 0) {
+            ld_rem = npw;
+            if (++ld_t < nT) {
+                ld_c = wave;
+                ld_w += nbg * 64;
+                ld_s += pngrp * 16;
+                if (ld_t + 1 == nT) ld_idle = nbg - 1;
+            } else {
+                ld_c = 1 << 24;
+            }
+        }
+    };
+
+    if (wave >= kP8) {
+        // ================= chain waves: wave 14 folds row 2 grp, wave 15
+        // row 2 grp + 1 of each lane's pair.  The fold is one dependent FMA
+        // chain per output and paces the phases: first pick of the SIMD's
+        // issue slots.
+        __builtin_amdgcn_s_setprio(3);
+        store_meta();
+        lds_barrier();
+        const int r = wave - kP8, row = 2 * grp + r;
+        const float* sa_row = sa_l + row * lay.sa_pitch;
+        const bool tail_pad = nblk != nbg * JG;  // the last chunk has padding blocks
+        float acc = 0.0f;
+        int pr_t = 0, pr_p = 0;
+        for (int u = 0; u < U; ++u) {
+            lds_barrier();
+            const float* fp = fbuf + (((u & 1) * 2 + r) * 64 + lane) * PP;
+            const int c0 = kP8 * pr_p;
+            const float* sp = sa_row + c0 * JG;
+            if (c0 + kP8 < nbg || (c0 + kP8 == nbg && !tail_pad)) {
+                // Full phase: all reads, then the FMAs in block order.
+                fvec fv[kP8], sv[kP8];
+#pragma unroll
+                for (int i = 0; i < kP8; ++i) {
+                    fv[i] = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    sv[i] = *reinterpret_cast<const fvec*>(sp + i * JG);
+                }
+#pragma unroll
+                for (int i = 0; i < kP8; ++i) {
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[i][jb], fv[i][jb], acc);
+                }
+            } else {
+                // The tile's last phase: whole chunks two at a time, then
+                // the blocks of a padded last chunk.
+                const int nb = nblk - c0 * JG, nwc = nb / JG;
+                int i = 0;
+                for (; i + 2 <= nwc; i += 2) {
+                    const fvec f0 = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    const fvec s0 = *reinterpret_cast<const fvec*>(sp + i * JG);
+                    const fvec f1 = *reinterpret_cast<const fvec*>(fp + (i + 1) * JG);
+                    const fvec s1 = *reinterpret_cast<const fvec*>(sp + (i + 1) * JG);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s0[jb], f0[jb], acc);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s1[jb], f1[jb], acc);
+                }
+                if (i < nwc) {
+                    const fvec f0 = *reinterpret_cast<const fvec*>(fp + i * JG);
+                    const fvec s0 = *reinterpret_cast<const fvec*>(sp + i * JG);
+#pragma unroll
+                    for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(s0[jb], f0[jb], acc);
+                    ++i;
+                }
+                for (int b = i * JG; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
+            }
+            if (++pr_p == npw) {
+                if (row < M) args.C[(size_t)row * args.N + (t_begin + pr_t) * 16 + col] = acc;
+                ++pr_t;
+                acc = 0.0f;
+                pr_p = 0;
+            }
+        }
+        return;
+    }
+
+    // ================= producers (waves 0..13)
+    Unit8<JG> ring[R];
+#pragma unroll
+    for (int d = 0; d < R; ++d) load_unit(ring[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    store_meta();
+    lds_barrier();
+
+    const int* sq0 = sq_l + (2 * grp) * lay.sa_pitch;
+    const int* sq1 = sq0 + lay.sa_pitch;
+    float* const fout = fbuf + lane * PP + wave * JG;
+
+    auto consume = [&](const Unit8<JG>& cur, int buf) {
+        const int c = cur.c;
+        if (c >= nbg) return;
+        // -zp * sum(q) of rows 2 grp and 2 grp + 1 (INT4).
+        int4 z0 = make_int4(0, 0, 0, 0), z1 = z0;
+        if (BITS == 4) {
+            z0 = *reinterpret_cast<const int4*>(sq0 + c * 4);
+            z1 = *reinterpret_cast<const int4*>(sq1 + c * 4);
+        }
+        // 128 * sum(b) of this lane's column for each block of the chunk.
+        int sb[JG];
+        if constexpr (HP) {
+            if constexpr (BITS == 4) {
+                const uint32_t wv[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
+                uint32_t n[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) n[b] = __builtin_amdgcn_udot8(wv[b], 0x11111111u, 0u, false);  // <= 120
+                const uint32_t p0 = octet_sum2(n[0] | n[1] << 16), p1 = octet_sum2(n[2] | n[3] << 16);
+                sb[0] = (int)(p0 & 0xFFFFu) << 7;
+                sb[1] = (int)(p0 >> 16) << 7;
+                sb[2] = (int)(p1 & 0xFFFFu) << 7;
+                sb[3] = (int)(p1 >> 16) << 7;
+            } else {
+                // Raw bytes b + 128 in [0, 255]: a lane's eight sum to
+                // sum(b) + 1024 in [0, 2040], the four octets to sum(b) + 4096.
+                const uint32_t ones = 0x01010101u, fl = 0x80808080u;
+                const uint32_t s0 = __builtin_amdgcn_udot4(cur.w.x ^ fl, ones,
+                                                           __builtin_amdgcn_udot4(cur.w.y ^ fl, ones, 0u, false), false);
+                const uint32_t s1 = __builtin_amdgcn_udot4(cur.w.z ^ fl, ones,
+                                                           __builtin_amdgcn_udot4(cur.w.w ^ fl, ones, 0u, false), false);
+                const uint32_t p = octet_sum2(s0 | s1 << 16);
+                sb[0] = ((int)(p & 0xFFFFu) - 4096) << 7;
+                sb[1] = ((int)(p >> 16) - 4096) << 7;
+            }
+        }
+        fvec f0, f1;
+#pragma unroll
+        for (int jb = 0; jb < JG; ++jb) {
+            // Blocks past nblk (last chunk) read padding; the chain never
+            // folds them.
+            const uint64_t bop = unpack_b(cur.w, jb, BITS);
+            const uint4& a2 = cur.a[jb >> 1];
+            const uint64_t aop = (jb & 1) ? ((uint64_t)a2.w << 32 | a2.z) : ((uint64_t)a2.y << 32 | a2.x);
+            const v4i dd = mfma16(aop, bop);
+            int cs0 = dd[0], cs1 = dd[2];
+            if constexpr (HP) {
+                cs0 = cs0 * 256 + dd[1] + sb[jb];
+                cs1 = cs1 * 256 + dd[3] + sb[jb];
+            }
+            if (BITS == 4) {
+                cs0 += jb == 0 ? z0.x : jb == 1 ? z0.y : jb == 2 ? z0.z : z0.w;
+                cs1 += jb == 0 ? z1.x : jb == 1 ? z1.y : jb == 2 ? z1.z : z1.w;
+            }
+            f0[jb] = (float)cs0 * cur.sc;
+            f1[jb] = (float)cs1 * cur.sc;
+        }
+        *reinterpret_cast<fvec*>(fout + (buf * 2) * 64 * PP) = f0;
+        *reinterpret_cast<fvec*>(fout + (buf * 2 + 1) * 64 * PP) = f1;
+    };
+
+    for (int u0 = 0; u0 < U; u0 += R) {
+#pragma unroll
+        for (int d = 0; d < R; ++d) {
+            const bool live = u0 + d < U;  // uniform over the workgroup
+            consume(ring[d], (u0 + d) & 1);
+            load_unit(ring[d]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (live) lds_barrier();
+        }
+    }
+}
+
+template <int BITS, bool HP>
+hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, hipStream_t st) {
+    auto kern = dec8_kernel<BITS, HP>;
+    if (!*attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
+        if (e != hipSuccess) return e;
+        *attr_set = true;
+    }
+    const int npw = (a.nbg + kP8 - 1) / kP8;
+    const int misc = a.sc_shift | npw << 16;
+    const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
+    kern<<<grid, kDecWaves * 64, lds, st>>>(a.W, a.S, rec, base_t, a.nblk, a.M, a.nbg, rem_t, a.ngrp, misc, a);
+    return hipGetLastError();
+}
+
+}  // namespace bq

@@ -42,6 +42,7 @@
 
 #include "../../include/breeze_qmm.h"
 #include "qmm_common.h"
+#include "dec8_kernel.h"
 
 using namespace bq;
 
@@ -147,6 +148,44 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
         *reinterpret_cast<uint2*>(rec + 8 * e) = ph;
         *reinterpret_cast<uint2*>(rec + 32 + 8 * e) = pl;
         if (e == 0) {
+            Sa[(size_t)m * nblk4 + j] = s;
+            Sq[(size_t)m * nblk4 + j] = sum;
+        }
+    }
+}
+
+// The same quantizer for the five-to-eight-row decode kernel: records in its
+// MFMA A-operand order, [chunk][JG / 2][64 lanes][16 B], lane 16 e + 2 m + s
+// holding k-octet e of record part s of row m for blocks 2 h and 2 h + 1 of
+// the chunk (8 bytes each).  Rows M..7 and the padding blocks of the last
+// chunk are zeros.  Scales and sums of q as quantize_kernel's.  Threads:
+// 8 rows x nblk_pad blocks x 4.
+template <bool HP, int JG>
+__global__ __launch_bounds__(256) void quantize_r8_kernel(const float* __restrict__ A, int M, int K, int nblk,
+                                                          int nblk_pad, int nblk4, uint8_t* __restrict__ R,
+                                                          float* __restrict__ Sa, int* __restrict__ Sq) {
+    const int gtid = blockIdx.x * 256 + threadIdx.x;
+    const int blk = gtid >> 2, e = gtid & 3;
+    const bool in = blk < 8 * nblk_pad;
+    const int m = in ? blk / nblk_pad : 0, j = in ? blk - m * nblk_pad : 0;
+    const bool real = in && m < M && j < nblk;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (real) {
+        const float* x = A + (size_t)m * K + 32 * j + 8 * e;
+        v0 = *reinterpret_cast<const float4*>(x);
+        v1 = *reinterpret_cast<const float4*>(x + 4);
+    }
+    float s;
+    int sum;
+    uint2 ph, pl;
+    quant4x8<HP>(v0, v1, s, ph, pl, sum);
+    if (in) {
+        if (!real) ph = pl = make_uint2(0u, 0u);
+        const int c = j / JG, jb = j - c * JG;
+        uint8_t* base = R + ((size_t)(c * (JG / 2) + (jb >> 1)) * 64) * 16 + (jb & 1) * 8;
+        *reinterpret_cast<uint2*>(base + (16 * e + 2 * m) * 16) = ph;
+        *reinterpret_cast<uint2*>(base + (16 * e + 2 * m + 1) * 16) = pl;
+        if (real && e == 0) {
             Sa[(size_t)m * nblk4 + j] = s;
             Sq[(size_t)m * nblk4 + j] = sum;
         }
@@ -743,6 +782,7 @@ struct Workspace {
     hipStream_t stream = nullptr;
     int n_cu = 0;
     bool attr_set[256] = {};  // decode kernel variants with the kernel attribute set
+    bool dec8_attr[4] = {};   // the same for the five-to-eight-row decode kernel, per (bits, mode)
     bool pf_attr[256] = {};
 };
 
@@ -1063,6 +1103,18 @@ int device_cus(Workspace& w, int dev) {
     return w.n_cu;
 }
 
+// Whether the five-to-eight-row decode kernel takes a call: a plain call
+// (no block-integer export, gate/up pair, multi-projection or argmax) of a
+// handle without per-block metadata, with its eight rows' block scales and
+// sums within two uint4 per thread and its LDS plan within the limit.
+bool dec8_takes(const Handle* h, int M, bool dots, bool pair, bool multi, bool argmax) {
+    if (M < 5 || M > kRows8 || dots || pair || multi || argmax || h->extra) return false;
+    const char* f = std::getenv("BREEZE_HIP_DEC8");
+    if (f && f[0] == '0') return false;
+    if ((size_t)kRows8 * h->nblk4 / 4 > 2 * (size_t)kDecWaves * 64) return false;
+    return dec8_lds(h->nblk, h->bits == 8 ? 2 : 4).total <= kLdsMax;
+}
+
 // Quantize + block dots + epilogue for M rows on `st`.  Exactly one of
 // dC / dCs is non-null; dIdx (optional) receives the per-row argmax.
 constexpr int kNotPairable = -100;  // run() with h2: the decode kernel does not take this call
@@ -1164,6 +1216,15 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     if ((h2 || mp) && !dec) return kNotPairable;
     if (mp && (h->extra || dIdx)) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
+    // Five to eight rows of a plain call whose row groups would copy staged
+    // records: one workgroup per tile range for all eight rows
+    // (dec8_kernel), when its scale and sum rows fit (two uint4 per thread).
+    // Both take the stand-alone quantizer; where the row groups quantize in
+    // their prologue (K <= 4096 at four rows a group) they keep the call,
+    // which saves that launch (~2.5 us): W8 K=4096 N=4096 at 8 rows 9.7 us
+    // against 12.2 us.  BREEZE_HIP_DEC8=0 keeps every call on the row
+    // groups.
+    const bool dec8 = dec && !fused && dec8_takes(h, M, dots, h2 != nullptr, mp != nullptr, dIdx != nullptr);
     // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
     // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the
     // norm kernel then the projections; M = 2, 320 row-blocks: even).
@@ -1183,6 +1244,23 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);
         else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
+    } else if (dec8) {
+        if (!ensure_quant(w, s, st, kRows8, h->nblk4)) return -4;
+        const size_t threads = (size_t)kRows8 * h->nblk_pad * 4;
+        const unsigned qb = (unsigned)((threads + 255) / 256);
+        const int JGq = h->bits == 8 ? 2 : 4;
+        if (hp && JGq == 4)
+            quantize_r8_kernel<true, 4><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+        else if (hp)
+            quantize_r8_kernel<true, 2><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+        else if (JGq == 4)
+            quantize_r8_kernel<false, 4><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+        else
+            quantize_r8_kernel<false, 2><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+        if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
+        a.Aq = s.aq;
+        a.Sa = s.sa;
+        a.Sq = s.sq;
     } else if (!fused) {
         if (!ensure_quant(w, s, st, M, h->nblk4)) return -4;
         const size_t threads = (size_t)M * h->nblk * 4;
@@ -1196,7 +1274,18 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     }
 
     hipError_t e;
-    if (dec) {
+    if (dec8) {
+        a.NG = std::min(a.ntiles, device_cus(w, dev));
+        a.RG = 1;
+        a.RS = kRows8;
+        const int lds8 = dec8_lds(h->nblk, JG).total;
+        const uint4* rec = reinterpret_cast<const uint4*>(s.aq);
+        bool* at = &w.dec8_attr[(h->bits == 8 ? 1 : 0) | (hp ? 2 : 0)];
+        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, a.NG, lds8, st)
+                                 : launch_dec8<8, false>(at, a, rec, a.NG, lds8, st);
+        else e = hp ? launch_dec8<4, true>(at, a, rec, a.NG, lds8, st)
+                    : launch_dec8<4, false>(at, a, rec, a.NG, lds8, st);
+    } else if (dec) {
         if (mp) {
             int t = 0;
             for (int k = 0; k < kMaxSeg; ++k) {
@@ -1687,7 +1776,7 @@ int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64
     s.rec_cap = region;
     // Stand-alone quantizer records for this call's rows: [M][nblk4] of 64 B
     // records, then the scales and sums.
-    const size_t nq = (size_t)M * h->nblk4;
+    const size_t nq = (size_t)(M >= 5 && M <= kRows8 ? kRows8 : M) * h->nblk4;
     if (nq * 72 <= region) {
         s.aq = recs;
         s.sa = reinterpret_cast<float*>(recs + nq * 64);

@@ -1,0 +1,94 @@
+"""The five-to-eight-row decode kernel (one workgroup per tile range for all
+eight rows, records through the register ring, the two-pass bias term
+128 * sum(b) summed in the lane) against the oracle, bit for bit, and against
+the row-group kernel it replaces for those rows (BREEZE_HIP_DEC8=0).
+
+Shapes cover a padded last chunk (nblk not a multiple of the chunk's
+blocks), a tile's K in exactly one phase and in a short last phase, several
+tiles per workgroup (more tiles than CUs, so the idle loads of a short last
+phase warm the next tile), per-column and grouped scales, INT4 and INT8
+weights, both activation modes, and weight bytes at the ends of their ranges
+(every column of a tile at -128 / +127, or nibbles at 0 / 15), which put the
+bias sums at their extremes.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from conftest import bits_equal, rng_weights
+
+pytestmark = pytest.mark.gpu
+
+# (K, N), all with more than 128 blocks (fewer go to the row-group kernel,
+# which quantizes in its prologue): a padded last chunk at both chunk sizes
+# (145 blocks); phases that are all full (168 blocks: 42 INT4 or 84 INT8
+# chunks, a multiple of 14) on one tile and on three; the C3 shape; more
+# tiles than CUs (544 tiles); a long K (the eight rows' scale rows past one
+# uint4 per thread).
+SHAPES = [(4640, 272), (5376, 16), (5376, 48), (12288, 4096), (5120, 8704), (24576, 64)]
+
+
+def _run(hb, torch, h, A, N):
+    c = hb.matmul(h, torch.from_numpy(A).cuda(), N)
+    torch.cuda.synchronize()
+    return c.cpu().numpy()
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("hp", [True, False])
+def test_dec8_bit_exact(gpu, hb, orc, hi_prec, K, N, bits, hp):
+    rng = np.random.default_rng(K * 7 + N + bits + (100 if hp else 0))
+    nblk = K // 32
+    qw, sc, _ = rng_weights(rng, N, K, bits)
+    if K >= 4096 and bits == 4:
+        sc = np.ascontiguousarray(np.repeat(sc[:, ::4], 4, axis=1)[:, :nblk])  # group 128
+    else:
+        sc = np.ascontiguousarray(np.repeat(sc[:, :1], nblk, axis=1))  # per column
+    # Extreme weight bytes in the first tile: bias sums at both ends.
+    if bits == 8:
+        qw[0:8] = 0      # raw 0 -> b = -128
+        qw[8:16] = 255   # b = +127
+    else:
+        qw[0:8] = 0x00
+        qw[8:16] = 0xFF
+    A8 = rng.normal(size=(8, K)).astype(np.float32)
+    A8[rng.random(A8.shape) < 0.01] *= 20.0
+    hb.set_hi_prec(hp)
+    h = hb.prepack(qw, sc, None, K, N, bits=bits)
+    try:
+        for M in (5, 6, 7, 8):
+            if K * N > 4096 * 4096 and M in (6, 7):
+                continue  # the large shapes at 5 and 8 rows only
+            A = np.ascontiguousarray(A8[:M])
+            case = dict(K=K, N=N, bits=bits, hp=hp, M=M)
+            print(f"dec8 {case}", flush=True)
+            want = orc.matmul(qw, sc, None, N, K, bits, A, hp)
+            got = _run(hb, gpu, h, A, N)
+            assert bits_equal(got, want), case
+            os.environ["BREEZE_HIP_DEC8"] = "0"
+            try:
+                old = _run(hb, gpu, h, A, N)
+            finally:
+                del os.environ["BREEZE_HIP_DEC8"]
+            assert bits_equal(old, want), case
+    finally:
+        hb.free(h)
+
+
+def test_dec8_then_fewer_rows(gpu, hb, orc, hi_prec):
+    """Eight rows, then five: rows past M in the shared record buffer are
+    rewritten as zeros, so the second call's results do not see the first's."""
+    rng = np.random.default_rng(77)
+    K, N = 4096, 512
+    qw, sc, _ = rng_weights(rng, N, K, 4)
+    hb.set_hi_prec(True)
+    h = hb.prepack(qw, sc, None, K, N, bits=4)
+    try:
+        for M in (8, 5, 8):
+            A = rng.normal(size=(M, K)).astype(np.float32)
+            want = orc.matmul(qw, sc, None, N, K, 4, A, True)
+            assert bits_equal(_run(hb, gpu, h, A, N), want), M
+    finally:
+        hb.free(h)
