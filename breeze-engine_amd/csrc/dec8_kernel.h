@@ -19,9 +19,8 @@ namespace bq {
 // quantizer writes in that operand order ([chunk][JG / 2][64 lanes][16 B]),
 // not through LDS: eight rows of K = 12288 are 192 KB.  The bias term
 // 128 * sum(b) of the two-pass product, which the four-row kernel takes from
-// two constant A rows, is summed in the lane: udot8 of the lane's nibbles
-// (INT4) or udot4 of its raw bytes (INT8), then over the chunk's four
-// k-octet lane groups with permlane swaps, two blocks to a dword.
+// two constant A rows, comes from a second MFMA per block
+// (v_mfma_i32_16x16x64_i8 of a constant A operand and the B octets twice).
 constexpr int kP8 = 14;
 constexpr int kRows8 = 8;
 
@@ -52,15 +51,6 @@ struct Unit8 {
     float sc;
     int c;  // chunk to compute; nbg or more: none (past the end)
 };
-
-// Sum over the four k-octet lane groups (lanes col + 16 q) of a dword of two
-// 16-bit partial sums; every lane of a column receives it.
-__device__ inline uint32_t octet_sum2(uint32_t p) {
-    const auto s32 = __builtin_amdgcn_permlane32_swap(p, p, false, false);
-    const uint32_t y = s32[0] + s32[1];
-    const auto s16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
-    return s16[0] + s16[1];
-}
 
 // Leading arguments in SGPRs at wave launch (kernarg preload), as in
 // dec_kernel.  misc = sc_shift | phases per tile << 16.  Tiles: the first
@@ -240,6 +230,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     const int* sq0 = sq_l + (2 * grp) * lay.sa_pitch;
     const int* sq1 = sq0 + lay.sa_pitch;
     float* const fout = fbuf + lane * PP + wave * JG;
+    // Constant A operand of the bias MFMA: rows 4 g + 1 all 64, the others
+    // zero.
+    const int k64s = (lane & 3) == 1 ? 0x40404040 : 0;
+    const v4i k64 = v4i{k64s, k64s, k64s, k64s};
 
     auto consume = [&](const Unit8<JG>& cur, int buf) {
         const int c = cur.c;
@@ -250,32 +244,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
             z0 = *reinterpret_cast<const int4*>(sq0 + c * 4);
             z1 = *reinterpret_cast<const int4*>(sq1 + c * 4);
         }
-        // 128 * sum(b) of this lane's column for each block of the chunk.
-        int sb[JG];
-        if constexpr (HP) {
-            if constexpr (BITS == 4) {
-                const uint32_t wv[4] = {cur.w.x, cur.w.y, cur.w.z, cur.w.w};
-                uint32_t n[4];
-#pragma unroll
-                for (int b = 0; b < 4; ++b) n[b] = __builtin_amdgcn_udot8(wv[b], 0x11111111u, 0u, false);  // <= 120
-                const uint32_t p0 = octet_sum2(n[0] | n[1] << 16), p1 = octet_sum2(n[2] | n[3] << 16);
-                sb[0] = (int)(p0 & 0xFFFFu) << 7;
-                sb[1] = (int)(p0 >> 16) << 7;
-                sb[2] = (int)(p1 & 0xFFFFu) << 7;
-                sb[3] = (int)(p1 >> 16) << 7;
-            } else {
-                // Raw bytes b + 128 in [0, 255]: a lane's eight sum to
-                // sum(b) + 1024 in [0, 2040], the four octets to sum(b) + 4096.
-                const uint32_t ones = 0x01010101u, fl = 0x80808080u;
-                const uint32_t s0 = __builtin_amdgcn_udot4(cur.w.x ^ fl, ones,
-                                                           __builtin_amdgcn_udot4(cur.w.y ^ fl, ones, 0u, false), false);
-                const uint32_t s1 = __builtin_amdgcn_udot4(cur.w.z ^ fl, ones,
-                                                           __builtin_amdgcn_udot4(cur.w.w ^ fl, ones, 0u, false), false);
-                const uint32_t p = octet_sum2(s0 | s1 << 16);
-                sb[0] = ((int)(p & 0xFFFFu) - 4096) << 7;
-                sb[1] = ((int)(p >> 16) - 4096) << 7;
-            }
-        }
         fvec f0, f1;
 #pragma unroll
         for (int jb = 0; jb < JG; ++jb) {
@@ -284,15 +252,26 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
             const uint64_t bop = unpack_b(cur.w, jb, BITS);
             const uint4& a2 = cur.a[jb >> 1];
             const uint64_t aop = (jb & 1) ? ((uint64_t)a2.w << 32 | a2.z) : ((uint64_t)a2.y << 32 | a2.x);
-            const v4i dd = mfma16(aop, bop);
-            int cs0 = dd[0], cs1 = dd[2];
-            if constexpr (HP) {
-                cs0 = cs0 * 256 + dd[1] + sb[jb];
-                cs1 = cs1 * 256 + dd[3] + sb[jb];
-            }
+            int e0 = 0, e1 = 0;
             if (BITS == 4) {
-                cs0 += jb == 0 ? z0.x : jb == 1 ? z0.y : jb == 2 ? z0.z : z0.w;
-                cs1 += jb == 0 ? z1.x : jb == 1 ? z1.y : jb == 2 ? z1.z : z1.w;
+                e0 = jb == 0 ? z0.x : jb == 1 ? z0.y : jb == 2 ? z0.z : z0.w;
+                e1 = jb == 0 ? z1.x : jb == 1 ? z1.y : jb == 2 ? z1.z : z1.w;
+            }
+            const v4i dd = mfma16(aop, bop);
+            int cs0 = dd[0] + e0, cs1 = dd[2] + e1;
+            if constexpr (HP) {
+                // 128 * sum(b) from a 16x16x64 MFMA of the constant A
+                // operand (rows 4 g + 1 all 64) with this lane's k-octet
+                // twice as B: every output lane's result 1 is 64 * 2 *
+                // sum(b) of its column.  Both MFMAs take a zero accumulator
+                // input and the sums are VALU adds (an MFMA result fed
+                // straight into the next MFMA's accumulator input was
+                // allocated with partial register overlaps).
+                const v4i bb = v4i{(int)(uint32_t)bop, (int)(uint32_t)(bop >> 32), (int)(uint32_t)bop,
+                                   (int)(uint32_t)(bop >> 32)};
+                const int s128 = __builtin_amdgcn_mfma_i32_16x16x64_i8(k64, bb, v4i{0, 0, 0, 0}, 0, 0, 0)[1];
+                cs0 = dd[0] * 256 + dd[1] + (s128 + e0);
+                cs1 = dd[2] * 256 + dd[3] + (s128 + e1);
             }
             f0[jb] = (float)cs0 * cur.sc;
             f1[jb] = (float)cs1 * cur.sc;
