@@ -1,6 +1,7 @@
-// dec8_kernel.h -- the decode GEMV for five to eight rows: one workgroup per
-// tile range serves all eight rows, so every weight chunk crosses from L2 to
-// a CU once.  Instantiated per (bits, activation mode) by dec_w{4,8}_{hp,lp}.hip.
+// dec8_kernel.h -- the decode GEMV in row groups of eight: one workgroup per
+// (tile range, eight rows), so every weight chunk crosses from L2 to a CU
+// once per eight rows.  Instantiated per (bits, activation mode) by
+// dec_w{4,8}_{hp,lp}.hip.
 #pragma once
 
 #include "qmm_common.h"
@@ -53,8 +54,10 @@ struct Unit8 {
 };
 
 // Leading arguments in SGPRs at wave launch (kernarg preload), as in
-// dec_kernel.  misc = sc_shift | phases per tile << 16.  Tiles: the first
-// rem_t workgroups own base_t + 1, the rest base_t.
+// dec_kernel.  misc = sc_shift | RG << 8 | xcd << 12 | phases per tile << 16
+// (RG row groups of eight rows; xcd: the RG workgroups of a tile range share
+// an XCD).  pM is all rows of the call.  Tiles: the first rem_t tile ranges
+// own base_t + 1, the rest base_t.
 template <int BITS, bool HP>
 __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, const float* pS, const uint4* pR,
                                                               int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
@@ -67,15 +70,36 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int nblk = pnblk, M = pM, nbg = pnbg;
+    const int nblk = pnblk, nbg = pnbg;
     const int nblk4 = (nblk + 3) / 4 * 4;
     const int sc_shift = misc & 31, npw = misc >> 16;
+    const int RG = (misc >> 8) & 15;
+
+    // Row group rg (rows 8 rg .. 8 rg + 7) of tile range g.  Workgroups are
+    // dealt to the 8 XCDs in turn; with xcd set the RG row groups of a tile
+    // range are blocks 8 (RG (g / 8) + rg) + g % 8, on one XCD, so the later
+    // reads of each weight chunk hit its L2.
+    int g, rg;
+    if (RG == 1) {
+        g = blockIdx.x;
+        rg = 0;
+    } else if ((misc >> 12) & 1) {
+        const int b = blockIdx.x, q = b >> 3;
+        g = (q / RG) * 8 + (b & 7);
+        rg = q % RG;
+    } else {
+        g = blockIdx.x / RG;
+        rg = blockIdx.x % RG;
+    }
+    const int m0 = kRows8 * rg;
+    const int M = min(kRows8, pM - m0);  // rows of this workgroup
+    pR += (size_t)rg * nbg * (JG / 2) * 64;
 
     // Block scales and sums of q first (at most two uint4 per thread per
-    // array: M * nblk4 <= 8192).
+    // array: 8 * nblk4 <= 8192).
     const int nmeta = M * nblk4 / 4;
-    const uint4* gsa = reinterpret_cast<const uint4*>(args.Sa);
-    const uint4* gsq = reinterpret_cast<const uint4*>(args.Sq);
+    const uint4* gsa = reinterpret_cast<const uint4*>(args.Sa + (size_t)m0 * nblk4);
+    const uint4* gsq = reinterpret_cast<const uint4*>(args.Sq + (size_t)m0 * nblk4);
     const int mi0 = min(tid, nmeta - 1), mi1 = min(tid + 1024, nmeta - 1);
     const bool two_meta = nmeta > 1024;
     uint4 ma0 = gsa[mi0], ma1 = ma0, mq0 = make_uint4(0u, 0u, 0u, 0u), mq1 = mq0;
@@ -86,7 +110,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    const int g = blockIdx.x;
     const int t_begin = g * pbase_t + min(g, prem_t);
     const int nT = pbase_t + (g < prem_t ? 1 : 0);
     const int U = nT * npw;  // phases of this workgroup
@@ -210,7 +233,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
                 for (int b = i * JG; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
             }
             if (++pr_p == npw) {
-                if (row < M) args.C[(size_t)row * args.N + (t_begin + pr_t) * 16 + col] = acc;
+                if (row < M) args.C[(size_t)(m0 + row) * args.N + (t_begin + pr_t) * 16 + col] = acc;
                 ++pr_t;
                 acc = 0.0f;
                 pr_p = 0;
@@ -302,7 +325,7 @@ hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int 
         *attr_set = true;
     }
     const int npw = (a.nbg + kP8 - 1) / kP8;
-    const int misc = a.sc_shift | npw << 16;
+    const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 12 | npw << 16;
     const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
     kern<<<grid, kDecWaves * 64, lds, st>>>(a.W, a.S, rec, base_t, a.nblk, a.M, a.nbg, rem_t, a.ngrp, misc, a);
     return hipGetLastError();

@@ -154,19 +154,20 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     }
 }
 
-// The same quantizer for the five-to-eight-row decode kernel: records in its
-// MFMA A-operand order, [chunk][JG / 2][64 lanes][16 B], lane 16 e + 2 m + s
-// holding k-octet e of record part s of row m for blocks 2 h and 2 h + 1 of
-// the chunk (8 bytes each).  Rows M..7 and the padding blocks of the last
-// chunk are zeros.  Scales and sums of q as quantize_kernel's.  Threads:
-// 8 rows x nblk_pad blocks x 4.
+// The same quantizer for the decode kernel in row groups of eight
+// (dec8_kernel): records in its MFMA A-operand order, per row group
+// [chunk][JG / 2][64 lanes][16 B], lane 16 e + 2 m + s holding k-octet e of
+// record part s of the group's row m for blocks 2 h and 2 h + 1 of the chunk
+// (8 bytes each).  Rows past M (to the end of the last group) and the padding
+// blocks of the last chunk are zeros.  Scales and sums of q as
+// quantize_kernel's.  Threads: 8 rg_count rows x nblk_pad blocks x 4.
 template <bool HP, int JG>
 __global__ __launch_bounds__(256) void quantize_r8_kernel(const float* __restrict__ A, int M, int K, int nblk,
-                                                          int nblk_pad, int nblk4, uint8_t* __restrict__ R,
+                                                          int nblk_pad, int nblk4, int rows, uint8_t* __restrict__ R,
                                                           float* __restrict__ Sa, int* __restrict__ Sq) {
     const int gtid = blockIdx.x * 256 + threadIdx.x;
     const int blk = gtid >> 2, e = gtid & 3;
-    const bool in = blk < 8 * nblk_pad;
+    const bool in = blk < rows * nblk_pad;
     const int m = in ? blk / nblk_pad : 0, j = in ? blk - m * nblk_pad : 0;
     const bool real = in && m < M && j < nblk;
     float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
@@ -181,10 +182,11 @@ __global__ __launch_bounds__(256) void quantize_r8_kernel(const float* __restric
     quant4x8<HP>(v0, v1, s, ph, pl, sum);
     if (in) {
         if (!real) ph = pl = make_uint2(0u, 0u);
-        const int c = j / JG, jb = j - c * JG;
-        uint8_t* base = R + ((size_t)(c * (JG / 2) + (jb >> 1)) * 64) * 16 + (jb & 1) * 8;
-        *reinterpret_cast<uint2*>(base + (16 * e + 2 * m) * 16) = ph;
-        *reinterpret_cast<uint2*>(base + (16 * e + 2 * m + 1) * 16) = pl;
+        const int c = j / JG, jb = j - c * JG, ml = m & 7;
+        uint8_t* base = R + (size_t)(m >> 3) * nblk_pad * 512 +
+                        ((size_t)(c * (JG / 2) + (jb >> 1)) * 64) * 16 + (jb & 1) * 8;
+        *reinterpret_cast<uint2*>(base + (16 * e + 2 * ml) * 16) = ph;
+        *reinterpret_cast<uint2*>(base + (16 * e + 2 * ml + 1) * 16) = pl;
         if (real && e == 0) {
             Sa[(size_t)m * nblk4 + j] = s;
             Sq[(size_t)m * nblk4 + j] = sum;
@@ -1107,8 +1109,13 @@ int device_cus(Workspace& w, int dev) {
 // (no block-integer export, gate/up pair, multi-projection or argmax) of a
 // handle without per-block metadata, with its eight rows' block scales and
 // sums within two uint4 per thread and its LDS plan within the limit.
+// Rows of the eight-row groups that take M rows (M rounded up to 8).
+int dec8_rows(int M) { return (M + kRows8 - 1) / kRows8 * kRows8; }
+constexpr int kDec8MaxRows = 32;  // four row groups
 bool dec8_takes(const Handle* h, int M, bool dots, bool pair, bool multi, bool argmax) {
-    if (M < 5 || M > kRows8 || dots || pair || multi || argmax || h->extra) return false;
+    int max_rows = kDec8MaxRows;
+    if (const char* r = std::getenv("BREEZE_HIP_DEC8_ROWS")) max_rows = std::min(kDec8MaxRows, std::max(5, std::atoi(r)));
+    if (M < 5 || M > max_rows || dots || pair || multi || argmax || h->extra) return false;
     const char* f = std::getenv("BREEZE_HIP_DEC8");
     if (f && f[0] == '0') return false;
     if ((size_t)kRows8 * h->nblk4 / 4 > 2 * (size_t)kDecWaves * 64) return false;
@@ -1216,21 +1223,26 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     if ((h2 || mp) && !dec) return kNotPairable;
     if (mp && (h->extra || dIdx)) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
-    // Five to eight rows of a plain call whose row groups would copy staged
-    // records: one workgroup per tile range for all eight rows
-    // (dec8_kernel), when its scale and sum rows fit (two uint4 per thread).
-    // Both take the stand-alone quantizer; where the row groups quantize in
-    // their prologue (K <= 4096 at four rows a group) they keep the call,
+    // 5-32 rows of a plain call, up to the decode kernel's row limit, whose
+    // four-row groups would copy staged records (or whose records do not fit
+    // them): row groups of eight (dec8_kernel), one workgroup per (tile
+    // range, eight rows), when its scale and sum rows fit (two uint4 per
+    // thread).  Both take the stand-alone quantizer; where the four-row
+    // groups quantize in their prologue (K <= 4096) they keep the call,
     // which saves that launch (~2.5 us): W8 K=4096 N=4096 at 8 rows 9.7 us
-    // against 12.2 us.  BREEZE_HIP_DEC8=0 keeps every call on the row
-    // groups.
-    const bool dec8 = dec && !fused && dec8_takes(h, M, dots, h2 != nullptr, mp != nullptr, dIdx != nullptr);
+    // against 12.2 us.  Measured against the four-row groups (us): W4
+    // K=12288 N=4096 at 8 / 16 / 32 rows 13.6 / 21.1 / 34.0 -> 13.1 / 18.6 /
+    // 29.2, W8 K=12288 N=4096 at 24 rows 49.3 -> 34.3, W4 K=17408 N=5120 at
+    // 16 rows 54.0 -> 30.6 (at 24 and 32 rows the GEMM took 167 us);
+    // W4 K=5120 N=5120 at 12 rows 13.3 -> 14.1 is the one loss seen.
+    // BREEZE_HIP_DEC8=0 keeps every call off it.
+    const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots, h2 != nullptr, mp != nullptr, dIdx != nullptr);
     // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
     // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the
     // norm kernel then the projections; M = 2, 320 row-blocks: even).
     if (mp && mp->norm && !(fused && Mr_max * h->nblk <= kNormFusedMaxBlocks)) return kNotPairable;
     // Prefill GEMM: more than 8 rows without a legacy corr.
-    const bool pre = !dec && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
+    const bool pre = !dec && !dec8 && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
     const int pf_rp = pick_pf_rp(M, std::getenv("BREEZE_HIP_PREFILL_RP"));
     const int pf_rows = 32 * pf_rp;  // rows per prefill workgroup
     const int Mpad = (M + pf_rows - 1) / pf_rows * pf_rows;
@@ -1245,18 +1257,20 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
     } else if (dec8) {
-        if (!ensure_quant(w, s, st, kRows8, h->nblk4)) return -4;
-        const size_t threads = (size_t)kRows8 * h->nblk_pad * 4;
+        const int rows8 = dec8_rows(M);
+        if (!ensure_quant(w, s, st, rows8, h->nblk4)) return -4;
+        const size_t threads = (size_t)rows8 * h->nblk_pad * 4;
         const unsigned qb = (unsigned)((threads + 255) / 256);
         const int JGq = h->bits == 8 ? 2 : 4;
+        const int K = h->K, nb = h->nblk, np = h->nblk_pad, n4 = h->nblk4;
         if (hp && JGq == 4)
-            quantize_r8_kernel<true, 4><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+            quantize_r8_kernel<true, 4><<<qb, 256, 0, st>>>(dA, M, K, nb, np, n4, rows8, s.aq, s.sa, s.sq);
         else if (hp)
-            quantize_r8_kernel<true, 2><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+            quantize_r8_kernel<true, 2><<<qb, 256, 0, st>>>(dA, M, K, nb, np, n4, rows8, s.aq, s.sa, s.sq);
         else if (JGq == 4)
-            quantize_r8_kernel<false, 4><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+            quantize_r8_kernel<false, 4><<<qb, 256, 0, st>>>(dA, M, K, nb, np, n4, rows8, s.aq, s.sa, s.sq);
         else
-            quantize_r8_kernel<false, 2><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, h->nblk_pad, h->nblk4, s.aq, s.sa, s.sq);
+            quantize_r8_kernel<false, 2><<<qb, 256, 0, st>>>(dA, M, K, nb, np, n4, rows8, s.aq, s.sa, s.sq);
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
         a.Aq = s.aq;
         a.Sa = s.sa;
@@ -1275,16 +1289,19 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
 
     hipError_t e;
     if (dec8) {
-        a.NG = std::min(a.ntiles, device_cus(w, dev));
-        a.RG = 1;
+        const int n_cu = device_cus(w, dev);
         a.RS = kRows8;
+        a.RG = dec8_rows(M) / kRows8;
+        a.NG = std::min(a.ntiles, std::max(1, n_cu / a.RG));
+        a.pair_xcd = (a.RG > 1 && a.NG % 8 == 0) ? 1 : 0;
+        const int grid = a.NG * a.RG;
         const int lds8 = dec8_lds(h->nblk, JG).total;
         const uint4* rec = reinterpret_cast<const uint4*>(s.aq);
         bool* at = &w.dec8_attr[(h->bits == 8 ? 1 : 0) | (hp ? 2 : 0)];
-        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, a.NG, lds8, st)
-                                 : launch_dec8<8, false>(at, a, rec, a.NG, lds8, st);
-        else e = hp ? launch_dec8<4, true>(at, a, rec, a.NG, lds8, st)
-                    : launch_dec8<4, false>(at, a, rec, a.NG, lds8, st);
+        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, st)
+                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, st);
+        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, st)
+                    : launch_dec8<4, false>(at, a, rec, grid, lds8, st);
     } else if (dec) {
         if (mp) {
             int t = 0;
@@ -1776,7 +1793,7 @@ int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64
     s.rec_cap = region;
     // Stand-alone quantizer records for this call's rows: [M][nblk4] of 64 B
     // records, then the scales and sums.
-    const size_t nq = (size_t)(M >= 5 && M <= kRows8 ? kRows8 : M) * h->nblk4;
+    const size_t nq = (size_t)(M >= 5 && M <= kDec8MaxRows ? dec8_rows(M) : M) * h->nblk4;
     if (nq * 72 <= region) {
         s.aq = recs;
         s.sa = reinterpret_cast<float*>(recs + nq * 64);

@@ -92,3 +92,30 @@ def test_dec8_then_fewer_rows(gpu, hb, orc, hi_prec):
             assert bits_equal(_run(hb, gpu, h, A, N), want), M
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("K,N", [(4640, 272), (5120, 8704), (12288, 4096), (17408, 80)])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dec8_row_groups_bit_exact(gpu, hb, orc, hi_prec, K, N, bits):
+    """Up to four row groups of eight rows, their workgroups on one XCD per
+    tile range (512 tiles) or not (17, 5 tiles); a partial last group at 9,
+    17 and 27 rows; K = 17408, whose records the four-row groups cannot hold
+    past 16 rows."""
+    rng = np.random.default_rng(K + N + bits)
+    nblk = K // 32
+    qw, sc, _ = rng_weights(rng, N, K, bits)
+    sc = np.ascontiguousarray(np.repeat(sc[:, :1], nblk, axis=1))
+    A32 = rng.normal(size=(32, K)).astype(np.float32)
+    A32[rng.random(A32.shape) < 0.01] *= 20.0
+    h = hb.prepack(qw, sc, None, K, N, bits=bits)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for M in (9, 16, 17, 27, 32):
+                A = np.ascontiguousarray(A32[:M])
+                case = dict(K=K, N=N, bits=bits, hp=hp, M=M)
+                print(f"dec8 row groups {case}", flush=True)
+                want = orc.matmul(qw, sc, None, N, K, bits, A, hp)
+                assert bits_equal(_run(hb, gpu, h, A, N), want), case
+    finally:
+        hb.free(h)
