@@ -189,6 +189,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
         const float* sa_row = sa_l + row * lay.sa_pitch;
         const bool tail_pad = nblk != nbg * JG;  // the last chunk has padding blocks
         float acc = 0.0f;
+        unsigned long long best = 0;
         int pr_t = 0, pr_p = 0;
         for (int u = 0; u < U; ++u) {
             lds_barrier();
@@ -233,10 +234,37 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
                 for (int b = i * JG; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
             }
             if (++pr_p == npw) {
-                if (row < M) args.C[(size_t)(m0 + row) * args.N + (t_begin + pr_t) * 16 + col] = acc;
+                const int n = (t_begin + pr_t) * 16 + col;
+                if (row < M) args.C[(size_t)(m0 + row) * args.N + n] = acc;
+                if (args.idx) {
+                    const unsigned long long k = argmax_key(acc, n);
+                    best = k > best ? k : best;
+                }
                 ++pr_t;
                 acc = 0.0f;
                 pr_p = 0;
+            }
+        }
+        if (args.idx) {
+            // Argmax as in dec_kernel: row maximum over the row's 16 lanes,
+            // merged into the device's keys with device-scope atomic max;
+            // after its atomics each chain wave takes a ticket, and the wave
+            // holding the last of the grid's 2 * gridDim.x tickets swaps the
+            // keys back to zero (re-arming them) and writes the indices.
+#pragma unroll
+            for (int sh = 1; sh < 16; sh <<= 1) {
+                const unsigned long long o = __shfl_xor(best, sh, 16);
+                best = o > best ? o : best;
+            }
+            if (col == 0 && row < M) (void)atomicMax(args.key + m0 + row, best);
+            __builtin_amdgcn_s_waitcnt(0);
+            unsigned int t = 0;
+            if (lane == 0) t = atomicAdd(args.ticket, 1u);
+            t = __shfl(t, 0);
+            if (t == 2 * gridDim.x - 1 && lane < pM) {
+                const unsigned long long k = atomicExch(args.key + lane, 0ull);
+                args.idx[lane] = (int64_t)(0xFFFFFFFFu - (uint32_t)(k & 0xFFFFFFFFull));
+                if (lane == 0) atomicExch(args.ticket, 0u);
             }
         }
         return;

@@ -1105,17 +1105,17 @@ int device_cus(Workspace& w, int dev) {
     return w.n_cu;
 }
 
-// Whether the five-to-eight-row decode kernel takes a call: a plain call
-// (no block-integer export, gate/up pair, multi-projection or argmax) of a
+// Whether the decode kernel in row groups of eight takes a call: a plain
+// call (no block-integer export, gate/up pair or multi-projection) of a
 // handle without per-block metadata, with its eight rows' block scales and
 // sums within two uint4 per thread and its LDS plan within the limit.
 // Rows of the eight-row groups that take M rows (M rounded up to 8).
 int dec8_rows(int M) { return (M + kRows8 - 1) / kRows8 * kRows8; }
 constexpr int kDec8MaxRows = 32;  // four row groups
-bool dec8_takes(const Handle* h, int M, bool dots, bool pair, bool multi, bool argmax) {
+bool dec8_takes(const Handle* h, int M, bool dots, bool pair, bool multi) {
     int max_rows = kDec8MaxRows;
     if (const char* r = std::getenv("BREEZE_HIP_DEC8_ROWS")) max_rows = std::min(kDec8MaxRows, std::max(5, std::atoi(r)));
-    if (M < 5 || M > max_rows || dots || pair || multi || argmax || h->extra) return false;
+    if (M < 5 || M > max_rows || dots || pair || multi || h->extra) return false;
     const char* f = std::getenv("BREEZE_HIP_DEC8");
     if (f && f[0] == '0') return false;
     if ((size_t)kRows8 * h->nblk4 / 4 > 2 * (size_t)kDecWaves * 64) return false;
@@ -1236,7 +1236,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // 16 rows 54.0 -> 30.6 (at 24 and 32 rows the GEMM took 167 us);
     // W4 K=5120 N=5120 at 12 rows 13.3 -> 14.1 is the one loss seen.
     // BREEZE_HIP_DEC8=0 keeps every call off it.
-    const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots, h2 != nullptr, mp != nullptr, dIdx != nullptr);
+    const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots, h2 != nullptr, mp != nullptr);
     // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
     // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the
     // norm kernel then the projections; M = 2, 320 row-blocks: even).
@@ -1288,6 +1288,36 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     }
 
     hipError_t e;
+    // The decode kernels' in-kernel argmax merges into per-stream state
+    // (a ticket, then kDecMaxRows row keys), zero between calls.
+    if ((dec8 || dec) && dIdx) {
+        if (!s.ticket && s.fixed) {
+            set_err("internal: fixed scratch without argmax state");
+            return -5;
+        }
+        if (!s.ticket) {
+            // Allocated and zeroed once per stream, outside capture; the
+            // kernel's last workgroup re-arms it to zero.
+            if (capturing(st)) {
+                set_err("argmax workspace: make one argmax call on the stream before capturing it");
+                return -4;
+            }
+            unsigned int* t = nullptr;
+            if (!hip_ok(hipMalloc(&t, (1 + kDecMaxRows) * sizeof(unsigned long long)), "argmax workspace"))
+                return -4;
+            // Cleared on st itself: a non-blocking stream does not wait
+            // for work on the null stream.
+            fill_u32_kernel<<<(2 * (1 + kDecMaxRows) + 63) / 64, 64, 0, st>>>(t, 2 * (1 + kDecMaxRows), 0u);
+            if (!hip_ok(hipGetLastError(), "argmax workspace clear")) {
+                w.retired.push_back(t);
+                return -4;
+            }
+            s.ticket = t;
+        }
+        a.ticket = s.ticket;
+        a.key = reinterpret_cast<unsigned long long*>(s.ticket) + 1;
+        a.idx = dIdx;
+    }
     if (dec8) {
         const int n_cu = device_cus(w, dev);
         a.RS = kRows8;
@@ -1345,34 +1375,6 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
             a.S2 = h2->S;
             a.Z2 = h2->Z;
             a.D2 = h2->D;
-        }
-        if (dIdx) {
-            if (!s.ticket && s.fixed) {
-                set_err("internal: fixed scratch without argmax state");
-                return -5;
-            }
-            if (!s.ticket) {
-                // Allocated and zeroed once per stream, outside capture; the
-                // kernel's last workgroup re-arms it to zero.
-                if (capturing(st)) {
-                    set_err("argmax workspace: make one argmax call on the stream before capturing it");
-                    return -4;
-                }
-                unsigned int* t = nullptr;
-                if (!hip_ok(hipMalloc(&t, (1 + kDecMaxRows) * sizeof(unsigned long long)), "argmax workspace"))
-                    return -4;
-                // Cleared on st itself: a non-blocking stream does not wait
-                // for work on the null stream.
-                fill_u32_kernel<<<(2 * (1 + kDecMaxRows) + 63) / 64, 64, 0, st>>>(t, 2 * (1 + kDecMaxRows), 0u);
-                if (!hip_ok(hipGetLastError(), "argmax workspace clear")) {
-                    w.retired.push_back(t);
-                    return -4;
-                }
-                s.ticket = t;
-            }
-            a.ticket = s.ticket;
-            a.key = reinterpret_cast<unsigned long long*>(s.ticket) + 1;
-            a.idx = dIdx;
         }
         const int grid = a.NG * a.RG;
         const bool x = h->extra;

@@ -119,3 +119,36 @@ def test_dec8_row_groups_bit_exact(gpu, hb, orc, hi_prec, K, N, bits):
                 assert bits_equal(_run(hb, gpu, h, A, N), want), case
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("hp", [True, False])
+def test_dec8_argmax(gpu, hb, orc, hi_prec, bits, hp):
+    """The in-kernel argmax at 5-12 rows (LM-head batches), several tiles
+    per workgroup: outputs bit-exact and indices equal to the first maximum,
+    with two identical columns (5 and 9000) holding every row's maximum, so
+    the tie must resolve to the lower index across workgroups.  Calls repeat
+    on one stream, so the re-armed keys and ticket are exercised."""
+    rng = np.random.default_rng(31 + bits + (10 if hp else 0))
+    K, N = 5120, 16 * 600
+    nblk = K // 32
+    qw, sc, _ = rng_weights(rng, N, K, bits)
+    sc = np.ascontiguousarray(np.repeat(sc[:, :1], nblk, axis=1))
+    top = 0xFF if bits == 4 else 255  # nibbles 15 / raw 255: the largest weights
+    qw[5] = top
+    qw[9000] = top
+    sc[5] = sc[9000] = 0.02
+    h = hb.prepack(qw, sc, None, K, N, bits=bits)
+    hb.set_hi_prec(hp)
+    try:
+        for M in (5, 8, 12, 8):
+            A = np.abs(rng.normal(size=(M, K))).astype(np.float32)
+            want = orc.matmul(qw, sc, None, N, K, bits, A, hp)
+            got, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+            gpu.cuda.synchronize()
+            case = dict(bits=bits, hp=hp, M=M)
+            assert bits_equal(got.cpu().numpy(), want), case
+            assert (want[:, 5] == want[:, 9000]).all() and np.argmax(want, axis=1).tolist() == [5] * M, case
+            assert idx.cpu().numpy().tolist() == [5] * M, case
+    finally:
+        hb.free(h)
