@@ -58,7 +58,7 @@ struct Unit8 {
 // (RG row groups of eight rows; xcd: the RG workgroups of a tile range share
 // an XCD).  pM is all rows of the call.  Tiles: the first rem_t tile ranges
 // own base_t + 1, the rest base_t.
-template <int BITS, bool HP>
+template <int BITS, bool HP, int FUSE>
 __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, const float* pS, const uint4* pR,
                                                               int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
                                                               int pngrp, int misc, GemvArgs args) {
@@ -66,6 +66,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     constexpr int NA = JG / 2;
     constexpr int PP = dec_pitch(JG);
     constexpr int R = kDecRing;
+    // FUSE (as in dec_kernel): plain, the gate/up pair (each tile's gate
+    // then up projection, C = silu(gate) * up), or several projections of
+    // the activation (tiles concatenated over the segment table).
+    constexpr bool PAIR = FUSE == kFusePair, MULTI = FUSE == kFuseMulti;
+    static_assert(FUSE == kFusePlain || PAIR || MULTI, "no norm in this kernel's prologue");
     typedef float fvec __attribute__((ext_vector_type(JG)));
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -112,7 +117,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
 
     const int t_begin = g * pbase_t + min(g, prem_t);
     const int nT = pbase_t + (g < prem_t ? 1 : 0);
-    const int U = nT * npw;  // phases of this workgroup
+    const int U = nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
 
     const Dec8Lds lay = dec8_lds(nblk, JG);
     float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
@@ -145,11 +150,22 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     // loads re-read the last tile.  A load with no work in a tile's short
     // last phase reads the chunk this producer loads in the next tile (L2
     // warm-up), or on the last tile the tile's last chunk.
-    int ld_c = wave, ld_rem = npw, ld_t = 0;
-    uint32_t ld_w = (uint32_t)t_begin * nbg * 64;
-    uint32_t ld_s = (uint32_t)t_begin * pngrp * 16;
+    // PAIR: ld_sel selects the up projection of the current tile.  MULTI:
+    // the weights and scales of segment ld_k are at lw and ls, and the
+    // cursor moves to the next segment's arrays when a tile crosses into it
+    // (the idle loads never leave a tile in either mode).
+    int ld_c = wave, ld_rem = npw, ld_t = 0, ld_sel = 0;
+    int ld_k = 0, t_off = 0;
+    if (MULTI) {
+        ld_k = (t_begin >= args.seg_end[0]) + (t_begin >= args.seg_end[1]) + (t_begin >= args.seg_end[2]);
+        t_off = ld_k ? args.seg_end[ld_k - 1] : 0;
+    }
+    const uint4* lw = MULTI ? args.segW[ld_k] : pW;
+    const float* ls = MULTI ? args.segS[ld_k] : pS;
+    uint32_t ld_w = (uint32_t)(t_begin - t_off) * nbg * 64;
+    uint32_t ld_s = (uint32_t)(t_begin - t_off) * pngrp * 16;
     const int pf_c = nbg + kP8 + wave;
-    const bool pf = npw >= 2 && wave + kP8 < nbg;
+    const bool pf = !PAIR && !MULTI && npw >= 2 && wave + kP8 < nbg;
     int ld_idle = (pf && nT > 1) ? pf_c : nbg - 1;
     auto load_unit = [&](Unit8<JG>& p) {
         const int c = min(ld_c, nbg - 1);
@@ -158,21 +174,35 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
         uint32_t si = ld_s + (uint32_t)((c * JG) >> sc_shift) * 16 + col;
         uint32_t ri = (uint32_t)c * (NA * 64) + lane;
         asm("" : "+v"(wi), "+v"(si), "+v"(ri));
-        p.w = pW[wi];
+        const bool up = PAIR && ld_sel;
+        p.w = (up ? args.W2 : lw)[wi];
 #pragma unroll
         for (int h = 0; h < NA; ++h) p.a[h] = pR[ri + 64 * h];
-        p.sc = pS[si];
+        p.sc = (up ? args.S2 : ls)[si];
         p.c = ld_c;
         ld_c += kP8;
         if (--ld_rem == 0) {
             ld_rem = npw;
-            if (++ld_t < nT) {
+            if (PAIR && ld_sel == 0 && ld_t < nT) {
+                ld_sel = 1;  // the same tile's up projection
                 ld_c = wave;
-                ld_w += nbg * 64;
-                ld_s += pngrp * 16;
-                if (ld_t + 1 == nT) ld_idle = nbg - 1;
             } else {
-                ld_c = 1 << 24;
+                if (PAIR) ld_sel = 0;
+                if (++ld_t < nT) {
+                    ld_c = wave;
+                    ld_w += nbg * 64;
+                    ld_s += pngrp * 16;
+                    if (MULTI && t_begin + ld_t == args.seg_end[ld_k]) {
+                        ++ld_k;
+                        lw = args.segW[ld_k];
+                        ls = args.segS[ld_k];
+                        ld_w = 0;
+                        ld_s = 0;
+                    }
+                    if (ld_t + 1 == nT) ld_idle = nbg - 1;
+                } else {
+                    ld_c = 1 << 24;
+                }
             }
         }
     };
@@ -188,9 +218,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
         const int r = wave - kP8, row = 2 * grp + r;
         const float* sa_row = sa_l + row * lay.sa_pitch;
         const bool tail_pad = nblk != nbg * JG;  // the last chunk has padding blocks
-        float acc = 0.0f;
+        float acc = 0.0f, gate = 0.0f;
         unsigned long long best = 0;
-        int pr_t = 0, pr_p = 0;
+        int pr_t = 0, pr_p = 0, pr_sel = 0, pr_k = 0;
         for (int u = 0; u < U; ++u) {
             lds_barrier();
             const float* fp = fbuf + (((u & 1) * 2 + r) * 64 + lane) * PP;
@@ -234,18 +264,37 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
                 for (int b = i * JG; b < nb; ++b) acc = __builtin_fmaf(sp[b], fp[b], acc);
             }
             if (++pr_p == npw) {
-                const int n = (t_begin + pr_t) * 16 + col;
-                if (row < M) args.C[(size_t)(m0 + row) * args.N + n] = acc;
-                if (args.idx) {
-                    const unsigned long long k = argmax_key(acc, n);
-                    best = k > best ? k : best;
+                if (PAIR && pr_sel == 0) {
+                    gate = acc;  // the up tile of the same columns follows
+                    pr_sel = 1;
+                } else {
+                    // silu(g) = g / (1 + exp(-g)) (qwen35_decoder.cpp:129),
+                    // times the up projection (qwen35_decoder.cpp:408): the
+                    // same expression as dec_kernel's.
+                    const float v = PAIR ? gate / (1.0f + expf(-gate)) * acc : acc;
+                    const int gt = t_begin + pr_t;
+                    if (MULTI) {
+                        while (gt >= args.seg_end[pr_k]) ++pr_k;
+                        if (row < M) {
+                            const int t0k = pr_k ? args.seg_end[pr_k - 1] : 0;
+                            args.segC[pr_k][(size_t)(m0 + row) * args.segN[pr_k] + (gt - t0k) * 16 + col] = v;
+                        }
+                    } else {
+                        const int n = gt * 16 + col;
+                        if (row < M) args.C[(size_t)(m0 + row) * args.N + n] = v;
+                        if (!PAIR && args.idx) {
+                            const unsigned long long k = argmax_key(acc, n);
+                            best = k > best ? k : best;
+                        }
+                    }
+                    if (PAIR) pr_sel = 0;
+                    ++pr_t;
                 }
-                ++pr_t;
                 acc = 0.0f;
                 pr_p = 0;
             }
         }
-        if (args.idx) {
+        if (!PAIR && !MULTI && args.idx) {
             // Argmax as in dec_kernel: row maximum over the row's 16 lanes,
             // merged into the device's keys with device-scope atomic max;
             // after its atomics each chain wave takes a ticket, and the wave
@@ -343,20 +392,30 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     }
 }
 
-template <int BITS, bool HP>
-hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, hipStream_t st) {
-    auto kern = dec8_kernel<BITS, HP>;
-    if (!*attr_set) {
+template <int BITS, bool HP, int FUSE>
+hipError_t launch_dec8_f(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, hipStream_t st) {
+    auto kern = dec8_kernel<BITS, HP, FUSE>;
+    if (!attr_set[FUSE]) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
         if (e != hipSuccess) return e;
-        *attr_set = true;
+        attr_set[FUSE] = true;
     }
     const int npw = (a.nbg + kP8 - 1) / kP8;
     const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 12 | npw << 16;
     const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
     kern<<<grid, kDecWaves * 64, lds, st>>>(a.W, a.S, rec, base_t, a.nblk, a.M, a.nbg, rem_t, a.ngrp, misc, a);
     return hipGetLastError();
+}
+
+// attr_set: this device's flags for the (bits, mode) pair, one per FUSE mode.
+template <int BITS, bool HP>
+hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, int fuse,
+                       hipStream_t st) {
+    if (fuse == kFusePair) return launch_dec8_f<BITS, HP, kFusePair>(attr_set, a, rec, grid, lds, st);
+    if (fuse == kFuseMulti) return launch_dec8_f<BITS, HP, kFuseMulti>(attr_set, a, rec, grid, lds, st);
+    if (fuse != kFusePlain) return hipErrorInvalidValue;
+    return launch_dec8_f<BITS, HP, kFusePlain>(attr_set, a, rec, grid, lds, st);
 }
 
 }  // namespace bq

@@ -784,7 +784,7 @@ struct Workspace {
     hipStream_t stream = nullptr;
     int n_cu = 0;
     bool attr_set[256] = {};  // decode kernel variants with the kernel attribute set
-    bool dec8_attr[4] = {};   // the same for the five-to-eight-row decode kernel, per (bits, mode)
+    bool dec8_attr[16] = {};  // the same for dec8_kernel, per (bits, mode) and FUSE mode
     bool pf_attr[256] = {};
 };
 
@@ -1105,17 +1105,18 @@ int device_cus(Workspace& w, int dev) {
     return w.n_cu;
 }
 
-// Whether the decode kernel in row groups of eight takes a call: a plain
-// call (no block-integer export, gate/up pair or multi-projection) of a
+// Whether the decode kernel in row groups of eight takes a call: one
+// without the block-integer export (plain, argmax, gate/up pair or
+// multi-projection; the caller's own limits apply to the last two) of a
 // handle without per-block metadata, with its eight rows' block scales and
 // sums within two uint4 per thread and its LDS plan within the limit.
 // Rows of the eight-row groups that take M rows (M rounded up to 8).
 int dec8_rows(int M) { return (M + kRows8 - 1) / kRows8 * kRows8; }
 constexpr int kDec8MaxRows = 32;  // four row groups
-bool dec8_takes(const Handle* h, int M, bool dots, bool pair, bool multi) {
+bool dec8_takes(const Handle* h, int M, bool dots) {
     int max_rows = kDec8MaxRows;
     if (const char* r = std::getenv("BREEZE_HIP_DEC8_ROWS")) max_rows = std::min(kDec8MaxRows, std::max(5, std::atoi(r)));
-    if (M < 5 || M > max_rows || dots || pair || multi || h->extra) return false;
+    if (M < 5 || M > max_rows || dots || h->extra) return false;
     const char* f = std::getenv("BREEZE_HIP_DEC8");
     if (f && f[0] == '0') return false;
     if ((size_t)kRows8 * h->nblk4 / 4 > 2 * (size_t)kDecWaves * 64) return false;
@@ -1236,7 +1237,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // 16 rows 54.0 -> 30.6 (at 24 and 32 rows the GEMM took 167 us);
     // W4 K=5120 N=5120 at 12 rows 13.3 -> 14.1 is the one loss seen.
     // BREEZE_HIP_DEC8=0 keeps every call off it.
-    const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots, h2 != nullptr, mp != nullptr);
+    const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots);
     // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
     // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the
     // norm kernel then the projections; M = 2, 320 row-blocks: even).
@@ -1288,6 +1289,39 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     }
 
     hipError_t e;
+    if (mp) {
+        int t = 0;
+        for (int k = 0; k < kMaxSeg; ++k) {
+            if (k < mp->n) {
+                a.segW[k] = mp->h[k]->W;
+                a.segS[k] = mp->h[k]->S;
+                a.segC[k] = mp->C[k];
+                a.segN[k] = mp->h[k]->N;
+                t += mp->h[k]->N / 16;
+                a.seg_end[k] = t;
+            } else {
+                a.segW[k] = nullptr;
+                a.segS[k] = nullptr;
+                a.segC[k] = nullptr;
+                a.segN[k] = 0;
+                a.seg_end[k] = std::numeric_limits<int>::max();
+            }
+        }
+        a.ntiles = t;
+        a.normW = mp->normW;
+        a.normOut = mp->normOut;
+        a.norm_eps = mp->eps;
+        const char* ex = std::getenv("BREEZE_HIP_NORM_EXACT");
+        a.norm_exact = ex && ex[0] == '1';
+    }
+    const bool pair = h2 != nullptr;
+    if (pair) {
+        a.W2 = h2->W;
+        a.S2 = h2->S;
+        a.Z2 = h2->Z;
+        a.D2 = h2->D;
+    }
+    const int fz = pair ? kFusePair : mp ? (mp->norm ? kFuseNormMulti : kFuseMulti) : kFusePlain;
     // The decode kernels' in-kernel argmax merges into per-stream state
     // (a ticket, then kDecMaxRows row keys), zero between calls.
     if ((dec8 || dec) && dIdx) {
@@ -1327,37 +1361,12 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         const int grid = a.NG * a.RG;
         const int lds8 = dec8_lds(h->nblk, JG).total;
         const uint4* rec = reinterpret_cast<const uint4*>(s.aq);
-        bool* at = &w.dec8_attr[(h->bits == 8 ? 1 : 0) | (hp ? 2 : 0)];
-        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, st)
-                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, st);
-        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, st)
-                    : launch_dec8<4, false>(at, a, rec, grid, lds8, st);
+        bool* at = &w.dec8_attr[4 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
+        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, fz, st)
+                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, fz, st);
+        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, fz, st)
+                    : launch_dec8<4, false>(at, a, rec, grid, lds8, fz, st);
     } else if (dec) {
-        if (mp) {
-            int t = 0;
-            for (int k = 0; k < kMaxSeg; ++k) {
-                if (k < mp->n) {
-                    a.segW[k] = mp->h[k]->W;
-                    a.segS[k] = mp->h[k]->S;
-                    a.segC[k] = mp->C[k];
-                    a.segN[k] = mp->h[k]->N;
-                    t += mp->h[k]->N / 16;
-                    a.seg_end[k] = t;
-                } else {
-                    a.segW[k] = nullptr;
-                    a.segS[k] = nullptr;
-                    a.segC[k] = nullptr;
-                    a.segN[k] = 0;
-                    a.seg_end[k] = std::numeric_limits<int>::max();
-                }
-            }
-            a.ntiles = t;
-            a.normW = mp->normW;
-            a.normOut = mp->normOut;
-            a.norm_eps = mp->eps;
-            const char* ex = std::getenv("BREEZE_HIP_NORM_EXACT");
-            a.norm_exact = ex && ex[0] == '1';
-        }
         const int n_cu = device_cus(w, dev);
         a.RS = rs;
         a.RG = (M + rs - 1) / rs;
@@ -1369,16 +1378,8 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
             a.pair_xcd = ng % 8 == 0 ? 1 : 0;
             a.NG = ng;
         }
-        const bool pair = h2 != nullptr;
-        if (pair) {
-            a.W2 = h2->W;
-            a.S2 = h2->S;
-            a.Z2 = h2->Z;
-            a.D2 = h2->D;
-        }
         const int grid = a.NG * a.RG;
         const bool x = h->extra;
-        const int fz = pair ? kFusePair : mp ? (mp->norm ? kFuseNormMulti : kFuseMulti) : kFusePlain;
         if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)
                                  : launch_dec_bits<8, false>(w.attr_set, a, grid, lds, fz, p64, fused, x, st);
         else e = hp ? launch_dec_bits<4, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)

@@ -40,7 +40,7 @@ def _pair(hb, rng, N, K, bits, explicit_zeros, same_layout=True, grouped=False):
 
 @pytest.mark.parametrize("bits,explicit_zeros,grouped", [(4, False, True), (8, False, True),
                                                          (4, False, False), (4, True, False), (8, False, False)])
-@pytest.mark.parametrize("N,K", [(64, 224), (16 * 1029, 768), (512, 4096)])
+@pytest.mark.parametrize("N,K", [(64, 224), (16 * 1029, 768), (512, 4096), (16 * 100, 5120)])
 def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, bits, explicit_zeros, grouped, N, K):
     torch = gpu
     rng = np.random.default_rng(N + K + bits)
