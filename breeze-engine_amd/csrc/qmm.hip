@@ -1071,15 +1071,22 @@ constexpr int kNormFusedMaxBlocks = 3 * 128;  // with the RMSNorm in the prologu
 // The GEMM gains with the column tiles it can spread over the CUs, the
 // decode kernel loses with every row group re-reading the weights, so the
 // limit falls with the width, and with INT8 (twice the bytes per weight).
+// With row groups of eight (dec8_kernel; `eight`: the call is one it takes)
+// the decode side reads the weights half as often and its limit rises on
+// two widths, measured GEMM -> dec8_kernel (us): W8 K=5120 N=17408 (1088
+// tiles) at 16 rows 41.4 -> 35.4 (at 24 rows 42.7 -> 46.9), W4 K=5120
+// N=17408 at 32 rows 53.5 -> 46.7; and stays where it was on W8 K=5120
+// N=151936 (16 rows: 180 -> 244), W8 K=4096 N=12288 (24 rows: 32.9 ->
+// 45.8) and W4 K=5120 N=27648 (32 rows: 54.5 -> 69.2).
 // BREEZE_HIP_DEC_ROWS sets it (1..kDecMaxRows) for tests and tuning.
 constexpr int kDecMaxRows = 32, kDecMaxGroups = 8;
-int dec_max_rows(int bits, int ntiles, const char* force) {
+int dec_max_rows(int bits, int ntiles, bool eight, const char* force) {
     if (force) {
         const int v = std::atoi(force);
         if (v >= 1 && v <= kDecMaxRows) return v;
     }
-    if (bits == 8) return ntiles >= 1024 ? 12 : ntiles > 512 ? 16 : 32;
-    return ntiles > 768 ? 24 : 32;
+    if (bits == 8) return ntiles >= (eight ? 2048 : 1024) ? 12 : ntiles > 512 ? 16 : 32;
+    return ntiles > (eight ? 1536 : 768) ? 24 : 32;
 }
 
 int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG, bool p64 = false) {
@@ -1204,8 +1211,12 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     const bool p64 = lds_p64 > 0;
     // The paired and multi-projection calls take row groups of 4, at most 16
     // rows.
+    // Past four rows the row groups quantize in their prologue only when
+    // four rows of K fit one prologue's blocks; otherwise dec8_kernel takes
+    // the call if it can.
+    const bool eight = 4 * h->nblk > kFusedMaxBlocks && dec8_takes(h, kRows8, dots);
     const int dec_rows = std::min((h2 || mp) ? 16 : kDecMaxRows,
-                                  dec_max_rows(h->bits, a.ntiles, std::getenv("BREEZE_HIP_DEC_ROWS")));
+                                  dec_max_rows(h->bits, a.ntiles, eight, std::getenv("BREEZE_HIP_DEC_ROWS")));
     int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     // Rows per row group: 4, or 2 or 1 where four rows of records do not
     // fit (long K: the staged copy holds 1536 row-blocks, so two rows reach

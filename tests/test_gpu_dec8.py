@@ -152,3 +152,23 @@ def test_dec8_argmax(gpu, hb, orc, hi_prec, bits, hp):
             assert idx.cpu().numpy().tolist() == [5] * M, case
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("bits,rows", [(8, 16), (4, 32)])
+def test_dec8_wide_limit(gpu, hb, orc, hi_prec, bits, rows):
+    """The widths where the eight-row groups take more rows than the
+    four-row groups did before the GEMM: W8 at 1088 tiles up to 16 rows, W4
+    at 1088 tiles up to 32."""
+    rng = np.random.default_rng(50 + bits)
+    K, N = 5120, 17408
+    nblk = K // 32
+    qw, sc, _ = rng_weights(rng, N, K, bits)
+    sc = np.ascontiguousarray(np.repeat(sc[:, :1], nblk, axis=1))
+    A = rng.normal(size=(rows, K)).astype(np.float32)
+    hb.set_hi_prec(True)
+    h = hb.prepack(qw, sc, None, K, N, bits=bits)
+    try:
+        want = orc.matmul(qw, sc, None, N, K, bits, A, True)
+        assert bits_equal(_run(hb, gpu, h, A, N), want)
+    finally:
+        hb.free(h)
