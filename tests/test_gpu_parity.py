@@ -495,13 +495,16 @@ def test_non_finite_and_extreme_activations(gpu, hb, orc, hi_prec, monkeypatch, 
             hb.free(h)
 
 
+@pytest.mark.parametrize("dec8", ["on", "off"])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_decode_staged_rows_with_argmax(gpu, hb, orc, hi_prec, bits):
-    """Four to eight rows whose records come from the stand-alone quantizer
-    (K = 4640: 145 blocks, a partial last chunk; five to eight rows in two
-    row-group workgroups per tile range): outputs bit-exact and the argmax
-    of every row first-max exact, several tiles per workgroup
-    (N = 16 * 600)."""
+def test_decode_staged_rows_with_argmax(gpu, hb, orc, hi_prec, monkeypatch, bits, dec8):
+    """Four to eight rows whose records come from the stand-alone quantizers
+    (K = 4640: 145 blocks, a partial last chunk; five to eight rows in one
+    eight-row workgroup per tile range, or with BREEZE_HIP_DEC8=0 in two
+    four-row ones): outputs bit-exact and the argmax of every row first-max
+    exact, several tiles per workgroup (N = 16 * 600)."""
+    if dec8 == "off":
+        monkeypatch.setenv("BREEZE_HIP_DEC8", "0")
     N, K = 16 * 600, 4640
     rng = np.random.default_rng(60 + bits)
     qw, sc, _ = rng_weights(rng, N, K, bits)
@@ -521,14 +524,19 @@ def test_decode_staged_rows_with_argmax(gpu, hb, orc, hi_prec, bits):
         hb.free(h)
 
 
+@pytest.mark.parametrize("dec8", ["on", "off"])
 @pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
-def test_decode_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros):
-    """9 to 32 rows through the decode kernel (three to eight workgroups of 4
-    rows per tile range, on one XCD when the range count allows; the limit
-    forced to 32), outputs and argmax against the oracle: K = 4608 (staged
-    records, 40 tiles: row groups placed on one XCD) and K = 96 (the prologue
-    quantizes; 20 tiles: the plain block order)."""
+def test_decode_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros, dec8):
+    """9 to 32 rows through the decode kernels' row groups (two to four
+    workgroups of 8 rows, or with BREEZE_HIP_DEC8=0 or explicit zero points
+    three to eight of 4 rows, per tile range, on one XCD when the range
+    count allows; the limit forced to 32), outputs and argmax against the
+    oracle: K = 4608 (staged records, 40 tiles: row groups placed on one
+    XCD) and K = 96 (the four-row groups quantize in their prologue; 20
+    tiles: the plain block order)."""
     monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "32")
+    if dec8 == "off":
+        monkeypatch.setenv("BREEZE_HIP_DEC8", "0")
     rng = np.random.default_rng(31)
     for K, N in ((4608, 640), (96, 320)):
         qw, sc, qz = rng_weights(rng, N, K, bits, explicit_zeros=explicit_zeros)
@@ -548,12 +556,16 @@ def test_decode_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_ze
             hb.free(h)
 
 
+@pytest.mark.parametrize("dec8", ["on", "off"])
 @pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
-def test_decode_two_row_groups_long_k(gpu, hb, orc, hi_prec, bits, explicit_zeros):
-    """K = 17408 (544 blocks): four rows of records exceed the decode
-    kernel's staged copy, so 3 to 16 rows run as workgroups of 2 rows (the
-    MLP down projection at decode batch sizes), outputs and argmax against
-    the oracle, default routing."""
+def test_decode_two_row_groups_long_k(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros, dec8):
+    """K = 17408 (544 blocks, the MLP down projection at decode batch sizes):
+    four rows of records exceed the four-row kernel's staged copy, so 3 to 16
+    rows run as its workgroups of 2 rows, except 5-16 rows of handles
+    without per-block metadata, which take the eight-row groups unless
+    BREEZE_HIP_DEC8=0.  Outputs and argmax against the oracle."""
+    if dec8 == "off":
+        monkeypatch.setenv("BREEZE_HIP_DEC8", "0")
     rng = np.random.default_rng(37)
     K, N = 17408, 320
     qw, sc, qz = rng_weights(rng, N, K, bits, explicit_zeros=explicit_zeros)
@@ -573,11 +585,16 @@ def test_decode_two_row_groups_long_k(gpu, hb, orc, hi_prec, bits, explicit_zero
         hb.free(h)
 
 
+@pytest.mark.parametrize("dec8", ["on", "off"])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_decode_one_row_groups_longer_k(gpu, hb, orc, hi_prec, bits):
-    """K = 26624 (832 blocks): even two rows of records exceed the decode
-    kernel's staged copy, so 2 to 8 rows run as workgroups of one row; more
-    rows take the GEMM.  Outputs and argmax against the oracle."""
+def test_decode_one_row_groups_longer_k(gpu, hb, orc, hi_prec, monkeypatch, bits, dec8):
+    """K = 26624 (832 blocks): even two rows of records exceed the four-row
+    kernel's staged copy, so 2 to 4 rows run as its workgroups of one row;
+    5 to 9 rows take the eight-row groups (with BREEZE_HIP_DEC8=0: one-row
+    workgroups up to 8 rows, the GEMM at 9).  Outputs and argmax against
+    the oracle."""
+    if dec8 == "off":
+        monkeypatch.setenv("BREEZE_HIP_DEC8", "0")
     rng = np.random.default_rng(41)
     K, N = 26624, 160
     qw, sc, qz = rng_weights(rng, N, K, bits)
