@@ -1215,7 +1215,9 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // four rows of K fit one prologue's blocks; otherwise dec8_kernel takes
     // the call if it can.
     const bool eight = 4 * h->nblk > kFusedMaxBlocks && dec8_takes(h, kRows8, dots);
-    const int dec_rows = std::min((h2 || mp) ? 16 : kDecMaxRows,
+    // The paired and multi-projection calls take up to 16 rows on the
+    // four-row groups and up to 32 on the eight-row groups.
+    const int dec_rows = std::min((h2 || mp) ? (eight ? kDec8MaxRows : 16) : kDecMaxRows,
                                   dec_max_rows(h->bits, a.ntiles, eight, std::getenv("BREEZE_HIP_DEC_ROWS")));
     int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
     // Rows per row group: 4, or 2 or 1 where four rows of records do not
@@ -1232,7 +1234,6 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         }
     }
     const bool dec = lds > 0;
-    if ((h2 || mp) && !dec) return kNotPairable;
     if (mp && (h->extra || dIdx)) return kNotPairable;
     const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
     // 5-32 rows of a plain call, up to the decode kernel's row limit, whose
@@ -1249,6 +1250,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // W4 K=5120 N=5120 at 12 rows 13.3 -> 14.1 is the one loss seen.
     // BREEZE_HIP_DEC8=0 keeps every call off it.
     const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots);
+    if ((h2 || mp) && !(dec8 || (dec && M <= 16))) return kNotPairable;
     // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
     // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the
     // norm kernel then the projections; M = 2, 320 row-blocks: even).

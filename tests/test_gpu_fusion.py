@@ -6,8 +6,9 @@ Both projections are the exact path (bit-identical to the oracle), so the
 result is compared with the oracle's projections through float32 SiLU and
 product: the only difference allowed is exp's last-place rounding (the
 device expf against numpy's), bounded here at 1e-6 relative.  The one-launch
-path (M <= 16, handles of the same layout) and the two-launch fallback use the
-same device arithmetic and must agree bit for bit."""
+path (handles of the same layout; up to 16 rows on the four-row groups, 32 on
+the eight-row groups) and the two-launch fallback use the same device
+arithmetic and must agree bit for bit."""
 import numpy as np
 import pytest
 
@@ -41,7 +42,8 @@ def _pair(hb, rng, N, K, bits, explicit_zeros, same_layout=True, grouped=False):
 @pytest.mark.parametrize("bits,explicit_zeros,grouped", [(4, False, True), (8, False, True),
                                                          (4, False, False), (4, True, False), (8, False, False)])
 @pytest.mark.parametrize("N,K", [(64, 224), (16 * 1029, 768), (512, 4096), (16 * 100, 5120)])
-def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, bits, explicit_zeros, grouped, N, K):
+def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros, grouped,
+                                               N, K):
     torch = gpu
     rng = np.random.default_rng(N + K + bits)
     (qg, sg, zg), (qu, su, zu), hg, hu = _pair(hb, rng, N, K, bits, explicit_zeros, grouped=grouped)
@@ -59,11 +61,18 @@ def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, bits, expl
                 got = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A[:rows]).cuda(), N).cpu().numpy()
                 np.testing.assert_allclose(got, want[:rows], rtol=1e-6, atol=1e-30, err_msg=f"{rows} rows")
                 fused[rows] = got
-            # Twenty rows take the two-launch fallback: same bits as one-launch rows.
+            # Twenty rows: one launch where the eight-row groups take the
+            # call (K past 4096, no per-block metadata), else the two-launch
+            # fallback, which BREEZE_HIP_DEC8=0 forces; every way gives the
+            # bits of the one-launch rows.
             got20 = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A).cuda(), N).cpu().numpy()
+            monkeypatch.setenv("BREEZE_HIP_DEC8", "0")
+            two = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A).cuda(), N).cpu().numpy()
+            monkeypatch.delenv("BREEZE_HIP_DEC8")
             torch.cuda.synchronize()
             assert bits_equal(got20[:16], fused[16]), hp
             assert bits_equal(got20[:1], fused[1]), hp
+            assert bits_equal(two, got20), hp
             np.testing.assert_allclose(got20, want, rtol=1e-6, atol=1e-30)
     finally:
         hb.free(hg)

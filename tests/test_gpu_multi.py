@@ -3,9 +3,9 @@ against the oracle, bit for bit: the Qwen3.5-27B decoder's in_qkv, in_z,
 in_b, in_a (kernel/qwen35_decoder.cpp:285-288; K = 5120, N = 10240, 6144,
 48, 48) and q, k, v (334-336; N = 12288, 1024, 1024), odd widths whose
 segment boundaries fall inside workgroups, a partial last chunk, one to
-sixteen rows (one to four row groups), and the shapes that fall back to one
-launch per projection (mixed bits, explicit zero points, more than 16
-rows)."""
+thirty-two rows (row groups of four up to 16 rows, of eight from 5), and the
+shapes that fall back to one launch per projection (mixed bits, explicit
+zero points, more than 16 rows that only the four-row groups could take)."""
 import numpy as np
 import pytest
 
@@ -39,7 +39,7 @@ def test_multi_projection_bit_exact(gpu, hb, orc, hi_prec, shape, bits):
     try:
         for hp in (True, False):
             hb.set_hi_prec(hp)
-            for M in (1, 2, 3, 5, 8, 12, 16):
+            for M in (1, 2, 3, 5, 8, 12, 16, 24, 32):
                 A = rng.normal(size=(M, K)).astype(np.float32)
                 A[rng.random(A.shape) < 0.01] *= 20.0
                 print(f"multi {shape} bits={bits} hp={hp} M={M}", flush=True)
