@@ -44,12 +44,17 @@ __host__ __device__ inline Dec8Lds dec8_lds(int nblk, int JG) {
     return l;
 }
 
-// Per-lane record bytes of one chunk: JG blocks of 8 bytes.
-template <int JG>
+// One weight chunk of a producer with its activation records (JG blocks of
+// 8 bytes per lane) and per-column metadata: one scale, or for EXTRA
+// handles (explicit zero points, legacy corr, scale groups smaller than a
+// chunk) the chunk's per-block scales, corr deltas and INT4 zero points.
+template <int JG, bool EXTRA>
 struct Unit8 {
     uint4 w;
     uint4 a[JG / 2];
-    float sc;
+    float sc[EXTRA ? JG : 1];
+    int dl[EXTRA ? JG : 1];
+    uint32_t zp;
     int c;  // chunk to compute; nbg or more: none (past the end)
 };
 
@@ -58,7 +63,7 @@ struct Unit8 {
 // (RG row groups of eight rows; xcd: the RG workgroups of a tile range share
 // an XCD).  pM is all rows of the call.  Tiles: the first rem_t tile ranges
 // own base_t + 1, the rest base_t.
-template <int BITS, bool HP, int FUSE>
+template <int BITS, bool HP, bool EXTRA, int FUSE>
 __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, const float* pS, const uint4* pR,
                                                               int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
                                                               int pngrp, int misc, GemvArgs args) {
@@ -126,7 +131,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     const int col = lane & 15, grp = lane >> 4;
 
     // Rows land at the padded pitch; sums of q premultiplied by -8 (the
-    // default zero point).  Threads past the end rewrite the last element.
+    // default zero point) or by -1 (EXTRA: times each block's zero point in
+    // the epilogue).  Threads past the end rewrite the last element.
     auto store_meta = [&]() {
         const int pad = (lay.sa_pitch - nblk4) >> 2;
         auto put = [&](int i, const uint4& va, const uint4& vq) {
@@ -137,7 +143,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
             const int d = i + m * pad;
             reinterpret_cast<uint4*>(sa_l)[d] = va;
             if (BITS == 4) {
-                const uint32_t f = 0xFFFFFFF8u;  // -8
+                const uint32_t f = EXTRA ? 0xFFFFFFFFu : 0xFFFFFFF8u;  // -1 or -8
                 reinterpret_cast<uint4*>(sq_l)[d] = make_uint4(f * vq.x, f * vq.y, f * vq.z, f * vq.w);
             }
         };
@@ -164,21 +170,35 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     const float* ls = MULTI ? args.segS[ld_k] : pS;
     uint32_t ld_w = (uint32_t)(t_begin - t_off) * nbg * 64;
     uint32_t ld_s = (uint32_t)(t_begin - t_off) * pngrp * 16;
+    uint32_t ld_m = (uint32_t)t_begin * nbg * 16;  // per-block metadata (EXTRA)
     const int pf_c = nbg + kP8 + wave;
     const bool pf = !PAIR && !MULTI && npw >= 2 && wave + kP8 < nbg;
     int ld_idle = (pf && nT > 1) ? pf_c : nbg - 1;
-    auto load_unit = [&](Unit8<JG>& p) {
+    auto load_unit = [&](Unit8<JG, EXTRA>& p) {
         const int c = min(ld_c, nbg - 1);
         const int cw = ld_c < nbg ? ld_c : ld_idle;
         uint32_t wi = ld_w + cw * 64 + lane;
         uint32_t si = ld_s + (uint32_t)((c * JG) >> sc_shift) * 16 + col;
         uint32_t ri = (uint32_t)c * (NA * 64) + lane;
-        asm("" : "+v"(wi), "+v"(si), "+v"(ri));
+        uint32_t mi = ld_m + c * 16 + col;
+        asm("" : "+v"(wi), "+v"(si), "+v"(ri), "+v"(mi));
         const bool up = PAIR && ld_sel;
         p.w = (up ? args.W2 : lw)[wi];
 #pragma unroll
         for (int h = 0; h < NA; ++h) p.a[h] = pR[ri + 64 * h];
-        p.sc = (up ? args.S2 : ls)[si];
+        if constexpr (EXTRA) {
+            typedef int ivec __attribute__((ext_vector_type(JG)));
+            const fvec sv = *reinterpret_cast<const fvec*>((up ? args.S2 : args.S) + (size_t)mi * JG);
+            const ivec dv = *reinterpret_cast<const ivec*>((up ? args.D2 : args.D) + (size_t)mi * JG);
+#pragma unroll
+            for (int jb = 0; jb < JG; ++jb) {
+                p.sc[jb] = sv[jb];
+                p.dl[jb] = dv[jb];
+            }
+            if (JG == 4) p.zp = *reinterpret_cast<const uint32_t*>((up ? args.Z2 : args.Z) + (size_t)mi * 4);
+        } else {
+            p.sc[0] = (up ? args.S2 : ls)[si];
+        }
         p.c = ld_c;
         ld_c += kP8;
         if (--ld_rem == 0) {
@@ -192,6 +212,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
                     ld_c = wave;
                     ld_w += nbg * 64;
                     ld_s += pngrp * 16;
+                    ld_m += nbg * 16;
                     if (MULTI && t_begin + ld_t == args.seg_end[ld_k]) {
                         ++ld_k;
                         lw = args.segW[ld_k];
@@ -320,7 +341,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     }
 
     // ================= producers (waves 0..13)
-    Unit8<JG> ring[R];
+    Unit8<JG, EXTRA> ring[R];
 #pragma unroll
     for (int d = 0; d < R; ++d) load_unit(ring[d]);
     __builtin_amdgcn_sched_barrier(0);
@@ -335,10 +356,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     const int k64s = (lane & 3) == 1 ? 0x40404040 : 0;
     const v4i k64 = v4i{k64s, k64s, k64s, k64s};
 
-    auto consume = [&](const Unit8<JG>& cur, int buf) {
+    auto consume = [&](const Unit8<JG, EXTRA>& cur, int buf) {
         const int c = cur.c;
         if (c >= nbg) return;
-        // -zp * sum(q) of rows 2 grp and 2 grp + 1 (INT4).
+        // -8 * sum(q) (or -sum(q) with EXTRA) of rows 2 grp and 2 grp + 1
+        // (INT4).
         int4 z0 = make_int4(0, 0, 0, 0), z1 = z0;
         if (BITS == 4) {
             z0 = *reinterpret_cast<const int4*>(sq0 + c * 4);
@@ -356,6 +378,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
             if (BITS == 4) {
                 e0 = jb == 0 ? z0.x : jb == 1 ? z0.y : jb == 2 ? z0.z : z0.w;
                 e1 = jb == 0 ? z1.x : jb == 1 ? z1.y : jb == 2 ? z1.z : z1.w;
+                if (EXTRA) {
+                    const int zp = (int)(int8_t)(cur.zp >> (8 * jb));  // the block's zero point
+                    e0 *= zp;
+                    e1 *= zp;
+                }
+            }
+            if (EXTRA) {
+                // The legacy corr delta, in units of the part-1 (low byte)
+                // dot: 256 of them per unit of the two-pass product.
+                const int d = (HP ? 256 : 1) * cur.dl[EXTRA ? jb : 0];
+                e0 += d;
+                e1 += d;
             }
             const v4i dd = mfma16(aop, bop);
             int cs0 = dd[0] + e0, cs1 = dd[2] + e1;
@@ -373,8 +407,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
                 cs0 = dd[0] * 256 + dd[1] + (s128 + e0);
                 cs1 = dd[2] * 256 + dd[3] + (s128 + e1);
             }
-            f0[jb] = (float)cs0 * cur.sc;
-            f1[jb] = (float)cs1 * cur.sc;
+            const float sc = cur.sc[EXTRA ? jb : 0];
+            f0[jb] = (float)cs0 * sc;
+            f1[jb] = (float)cs1 * sc;
         }
         *reinterpret_cast<fvec*>(fout + (buf * 2) * 64 * PP) = f0;
         *reinterpret_cast<fvec*>(fout + (buf * 2 + 1) * 64 * PP) = f1;
@@ -392,14 +427,15 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     }
 }
 
-template <int BITS, bool HP, int FUSE>
+template <int BITS, bool HP, bool EXTRA, int FUSE>
 hipError_t launch_dec8_f(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, hipStream_t st) {
-    auto kern = dec8_kernel<BITS, HP, FUSE>;
-    if (!attr_set[FUSE]) {
+    auto kern = dec8_kernel<BITS, HP, EXTRA, FUSE>;
+    bool& set = attr_set[FUSE + (EXTRA ? 3 : 0)];
+    if (!set) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
         if (e != hipSuccess) return e;
-        attr_set[FUSE] = true;
+        set = true;
     }
     const int npw = (a.nbg + kP8 - 1) / kP8;
     const int misc = a.sc_shift | a.RG << 8 | a.pair_xcd << 12 | npw << 16;
@@ -408,14 +444,22 @@ hipError_t launch_dec8_f(bool* attr_set, const GemvArgs& a, const uint4* rec, in
     return hipGetLastError();
 }
 
-// attr_set: this device's flags for the (bits, mode) pair, one per FUSE mode.
+// attr_set: this device's flags for the (bits, mode) pair, one per (FUSE
+// mode, per-block metadata) variant.  Handles with per-block metadata take
+// the plain and paired calls (the multi-projection launch sends them one by
+// one).
 template <int BITS, bool HP>
-hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, int fuse,
+hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, int fuse, bool extra,
                        hipStream_t st) {
-    if (fuse == kFusePair) return launch_dec8_f<BITS, HP, kFusePair>(attr_set, a, rec, grid, lds, st);
-    if (fuse == kFuseMulti) return launch_dec8_f<BITS, HP, kFuseMulti>(attr_set, a, rec, grid, lds, st);
+    if (extra) {
+        if (fuse == kFusePair) return launch_dec8_f<BITS, HP, true, kFusePair>(attr_set, a, rec, grid, lds, st);
+        if (fuse != kFusePlain) return hipErrorInvalidValue;
+        return launch_dec8_f<BITS, HP, true, kFusePlain>(attr_set, a, rec, grid, lds, st);
+    }
+    if (fuse == kFusePair) return launch_dec8_f<BITS, HP, false, kFusePair>(attr_set, a, rec, grid, lds, st);
+    if (fuse == kFuseMulti) return launch_dec8_f<BITS, HP, false, kFuseMulti>(attr_set, a, rec, grid, lds, st);
     if (fuse != kFusePlain) return hipErrorInvalidValue;
-    return launch_dec8_f<BITS, HP, kFusePlain>(attr_set, a, rec, grid, lds, st);
+    return launch_dec8_f<BITS, HP, false, kFusePlain>(attr_set, a, rec, grid, lds, st);
 }
 
 }  // namespace bq

@@ -784,7 +784,7 @@ struct Workspace {
     hipStream_t stream = nullptr;
     int n_cu = 0;
     bool attr_set[256] = {};  // decode kernel variants with the kernel attribute set
-    bool dec8_attr[16] = {};  // the same for dec8_kernel, per (bits, mode) and FUSE mode
+    bool dec8_attr[32] = {};  // the same for dec8_kernel, per (bits, mode) and (FUSE mode, metadata)
     bool pf_attr[256] = {};
 };
 
@@ -1112,18 +1112,18 @@ int device_cus(Workspace& w, int dev) {
     return w.n_cu;
 }
 
-// Whether the decode kernel in row groups of eight takes a call: one
-// without the block-integer export (plain, argmax, gate/up pair or
-// multi-projection; the caller's own limits apply to the last two) of a
-// handle without per-block metadata, with its eight rows' block scales and
-// sums within two uint4 per thread and its LDS plan within the limit.
 // Rows of the eight-row groups that take M rows (M rounded up to 8).
 int dec8_rows(int M) { return (M + kRows8 - 1) / kRows8 * kRows8; }
 constexpr int kDec8MaxRows = 32;  // four row groups
+// Whether the decode kernel in row groups of eight takes a call: one
+// without the block-integer export (plain, argmax, gate/up pair or
+// multi-projection; the caller's own limits apply to the last two), with
+// its eight rows' block scales and sums within two uint4 per thread and its
+// LDS plan within the limit.
 bool dec8_takes(const Handle* h, int M, bool dots) {
     int max_rows = kDec8MaxRows;
     if (const char* r = std::getenv("BREEZE_HIP_DEC8_ROWS")) max_rows = std::min(kDec8MaxRows, std::max(5, std::atoi(r)));
-    if (M < 5 || M > max_rows || dots || h->extra) return false;
+    if (M < 5 || M > max_rows || dots) return false;
     const char* f = std::getenv("BREEZE_HIP_DEC8");
     if (f && f[0] == '0') return false;
     if ((size_t)kRows8 * h->nblk4 / 4 > 2 * (size_t)kDecWaves * 64) return false;
@@ -1374,11 +1374,12 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         const int grid = a.NG * a.RG;
         const int lds8 = dec8_lds(h->nblk, JG).total;
         const uint4* rec = reinterpret_cast<const uint4*>(s.aq);
-        bool* at = &w.dec8_attr[4 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
-        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, fz, st)
-                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, fz, st);
-        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, fz, st)
-                    : launch_dec8<4, false>(at, a, rec, grid, lds8, fz, st);
+        bool* at = &w.dec8_attr[8 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
+        const bool x = h->extra;
+        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, fz, x, st)
+                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, fz, x, st);
+        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, fz, x, st)
+                    : launch_dec8<4, false>(at, a, rec, grid, lds8, fz, x, st);
     } else if (dec) {
         const int n_cu = device_cus(w, dev);
         a.RS = rs;

@@ -172,3 +172,50 @@ def test_dec8_wide_limit(gpu, hb, orc, hi_prec, bits, rows):
         assert bits_equal(_run(hb, gpu, h, A, N), want)
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("kind", ["zeros", "group2", "legacy4", "legacy8"])
+def test_dec8_per_block_metadata(gpu, hb, orc, hi_prec, kind):
+    """Handles with per-block metadata through the eight-row groups (K past
+    4096, 5 to 32 rows): explicit INT4 zero points (the block's zero point
+    times -sum(q) of the row), INT4 scales per two blocks (smaller than a
+    chunk, so per-block scales), and legacy handles whose corr disagrees with
+    the weights (the corr delta, 256 per unit in the two-pass mode), INT4
+    with zero points and INT8.  Both activation modes, against the oracle
+    and against the four-row groups (BREEZE_HIP_DEC8=0)."""
+    rng = np.random.default_rng(sum(map(ord, kind)))
+    N, K = 80, 4640
+    nblk = K // 32
+    if kind in ("zeros", "group2"):
+        bits = 4
+        qw, sc, qz = rng_weights(rng, N, K, 4, explicit_zeros=kind == "zeros")
+        if kind == "group2":
+            sc = np.ascontiguousarray(np.repeat(sc[:, ::2], 2, axis=1)[:, :nblk])
+        h = hb.prepack(qw, sc, qz, K, N, bits=4)
+        want_of = lambda A, hp: orc.matmul(qw, sc, qz, N, K, 4, A, hp)
+    else:
+        bits = 4 if kind == "legacy4" else 8
+        gb = 64 if bits == 8 else 32
+        B = rng.integers(0, 256, (N // 16, nblk, 8, gb), dtype=np.uint8)
+        scale = rng.uniform(0.001, 0.02, (N // 16, nblk, 16)).astype(np.float32)
+        zp = rng.integers(0, 16, (N // 16, nblk, 16), dtype=np.int8) if bits == 4 else None
+        corr = rng.integers(-5000, 5000, (N // 16, nblk, 16), dtype=np.int32)
+        h = hb._lib.i4_prepack(hb._p(B), hb._p(scale), hb._p(zp), hb._p(corr), N, K, nblk, bits)
+        assert h, hb.last_error()
+        want_of = lambda A, hp: orc.matmul_legacy(B, scale, zp, corr, N, K, bits, A, hp)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for M in (5, 8, 17, 32):
+                A = rng.normal(size=(M, K)).astype(np.float32)
+                A[rng.random(A.shape) < 0.01] *= 20.0
+                case = dict(kind=kind, hp=hp, M=M)
+                want = want_of(A, hp)
+                assert bits_equal(_run(hb, gpu, h, A, N), want), case
+                os.environ["BREEZE_HIP_DEC8"] = "0"
+                try:
+                    assert bits_equal(_run(hb, gpu, h, A, N), want), case
+                finally:
+                    del os.environ["BREEZE_HIP_DEC8"]
+    finally:
+        hb.free(h)
