@@ -20,8 +20,8 @@ namespace bq {
 // quantizer writes in that operand order ([chunk][JG / 2][64 lanes][16 B]),
 // not through LDS: eight rows of K = 12288 are 192 KB.  The bias term
 // 128 * sum(b) of the two-pass product, which the four-row kernel takes from
-// two constant A rows, comes from a second MFMA per block
-// (v_mfma_i32_16x16x64_i8 of a constant A operand and the B octets twice).
+// two constant A rows, comes from a second MFMA per block of a constant A
+// operand with the same B operand.
 constexpr int kP8 = 14;
 constexpr int kRows8 = 8;
 
@@ -351,10 +351,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     const int* sq0 = sq_l + (2 * grp) * lay.sa_pitch;
     const int* sq1 = sq0 + lay.sa_pitch;
     float* const fout = fbuf + lane * PP + wave * JG;
-    // Constant A operand of the bias MFMA: rows 4 g + 1 all 64, the others
-    // zero.
-    const int k64s = (lane & 3) == 1 ? 0x40404040 : 0;
-    const v4i k64 = v4i{k64s, k64s, k64s, k64s};
+    // Constant A operand of the bias MFMA: rows 4 g + 1 and 4 g + 3 (odd
+    // lanes' rows) all 64, the others zero.
+    const long k64 = (lane & 1) ? 0x4040404040404040l : 0l;
 
     auto consume = [&](const Unit8<JG, EXTRA>& cur, int buf) {
         const int c = cur.c;
@@ -394,16 +393,15 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
             const v4i dd = mfma16(aop, bop);
             int cs0 = dd[0] + e0, cs1 = dd[2] + e1;
             if constexpr (HP) {
-                // 128 * sum(b) from a 16x16x64 MFMA of the constant A
-                // operand (rows 4 g + 1 all 64) with this lane's k-octet
-                // twice as B: every output lane's result 1 is 64 * 2 *
-                // sum(b) of its column.  Both MFMAs take a zero accumulator
-                // input and the sums are VALU adds (an MFMA result fed
-                // straight into the next MFMA's accumulator input was
-                // allocated with partial register overlaps).
-                const v4i bb = v4i{(int)(uint32_t)bop, (int)(uint32_t)(bop >> 32), (int)(uint32_t)bop,
-                                   (int)(uint32_t)(bop >> 32)};
-                const int s128 = __builtin_amdgcn_mfma_i32_16x16x64_i8(k64, bb, v4i{0, 0, 0, 0}, 0, 0, 0)[1];
+                // 128 * sum(b) from a 16x16x32 MFMA of the constant A
+                // operand (rows 4 g + 1 and 4 g + 3 all 64) with the same B
+                // operand: results 1 and 3 of every output lane are each
+                // 64 * sum(b) of its column.  Both MFMAs take a zero
+                // accumulator input and the sums are VALU adds (an MFMA
+                // result fed straight into the next MFMA's accumulator input
+                // was allocated with partial register overlaps).
+                const v4i bs = __builtin_amdgcn_mfma_i32_16x16x32_i8(k64, (long)bop, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const int s128 = bs[1] + bs[3];
                 cs0 = dd[0] * 256 + dd[1] + (s128 + e0);
                 cs1 = dd[2] * 256 + dd[3] + (s128 + e1);
             }
