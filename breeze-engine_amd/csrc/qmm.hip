@@ -1077,7 +1077,14 @@ constexpr int kNormFusedMaxBlocks = 3 * 128;  // with the RMSNorm in the prologu
 // tiles) at 16 rows 41.4 -> 35.4 (at 24 rows 42.7 -> 46.9), W4 K=5120
 // N=17408 at 32 rows 53.5 -> 46.7; and stays where it was on W8 K=5120
 // N=151936 (16 rows: 180 -> 244), W8 K=4096 N=12288 (24 rows: 32.9 ->
-// 45.8) and W4 K=5120 N=27648 (32 rows: 54.5 -> 69.2).
+// 45.8) and W4 K=5120 N=27648 (32 rows: 54.5 -> 69.2).  From 2048 W8 tiles
+// the GEMM takes 9 rows and more (argmax calls): W8 K=5120 N=151936 at 9 /
+// 12 rows 193.8 / 188.8 us against 245.2 / 247.1, K=4096 N=151936 159.0 /
+// 159.7 against 253.9 / 253.4 (four-row groups), K=5120 N=65536 99.7 /
+// 100.6 against 111.1 / 111.3.  W4 past 1536 tiles stops at 16 rows on
+// the eight-row groups: K=5120 N=151936 at 16 / 24 rows 191.6 / 293.0 us
+// against the GEMM's 277.0 / 285.3, N=65536 90.7 / 128.3 against 97.5 /
+// 101.5.
 // BREEZE_HIP_DEC_ROWS sets it (1..kDecMaxRows) for tests and tuning.
 constexpr int kDecMaxRows = 32, kDecMaxGroups = 8;
 int dec_max_rows(int bits, int ntiles, bool eight, const char* force) {
@@ -1085,8 +1092,9 @@ int dec_max_rows(int bits, int ntiles, bool eight, const char* force) {
         const int v = std::atoi(force);
         if (v >= 1 && v <= kDecMaxRows) return v;
     }
-    if (bits == 8) return ntiles >= (eight ? 2048 : 1024) ? 12 : ntiles > 512 ? 16 : 32;
-    return ntiles > (eight ? 1536 : 768) ? 24 : 32;
+    if (bits == 8) return ntiles >= 2048 ? 8 : ntiles >= 1024 ? (eight ? 16 : 12) : ntiles > 512 ? 16 : 32;
+    if (eight) return ntiles > 1536 ? 16 : 32;
+    return ntiles > 768 ? 24 : 32;
 }
 
 int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG, bool p64 = false) {
