@@ -2,8 +2,9 @@
 allocating device entry points, through the C ABI, bit for bit: each case
 makes two calls in a row, the second with a smaller input, so the second
 runs on the scratch contents the first left behind.  Cases cover every
-kernel route that uses scratch: the decode kernel with staged activation
-records, the decode argmax state, the prefill GEMM's records, the rows
+kernel route that uses scratch: the decode kernels with staged activation
+records (four-row groups, and eight-row groups at 24 then 9 rows), the
+decode argmax state, the prefill GEMM's records, the rows
 kernel (legacy corr) and the argmax partials after it; plus a shape that
 needs no scratch and one too large for the fixed scratch, which is refused.
 """
@@ -39,7 +40,8 @@ def _reference_call(hb, torch, h, A, N, argmax):
     return c.cpu().numpy(), None
 
 
-@pytest.mark.parametrize("case", ["fused", "staged", "argmax", "row_groups_argmax", "prefill", "prefill_argmax"])
+@pytest.mark.parametrize("case", ["fused", "staged", "argmax", "row_groups_argmax", "eight_row_groups", "prefill",
+                                  "prefill_argmax"])
 @pytest.mark.parametrize("bits", [4, 8])
 def test_noalloc_matches_allocating_entry(gpu, hb, hi_prec, case, bits):
     torch = gpu
@@ -48,6 +50,7 @@ def test_noalloc_matches_allocating_entry(gpu, hb, hi_prec, case, bits):
         "staged": (4608, 256, (8, 4), False),
         "argmax": (1024, 16 * 600, (2, 1), True),
         "row_groups_argmax": (1024, 16 * 320, (16, 12), True),
+        "eight_row_groups": (4608, 256, (24, 9), True),
         "prefill": (1056, 304, (130, 20), False),
         "prefill_argmax": (640, 16 * 300, (40, 17), True),
     }[case]
