@@ -28,21 +28,25 @@ constexpr int kRows8 = 8;
 // LDS: block scales and (INT4) -zp * sum(q) of the eight rows, row pitch
 // padded 16 B past a multiple of 256 B (the four rows a fold or epilogue
 // reads together fall on different banks), then the phase buffer
-// [2 buffers][2 rows][64 lanes][dec_pitch(JG)] of f values.
+// [2 buffers][2 rows][64 lanes][dec_pitch(JG)] of f values, then (LREC) the
+// row group's activation records in their global layout.
 struct Dec8Lds {
     int sa_pitch;         // elements per row
-    int sa, sq, fbuf, total;  // byte offsets, bytes used
+    int sa, sq, fbuf, recs, total;  // byte offsets, bytes used
 };
-__host__ __device__ inline Dec8Lds dec8_lds(int nblk, int JG) {
+__host__ __device__ inline Dec8Lds dec8_lds(int nblk, int JG, bool lrec = false) {
     Dec8Lds l;
     l.sa_pitch = ((nblk + 3) / 4 * 4 + 59) / 64 * 64 + 4;
     int off = 0;
     l.sa = lds_take(off, kRows8 * l.sa_pitch * 4);
     l.sq = lds_take(off, kRows8 * l.sa_pitch * 4);
     l.fbuf = lds_take(off, 2 * 2 * 64 * dec_pitch(JG) * 4);
+    l.recs = lds_take(off, lrec ? (nblk + JG - 1) / JG * JG * 512 : 0);
     l.total = off;
     return l;
 }
+// Records copied into LDS (LREC): at most this many uint4 per thread.
+constexpr int kRecCopy = 8;
 
 // One weight chunk of a producer with its activation records (JG blocks of
 // 8 bytes per lane) and per-column metadata: one scale, or for EXTRA
@@ -63,7 +67,11 @@ struct Unit8 {
 // (RG row groups of eight rows; xcd: the RG workgroups of a tile range share
 // an XCD).  pM is all rows of the call.  Tiles: the first rem_t tile ranges
 // own base_t + 1, the rest base_t.
-template <int BITS, bool HP, bool EXTRA, int FUSE>
+// LREC: the workgroup copies its row group's records into LDS once and the
+// producers read them there, instead of from L2 for every tile (a
+// workgroup with several tiles otherwise streams the records once per tile,
+// as many bytes as the INT8 weights).
+template <int BITS, bool HP, bool EXTRA, int FUSE, bool LREC>
 __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, const float* pS, const uint4* pR,
                                                               int pbase_t, int pnblk, int pM, int pnbg, int prem_t,
                                                               int pngrp, int misc, GemvArgs args) {
@@ -118,6 +126,27 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
         mq0 = gsq[mi0];
         if (two_meta) mq1 = gsq[mi1];
     }
+    // LREC: the records (nbg * NA * 64 uint4, at most kRecCopy = 8 per
+    // thread), all loads in flight before any store, in named registers (an
+    // array assigned under these branches was placed in scratch).  Each
+    // group of 1024 is taken or skipped by the whole workgroup; threads past
+    // the end of a group re-read its last record.
+    const int nrec = nbg * NA * 64;
+    static_assert(kRecCopy == 8, "the copy spells out eight groups");
+    uint4 rc0, rc1, rc2, rc3, rc4, rc5, rc6, rc7;
+    auto ldr = [&](int k, uint4& v) {
+        if (1024 * k < nrec) v = pR[min(tid + 1024 * k, nrec - 1)];
+    };
+    if constexpr (LREC) {
+        ldr(0, rc0);
+        ldr(1, rc1);
+        ldr(2, rc2);
+        ldr(3, rc3);
+        ldr(4, rc4);
+        ldr(5, rc5);
+        ldr(6, rc6);
+        ldr(7, rc7);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     const int t_begin = g * pbase_t + min(g, prem_t);
@@ -128,6 +157,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
     int* sq_l = reinterpret_cast<int*>(smem + lay.sq);
     float* fbuf = reinterpret_cast<float*>(smem + lay.fbuf);  // [2][2][64][PP]
+    uint4* rec_l = reinterpret_cast<uint4*>(smem + lay.recs);   // LREC
     const int col = lane & 15, grp = lane >> 4;
 
     // Rows land at the padded pitch; sums of q premultiplied by -8 (the
@@ -149,6 +179,19 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
         };
         put(mi0, ma0, mq0);
         if (two_meta) put(mi1, ma1, mq1);
+        if constexpr (LREC) {
+            auto str = [&](int k, const uint4& v) {
+                if (1024 * k < nrec && tid + 1024 * k < nrec) rec_l[tid + 1024 * k] = v;
+            };
+            str(0, rc0);
+            str(1, rc1);
+            str(2, rc2);
+            str(3, rc3);
+            str(4, rc4);
+            str(5, rc5);
+            str(6, rc6);
+            str(7, rc7);
+        }
     };
 
     // Load cursor (as in dec_kernel): chunk ld_c of local tile ld_t, ld_rem
@@ -184,8 +227,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
         asm("" : "+v"(wi), "+v"(si), "+v"(ri), "+v"(mi));
         const bool up = PAIR && ld_sel;
         p.w = (up ? args.W2 : lw)[wi];
+        if constexpr (!LREC) {
 #pragma unroll
-        for (int h = 0; h < NA; ++h) p.a[h] = pR[ri + 64 * h];
+            for (int h = 0; h < NA; ++h) p.a[h] = pR[ri + 64 * h];
+        }
         if constexpr (EXTRA) {
             typedef int ivec __attribute__((ext_vector_type(JG)));
             const fvec sv = *reinterpret_cast<const fvec*>((up ? args.S2 : args.S) + (size_t)mi * JG);
@@ -358,6 +403,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     auto consume = [&](const Unit8<JG, EXTRA>& cur, int buf) {
         const int c = cur.c;
         if (c >= nbg) return;
+        uint4 av[NA];
+#pragma unroll
+        for (int h = 0; h < NA; ++h) av[h] = LREC ? rec_l[(c * NA + h) * 64 + lane] : cur.a[h];
         // -8 * sum(q) (or -sum(q) with EXTRA) of rows 2 grp and 2 grp + 1
         // (INT4).
         int4 z0 = make_int4(0, 0, 0, 0), z1 = z0;
@@ -371,7 +419,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
             // Blocks past nblk (last chunk) read padding; the chain never
             // folds them.
             const uint64_t bop = unpack_b(cur.w, jb, BITS);
-            const uint4& a2 = cur.a[jb >> 1];
+            const uint4& a2 = av[jb >> 1];
             const uint64_t aop = (jb & 1) ? ((uint64_t)a2.w << 32 | a2.z) : ((uint64_t)a2.y << 32 | a2.x);
             int e0 = 0, e1 = 0;
             if (BITS == 4) {
@@ -425,10 +473,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     }
 }
 
-template <int BITS, bool HP, bool EXTRA, int FUSE>
+template <int BITS, bool HP, bool EXTRA, int FUSE, bool LREC>
 hipError_t launch_dec8_f(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, hipStream_t st) {
-    auto kern = dec8_kernel<BITS, HP, EXTRA, FUSE>;
-    bool& set = attr_set[FUSE + (EXTRA ? 3 : 0)];
+    auto kern = dec8_kernel<BITS, HP, EXTRA, FUSE, LREC>;
+    bool& set = attr_set[FUSE + (EXTRA ? 3 : 0) + (LREC ? 6 : 0)];
     if (!set) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
@@ -443,21 +491,28 @@ hipError_t launch_dec8_f(bool* attr_set, const GemvArgs& a, const uint4* rec, in
 }
 
 // attr_set: this device's flags for the (bits, mode) pair, one per (FUSE
-// mode, per-block metadata) variant.  Handles with per-block metadata take
-// the plain and paired calls (the multi-projection launch sends them one by
-// one).
+// mode, per-block metadata, records in LDS) variant.  Handles with per-block
+// metadata take the plain and paired calls (the multi-projection launch
+// sends them one by one).
+template <int BITS, bool HP, bool LREC>
+hipError_t launch_dec8_l(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, int fuse, bool extra,
+                         hipStream_t st) {
+    if (extra) {
+        if (fuse == kFusePair) return launch_dec8_f<BITS, HP, true, kFusePair, LREC>(attr_set, a, rec, grid, lds, st);
+        if (fuse != kFusePlain) return hipErrorInvalidValue;
+        return launch_dec8_f<BITS, HP, true, kFusePlain, LREC>(attr_set, a, rec, grid, lds, st);
+    }
+    if (fuse == kFusePair) return launch_dec8_f<BITS, HP, false, kFusePair, LREC>(attr_set, a, rec, grid, lds, st);
+    if (fuse == kFuseMulti) return launch_dec8_f<BITS, HP, false, kFuseMulti, LREC>(attr_set, a, rec, grid, lds, st);
+    if (fuse != kFusePlain) return hipErrorInvalidValue;
+    return launch_dec8_f<BITS, HP, false, kFusePlain, LREC>(attr_set, a, rec, grid, lds, st);
+}
+
 template <int BITS, bool HP>
 hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, int fuse, bool extra,
-                       hipStream_t st) {
-    if (extra) {
-        if (fuse == kFusePair) return launch_dec8_f<BITS, HP, true, kFusePair>(attr_set, a, rec, grid, lds, st);
-        if (fuse != kFusePlain) return hipErrorInvalidValue;
-        return launch_dec8_f<BITS, HP, true, kFusePlain>(attr_set, a, rec, grid, lds, st);
-    }
-    if (fuse == kFusePair) return launch_dec8_f<BITS, HP, false, kFusePair>(attr_set, a, rec, grid, lds, st);
-    if (fuse == kFuseMulti) return launch_dec8_f<BITS, HP, false, kFuseMulti>(attr_set, a, rec, grid, lds, st);
-    if (fuse != kFusePlain) return hipErrorInvalidValue;
-    return launch_dec8_f<BITS, HP, false, kFusePlain>(attr_set, a, rec, grid, lds, st);
+                       bool lrec, hipStream_t st) {
+    return lrec ? launch_dec8_l<BITS, HP, true>(attr_set, a, rec, grid, lds, fuse, extra, st)
+                : launch_dec8_l<BITS, HP, false>(attr_set, a, rec, grid, lds, fuse, extra, st);
 }
 
 }  // namespace bq

@@ -5,6 +5,6 @@
 namespace bq {
 template hipError_t launch_dec_bits<4, false>(bool*, const GemvArgs&, int, int, int, bool, bool, bool,
                                                     hipStream_t);
-template hipError_t launch_dec8<4, false>(bool*, const GemvArgs&, const uint4*, int, int, int, bool,
+template hipError_t launch_dec8<4, false>(bool*, const GemvArgs&, const uint4*, int, int, int, bool, bool,
                                           hipStream_t);
 }  // namespace bq

@@ -784,7 +784,7 @@ struct Workspace {
     hipStream_t stream = nullptr;
     int n_cu = 0;
     bool attr_set[256] = {};  // decode kernel variants with the kernel attribute set
-    bool dec8_attr[32] = {};  // the same for dec8_kernel, per (bits, mode) and (FUSE mode, metadata)
+    bool dec8_attr[48] = {};  // the same for dec8_kernel, per (bits, mode) and (FUSE mode, metadata, LDS records)
     bool pf_attr[256] = {};
 };
 
@@ -1120,6 +1120,15 @@ int device_cus(Workspace& w, int dev) {
     return w.n_cu;
 }
 
+// Tiles per workgroup from which dec8_kernel copies its records into LDS
+// (BREEZE_HIP_DEC8_LREC sets it; 0 never).
+int dec8_lrec_min_tiles() {
+    if (const char* v = std::getenv("BREEZE_HIP_DEC8_LREC")) {
+        const int t = std::atoi(v);
+        return t > 0 ? t : std::numeric_limits<int>::max();
+    }
+    return 2;
+}
 // Rows of the eight-row groups that take M rows (M rounded up to 8).
 int dec8_rows(int M) { return (M + kRows8 - 1) / kRows8 * kRows8; }
 constexpr int kDec8MaxRows = 32;  // four row groups
@@ -1380,14 +1389,20 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.NG = std::min(a.ntiles, std::max(1, n_cu / a.RG));
         a.pair_xcd = (a.RG > 1 && a.NG % 8 == 0) ? 1 : 0;
         const int grid = a.NG * a.RG;
-        const int lds8 = dec8_lds(h->nblk, JG).total;
+        // Records in LDS for workgroups with several tiles (or paired tiles),
+        // where they fit: read once instead of once per tile.
+        const int tiles_wg = a.ntiles / a.NG * (pair ? 2 : 1);
+        const int lrec_lds = dec8_lds(h->nblk, JG, true).total;
+        const bool lrec = tiles_wg >= dec8_lrec_min_tiles() && lrec_lds <= kLdsMax &&
+                          h->nblk_pad * 32 <= kRecCopy * kDecWaves * 64;
+        const int lds8 = lrec ? lrec_lds : dec8_lds(h->nblk, JG).total;
         const uint4* rec = reinterpret_cast<const uint4*>(s.aq);
-        bool* at = &w.dec8_attr[8 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
+        bool* at = &w.dec8_attr[12 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
         const bool x = h->extra;
-        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, fz, x, st)
-                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, fz, x, st);
-        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, fz, x, st)
-                    : launch_dec8<4, false>(at, a, rec, grid, lds8, fz, x, st);
+        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, fz, x, lrec, st)
+                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, fz, x, lrec, st);
+        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, fz, x, lrec, st)
+                    : launch_dec8<4, false>(at, a, rec, grid, lds8, fz, x, lrec, st);
     } else if (dec) {
         const int n_cu = device_cus(w, dev);
         a.RS = rs;

@@ -527,7 +527,7 @@ hipError_t launch_dec_bits(bool* attr_set, const GemvArgs& a, int grid, int lds,
 // activation records in MFMA operand order, written by quantize_r8_kernel.
 template <int BITS, bool HP>
 hipError_t launch_dec8(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, int fuse, bool extra,
-                       hipStream_t st);
+                       bool lrec, hipStream_t st);
 template <int BITS, bool HP>
 hipError_t launch_pf(bool* pf_attr, const PfArgs& p, int scm, int rp, int ct, dim3 grid, hipStream_t st);
 

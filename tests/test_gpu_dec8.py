@@ -219,3 +219,45 @@ def test_dec8_per_block_metadata(gpu, hb, orc, hi_prec, kind):
                     del os.environ["BREEZE_HIP_DEC8"]
     finally:
         hb.free(h)
+
+
+@pytest.mark.parametrize("bits,K", [(8, 5120), (4, 4640)])
+def test_dec8_records_in_lds(gpu, hb, orc, hi_prec, bits, K):
+    """Workgroups with several tiles copy their records into LDS once
+    (where they fit: W8 up to K = 5120, W4 K = 4640): outputs and argmax
+    bit-exact against the oracle and against the records read from L2 per
+    tile (BREEZE_HIP_DEC8_LREC=0), at 5, 8 and 24 rows (three row groups),
+    and through the gate/up pair."""
+    rng = np.random.default_rng(K + bits)
+    N = 16 * 700  # 700 tiles: 2-3 per workgroup at one row group, more with three
+    nblk = K // 32
+    qw, sc, _ = rng_weights(rng, N, K, bits)
+    sc = np.ascontiguousarray(np.repeat(sc[:, :1], nblk, axis=1))
+    qu, su, _ = rng_weights(rng, N, K, bits)
+    su = np.ascontiguousarray(np.repeat(su[:, :1], nblk, axis=1))
+    h = hb.prepack(qw, sc, None, K, N, bits=bits)
+    hu = hb.prepack(qu, su, None, K, N, bits=bits)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            for M in (5, 8, 24):
+                A = rng.normal(size=(M, K)).astype(np.float32)
+                want = orc.matmul(qw, sc, None, N, K, bits, A, hp)
+                case = dict(bits=bits, K=K, hp=hp, M=M)
+                got, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+                pair = hb.matmul_silu_mul(h, hu, gpu.from_numpy(A).cuda(), N)
+                os.environ["BREEZE_HIP_DEC8_LREC"] = "0"
+                try:
+                    got_l2, idx_l2 = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+                    pair_l2 = hb.matmul_silu_mul(h, hu, gpu.from_numpy(A).cuda(), N)
+                finally:
+                    del os.environ["BREEZE_HIP_DEC8_LREC"]
+                gpu.cuda.synchronize()
+                assert bits_equal(got.cpu().numpy(), want), case
+                assert idx.cpu().numpy().tolist() == np.argmax(want, axis=1).tolist(), case
+                assert bits_equal(got_l2.cpu().numpy(), want), case
+                assert idx_l2.cpu().numpy().tolist() == idx.cpu().numpy().tolist(), case
+                assert bits_equal(pair.cpu().numpy(), pair_l2.cpu().numpy()), case
+    finally:
+        hb.free(h)
+        hb.free(hu)
