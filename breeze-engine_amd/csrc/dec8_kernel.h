@@ -28,8 +28,14 @@ constexpr int kRows8 = 8;
 // LDS: block scales and (INT4) -zp * sum(q) of the eight rows, row pitch
 // padded 16 B past a multiple of 256 B (the four rows a fold or epilogue
 // reads together fall on different banks), then the phase buffer
-// [2 buffers][2 rows][64 lanes][dec_pitch(JG)] of f values, then (LREC) the
+// [2 buffers][2 rows][64 lanes][dec8_pitch(JG)] of f values, then (LREC) the
 // row group's activation records in their global layout.
+// Phase-buffer pitch (floats per lane) for 14 producers: JG-wide stores
+// and reads at this lane stride fall on distinct banks (60 l mod 64 are
+// distinct multiples of 4 over 16 lanes; 34 as in dec_kernel for JG = 2).
+__host__ __device__ constexpr int dec8_pitch(int JG) { return JG == 4 ? 60 : dec_pitch(JG); }
+static_assert(kP8 * 4 <= 60, "a producer's slot in the phase buffer");
+
 struct Dec8Lds {
     int sa_pitch;         // elements per row
     int sa, sq, fbuf, recs, total;  // byte offsets, bytes used
@@ -40,7 +46,7 @@ __host__ __device__ inline Dec8Lds dec8_lds(int nblk, int JG, bool lrec = false)
     int off = 0;
     l.sa = lds_take(off, kRows8 * l.sa_pitch * 4);
     l.sq = lds_take(off, kRows8 * l.sa_pitch * 4);
-    l.fbuf = lds_take(off, 2 * 2 * 64 * dec_pitch(JG) * 4);
+    l.fbuf = lds_take(off, 2 * 2 * 64 * dec8_pitch(JG) * 4);
     l.recs = lds_take(off, lrec ? (nblk + JG - 1) / JG * JG * 512 : 0);
     l.total = off;
     return l;
@@ -77,7 +83,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
                                                               int pngrp, int misc, GemvArgs args) {
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int NA = JG / 2;
-    constexpr int PP = dec_pitch(JG);
+    constexpr int PP = dec8_pitch(JG);
     constexpr int R = kDecRing;
     // FUSE (as in dec_kernel): plain, the gate/up pair (each tile's gate
     // then up projection, C = silu(gate) * up), or several projections of
