@@ -181,10 +181,11 @@ def test_dec8_per_block_metadata(gpu, hb, orc, hi_prec, kind):
     times -sum(q) of the row), INT4 scales per two blocks (smaller than a
     chunk, so per-block scales), and legacy handles whose corr disagrees with
     the weights (the corr delta, 256 per unit in the two-pass mode), INT4
-    with zero points and INT8.  Both activation modes, against the oracle
-    and against the four-row groups (BREEZE_HIP_DEC8=0)."""
+    with zero points and INT8.  600 tiles, so workgroups hold several tiles
+    and copy their records into LDS.  Both activation modes, against the
+    oracle and against the four-row groups (BREEZE_HIP_DEC8=0)."""
     rng = np.random.default_rng(sum(map(ord, kind)))
-    N, K = 80, 4640
+    N, K = 16 * 600, 4640
     nblk = K // 32
     if kind in ("zeros", "group2"):
         bits = 4
