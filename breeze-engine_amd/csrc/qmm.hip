@@ -1389,9 +1389,9 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.NG = std::min(a.ntiles, std::max(1, n_cu / a.RG));
         a.pair_xcd = (a.RG > 1 && a.NG % 8 == 0) ? 1 : 0;
         const int grid = a.NG * a.RG;
-        // Records in LDS for workgroups with several tiles (or paired tiles),
-        // where they fit: read once instead of once per tile.
-        const int tiles_wg = a.ntiles / a.NG * (pair ? 2 : 1);
+        // Records in LDS where the busiest workgroups have several tiles (or
+        // paired tiles) and they fit: read once instead of once per tile.
+        const int tiles_wg = (a.ntiles + a.NG - 1) / a.NG * (pair ? 2 : 1);
         const int lrec_lds = dec8_lds(h->nblk, JG, true).total;
         const bool lrec = tiles_wg >= dec8_lrec_min_tiles() && lrec_lds <= kLdsMax &&
                           h->nblk_pad * 32 <= kRecCopy * kDecWaves * 64;
