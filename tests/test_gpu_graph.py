@@ -19,10 +19,13 @@ def _mlp(hb, torch, hg, hu, hd, x, inter, H):
     return hb.matmul(hd, torch.nn.functional.silu(g) * u, H)
 
 
-@pytest.mark.parametrize("rows,bits", [(1, 4), (4, 4), (64, 8)])
-def test_captured_mlp_block_replays_bit_exact(gpu, hb, hi_prec, rows, bits):
+# Hidden sizes past 4096 put the gate and up projections on the stand-alone
+# quantizer and the eight-row groups (8 rows: one group, W4 with zero points;
+# 16 rows: two, W8).
+@pytest.mark.parametrize("rows,bits,H,inter", [(1, 4, 512, 1024), (4, 4, 512, 1024), (64, 8, 512, 1024),
+                                               (8, 4, 5120, 1024), (16, 8, 4640, 2048)])
+def test_captured_mlp_block_replays_bit_exact(gpu, hb, hi_prec, rows, bits, H, inter):
     torch = gpu
-    H, inter = 512, 1024
     rng = np.random.default_rng(rows + bits)
     hs = []
     for K, N in ((H, inter), (H, inter), (inter, H)):
