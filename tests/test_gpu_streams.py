@@ -18,8 +18,10 @@ pytestmark = pytest.mark.gpu
 
 def test_two_streams_on_one_device(gpu, hb, orc, hi_prec):
     """Interleaved calls on two streams, each shape using scratch: staged
-    decode records (4 rows of K = 4608), prefill records (130 rows) and the
-    decode argmax state.  Each stream's outputs equal the oracle's."""
+    decode records (4 rows of K = 4608 on the four-row groups, 8 and 20 rows
+    on the eight-row groups), prefill records (130 rows) and the decode
+    argmax state (1 row, and 8 rows on the eight-row groups).  Each stream's
+    outputs equal the oracle's."""
     torch = gpu
     N, K = 256, 4608
     rng = np.random.default_rng(77)
@@ -30,17 +32,17 @@ def test_two_streams_on_one_device(gpu, hb, orc, hi_prec):
         main = torch.cuda.current_stream()
         streams = [torch.cuda.Stream(), torch.cuda.Stream()]
         cases = []
-        for rows in (4, 130, 1):
+        for rows, am in ((4, False), (8, False), (20, False), (130, False), (1, True), (8, True)):
             for s in streams:
                 A = rng.normal(size=(rows, K)).astype(np.float32)
-                cases.append((s, A, torch.from_numpy(A).cuda()))
+                cases.append((s, A, torch.from_numpy(A).cuda(), am))
         for s in streams:
             s.wait_stream(main)
         outs = []
         for _ in range(2):
-            for s, A, dA in cases:
+            for s, A, dA, am in cases:
                 with torch.cuda.stream(s):
-                    if A.shape[0] == 1:
+                    if am:
                         outs.append(hb.matmul_argmax(h, dA, N))
                     else:
                         outs.append((hb.matmul(h, dA, N), None))
