@@ -1263,8 +1263,10 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // against 12.2 us.  Measured against the four-row groups (us): W4
     // K=12288 N=4096 at 8 / 16 / 32 rows 13.6 / 21.1 / 34.0 -> 13.1 / 18.6 /
     // 29.2, W8 K=12288 N=4096 at 24 rows 49.3 -> 34.3, W4 K=17408 N=5120 at
-    // 16 rows 54.0 -> 30.6 (at 24 and 32 rows the GEMM took 167 us);
-    // W4 K=5120 N=5120 at 12 rows 13.3 -> 14.1 is the one loss seen.
+    // 16 rows 54.0 -> 30.6 (at 24 and 32 rows the GEMM took 167 us).  At
+    // 9 / 12 rows (with the records in LDS): W4 K=17408 N=5120 40.1 / 44.9
+    // -> 26.9 / 27.1, W8 K=5120 N=5120 16.4 / 16.4 -> 12.5 / 12.7; W4
+    // K=5120 N=5120 13.3 / 13.5 -> 13.9 / 13.3 is the one loss seen.
     // BREEZE_HIP_DEC8=0 keeps every call off it.
     const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots);
     if ((h2 || mp) && !(dec8 || (dec && M <= 16))) return kNotPairable;
