@@ -1267,8 +1267,18 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // 9 / 12 rows (with the records in LDS): W4 K=17408 N=5120 40.1 / 44.9
     // -> 26.9 / 27.1, W8 K=5120 N=5120 16.4 / 16.4 -> 12.5 / 12.7; W4
     // K=5120 N=5120 13.3 / 13.5 -> 13.9 / 13.3 is the one loss seen.
-    // BREEZE_HIP_DEC8=0 keeps every call off it.
-    const bool dec8 = M <= dec_rows && !fused && dec8_takes(h, M, dots);
+    // BREEZE_HIP_DEC8=0 keeps every call off it, =2 gives it every call the
+    // four-row groups quantize in their prologue (for measurements).
+    // Where the four-row groups quantize in their prologue, the eight-row
+    // groups take the call from 24 rows, and from 12 rows with K >= 3072
+    // (us, four-row -> eight-row): W8 K=3072 N=8192 at 12 / 24 rows 15.3 /
+    // 25.1 -> 12.3 / 16.9, W4 K=4096 N=12288 at 16 / 32 rows 20.6 / 36.2
+    // -> 17.4 / 27.6, W4 K=2048 N=8192 at 12 / 24 rows 9.05 / 14.3 ->
+    // 11.3 / 13.0; at 8 rows W8 K=N=4096 9.4 -> 12.1.  Never a norm call:
+    // the norm runs in the four-row groups' prologue only.
+    const char* d8 = std::getenv("BREEZE_HIP_DEC8");
+    const bool dec8_fused = M >= 24 || (M >= 12 && h->nblk >= 96) || (d8 && d8[0] == '2');
+    const bool dec8 = M <= dec_rows && (!fused || dec8_fused) && !(mp && mp->norm) && dec8_takes(h, M, dots);
     if ((h2 || mp) && !(dec8 || (dec && M <= 16))) return kNotPairable;
     // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
     // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the

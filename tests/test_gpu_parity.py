@@ -532,8 +532,9 @@ def test_decode_row_groups(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_ze
     three to eight of 4 rows, per tile range, on one XCD when the range
     count allows; the limit forced to 32), outputs and argmax against the
     oracle: K = 4608 (staged records, 40 tiles: row groups placed on one
-    XCD) and K = 96 (the four-row groups quantize in their prologue; 20
-    tiles: the plain block order)."""
+    XCD) and K = 96 (the four-row groups quantize in their prologue up to 20
+    rows, the eight-row groups take 25 and 32; 20 tiles: the plain block
+    order)."""
     monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "32")
     if dec8 == "off":
         monkeypatch.setenv("BREEZE_HIP_DEC8", "0")
