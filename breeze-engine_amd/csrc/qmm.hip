@@ -1274,10 +1274,12 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     // (us, four-row -> eight-row): W8 K=3072 N=8192 at 12 / 24 rows 15.3 /
     // 25.1 -> 12.3 / 16.9, W4 K=4096 N=12288 at 16 / 32 rows 20.6 / 36.2
     // -> 17.4 / 27.6, W4 K=2048 N=8192 at 12 / 24 rows 9.05 / 14.3 ->
-    // 11.3 / 13.0; at 8 rows W8 K=N=4096 9.4 -> 12.1.  Never a norm call:
-    // the norm runs in the four-row groups' prologue only.
+    // 11.3 / 13.0; at 8 rows W8 K=N=4096 9.4 -> 12.1, but from 8 rows on
+    // wide K=4096 shapes W8 N=12288 18.5 -> 14.7, W4 N=12288 14.2 -> 13.1.
+    // Never a norm call: the norm runs in the four-row groups' prologue only.
     const char* d8 = std::getenv("BREEZE_HIP_DEC8");
-    const bool dec8_fused = M >= 24 || (M >= 12 && h->nblk >= 96) || (d8 && d8[0] == '2');
+    const bool dec8_fused = M >= 24 || (M >= 12 && h->nblk >= 96) ||
+                            (M >= 8 && h->nblk >= 128 && a.ntiles >= 768) || (d8 && d8[0] == '2');
     const bool dec8 = M <= dec_rows && (!fused || dec8_fused) && !(mp && mp->norm) && dec8_takes(h, M, dots);
     if ((h2 || mp) && !(dec8 || (dec && M <= 16))) return kNotPairable;
     // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
