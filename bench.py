@@ -35,10 +35,13 @@ defeat the parallel in-order rebuild, with that rebuild forced), and
 launch, one launch per projection, and with the RMSNorm in front).
 """
 import argparse
+import csv
+import glob
+import hashlib
 import json
 import os
+import statistics
 import sys
-import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 PKG_DIR = os.path.join(ROOT, "breeze-engine_amd")
@@ -52,6 +55,38 @@ HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 ROTATE_BYTES = 512 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_w4_gemv.json")
+HEADLINE_KERNEL = "dec_kernel"
+
+
+def kernel_source_files():
+    """The files whose change can change a kernel's code: every file under
+    the package's csrc/ and the build script (its compiler flags)."""
+    files = sorted(glob.glob(os.path.join(PKG_DIR, "csrc", "*")))
+    return files + [os.path.join(PKG_DIR, "breeze_amd", "_build.py")]
+
+
+def kernel_sources_digest(files=None):
+    """First 16 hex digits of a sha256 over the kernel sources (path relative
+    to the repository, then content, in name order).  Profiles record it, and
+    a profile whose digest differs from the tree's was taken on other
+    kernels."""
+    h = hashlib.sha256()
+    for f in files or kernel_source_files():
+        h.update(os.path.relpath(f, ROOT).encode() + b"\0")
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
+def traffic_record(path=TRAFFIC_FILE):
+    """The headline's profile record and whether it is stale (its kernel
+    sources digest differs from this tree's, or it has none)."""
+    if not os.path.exists(path):
+        return None, True
+    with open(path) as f:
+        tr = json.load(f)
+    return tr, tr.get("sources_digest") != kernel_sources_digest()
 
 
 def _handles(hb, d, min_bytes):
@@ -73,10 +108,13 @@ def gate(torch, stream):
         torch.cuda._sleep(1_000_000)
 
 
-def time_workload(hb, torch, name, rows, steps, warmup, argmax=False):
+def time_workload(hb, torch, name, rows, steps, warmup, argmax=False, graph=False):
     """Per-call time (s) of one workload: `warmup` untimed calls, then
     `steps` calls bracketed by synchronisation and HIP events on the stream
-    the library launches on."""
+    the library launches on.  graph: the `steps` calls are captured in one
+    HIP graph on a stream of their own and the timed region is one replay of
+    it (dispatches then follow each other at the GPU's own pace, also under a
+    profiler whose interception slows the host's enqueue)."""
     from breeze_amd import workloads
 
     d = workloads.make_config(name, rows)
@@ -86,7 +124,11 @@ def time_workload(hb, torch, name, rows, steps, warmup, argmax=False):
     M = A.shape[0]
     out = torch.empty((M, N), dtype=torch.float32, device="cuda")
     idx = torch.empty((M,), dtype=torch.int64, device="cuda")
-    stream = torch.cuda.current_stream()
+    if graph:
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+    else:
+        stream = torch.cuda.current_stream()
     sp = hb._vp(stream.cuda_stream)
     ap, op, ip = hb._vp(A.data_ptr()), hb._vp(out.data_ptr()), hb._vp(idx.data_ptr())
     lib = hb._lib
@@ -109,11 +151,24 @@ def time_workload(hb, torch, name, rows, steps, warmup, argmax=False):
         torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        gate(torch, stream)
-        e0.record(stream)
-        for i in range(steps):
-            call(hs[i % len(hs)])
-        e1.record(stream)
+        if graph:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                for i in range(steps):
+                    call(hs[i % len(hs)])
+            with torch.cuda.stream(stream):
+                g.replay()  # untimed: the graph's first launch uploads it
+                torch.cuda.synchronize()
+                gate(torch, stream)
+                e0.record(stream)
+                g.replay()
+                e1.record(stream)
+        else:
+            gate(torch, stream)
+            e0.record(stream)
+            for i in range(steps):
+                call(hs[i % len(hs)])
+            e1.record(stream)
         torch.cuda.synchronize()
         err = hb.last_error()
         if err:
@@ -173,9 +228,11 @@ def cpu_baseline(torch):
         "unit": "GB/s",
         "cores": res["threads"],
         "kind": res["kind"],
-        "sample": f"{head['workload']}, hi-prec mode, {head['calls']} timed calls after 3 warmup "
-                  f"({head['us']} us/call); every workload below the same way (at most 20 calls or about "
-                  f"4 s each); threads one per physical core on {where}",
+        "sample": f"{head['workload']}, hi-prec mode set once, the native i4_matmul on preallocated input "
+                  f"and output, {head['calls']} timed calls after 3 warmup (mean {head['us']} us/call, median "
+                  f"{head['us_median']}, min {head['us_min']}; value from the mean, as the reference's benchmark "
+                  f"reports); every workload below the same way (at most 20 calls or about 4 s each); threads "
+                  f"one per physical core on {where}",
         "cpu_model": res["cpu_model"],
         "cpus": res["cpus"],
         "omp": res["omp"],
@@ -271,6 +328,204 @@ def time_multi(hb, torch, label, rows, steps, warmup):
     return res
 
 
+# ---------------------------------------------------------------- profile summaries
+#
+# A profile of one workload is four runs of `bench.py --workload NAME` on one
+# box, each its own process, with their output under one directory D:
+#   D/trace   rocprofv3 --kernel-trace --stats --output-format csv -d D/trace -o t
+#             (200 timed calls);
+#   D/fetch, D/write   rocprofv3 --pmc FETCH_SIZE (or WRITE_SIZE) --output-format csv
+#             -d D/fetch -o p (50 timed calls);
+#   D/plain.json   the same workload without the profiler (its JSON line).
+# and the calibration of the two counters, `bench.py --copy-calibration` under
+# each --pmc run (C/fetch, C/write).  --profile-summary D turns them into the
+# text summary kept under profiles/, stamped with the kernel sources digest.
+
+
+def _trace_rows(path, kernel, last):
+    rows = [r for r in csv.DictReader(open(path)) if kernel in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    return rows[-last:]
+
+
+def _counter_median(path, kernel, last=50):
+    per = {}
+    for r in csv.DictReader(open(path)):
+        if kernel in r["Kernel_Name"]:
+            per[int(r["Dispatch_Id"])] = per.get(int(r["Dispatch_Id"]), 0.0) + float(r["Counter_Value"])
+    vals = [per[k] for k in sorted(per)][-last:]
+    if not vals:
+        raise SystemExit(f"no {kernel} dispatch in {path}")
+    return statistics.median(vals)
+
+
+def _short_name(name):
+    """A kernel's name without its return type and parameter list."""
+    if name.startswith("void "):
+        name = name[5:]
+    if name.endswith(")"):
+        depth = 0
+        for i in range(len(name) - 1, -1, -1):
+            depth += {")": 1, "(": -1}.get(name[i], 0)
+            if depth == 0:
+                return name[:i]
+    return name
+
+
+def _pct(vals, q):
+    v = sorted(vals)
+    return v[min(len(v) - 1, int(q * (len(v) - 1) + 0.5))]
+
+
+def profile_summary(d, cal, workload, kernel, steps, commit, out, traffic_out=None):
+    """Writes the summary of the profile in directory d (see above) of one
+    workload's dominant kernel (`kernel`: a substring of its name)."""
+    from breeze_amd import workloads
+
+    name, _, r = workload.partition(":")
+    rows = int(r) if r else None
+    prefill = name.endswith("prefill")
+    if name in workloads.LABELS:
+        M = workloads.CONFIGS[name][1] if rows is None else rows
+        label = workloads.LABELS[name].format(M=M)
+        alg = workloads.algorithmic_ops(name, M) if prefill else workloads.algorithmic_bytes(name, M)
+    else:
+        # The decoder workloads (multi, rmsnorm): kernel times only.
+        label, alg = f"{name} workload, {rows or 1} row(s) (bench.py --workload {workload})", None
+    tr = _trace_rows(os.path.join(d, "trace", "t_kernel_trace.csv"), kernel, steps)
+    if len(tr) < steps:
+        raise SystemExit(f"{len(tr)} {kernel} dispatches in the trace, expected {steps}")
+    us = [(int(x["End_Timestamp"]) - int(x["Start_Timestamp"])) / 1e3 for x in tr]
+    starts = [int(x["Start_Timestamp"]) for x in tr]
+    spacing = statistics.median([(b - a) / 1e3 for a, b in zip(starts, starts[1:])])
+    mean, med = statistics.mean(us), statistics.median(us)
+    # Other kernels of the same calls (the stand-alone quantizer ahead of a
+    # staged decode or prefill call), over the same span of the trace.
+    t0, t1 = starts[0], int(tr[-1]["End_Timestamp"])
+    others = {}
+    for x in csv.DictReader(open(os.path.join(d, "trace", "t_kernel_trace.csv"))):
+        if kernel not in x["Kernel_Name"] and t0 <= int(x["Start_Timestamp"]) <= t1:
+            others.setdefault(x["Kernel_Name"], []).append(
+                (int(x["End_Timestamp"]) - int(x["Start_Timestamp"])) / 1e3)
+    plain = None
+    pj = os.path.join(d, "plain.json")
+    if os.path.exists(pj) and alg is not None:
+        plain = json.loads(open(pj).read().strip().splitlines()[-1])
+
+    def rate(t_us):
+        if alg is None:
+            return f"{t_us:.3f} us"
+        if prefill:
+            v = alg / (t_us * 1e-6) / 1e12
+            return f"{v:.1f} TOPS = {v / INT8_PEAK_TOPS:.4f} of {INT8_PEAK_TOPS / 1000:.1f} POPS"
+        v = alg / (t_us * 1e-6) / 1e9
+        return f"{v:.1f} GB/s = {v / HBM_PEAK_GBS:.4f} of {HBM_PEAK_GBS / 1000:.0f} TB/s"
+
+    full = tr[0]["Kernel_Name"]
+    digest = kernel_sources_digest()
+    wl = f"--workload {workload}"
+    lines = [
+        f"{_short_name(full)} on the {label}, MI355X (gfx950)",
+        "",
+        f"Kernel sources digest {digest} (sha256 of breeze-engine_amd/csrc/* and breeze_amd/_build.py,",
+        f"bench.kernel_sources_digest); taken at commit {commit}.  bench.py marks the roofline stale",
+        "when the tree's digest differs.",
+        "",
+        "Commands (from the repository root, each its own process, all on one box; D and C are",
+        "output directories):",
+        f"  rocprofv3 --kernel-trace --stats --output-format csv -d D/trace -o t -- "
+        f"python3 -u bench.py {wl} --steps {steps} --warmup 5",
+        f"  rocprofv3 --pmc FETCH_SIZE --output-format csv -d D/fetch -o p -- python3 -u bench.py {wl} "
+        "--steps 50 --warmup 2",
+        f"  rocprofv3 --pmc WRITE_SIZE --output-format csv -d D/write -o p -- python3 -u bench.py {wl} "
+        "--steps 50 --warmup 2",
+        "  rocprofv3 --pmc FETCH_SIZE (and WRITE_SIZE) --output-format csv -d C/fetch (C/write) -o p -- "
+        "python3 -u bench.py --copy-calibration",
+        f"  python3 -u bench.py {wl} --steps {steps} --warmup 20 > D/plain.json   (no profiler)",
+        f"  python3 bench.py --profile-summary D --calibration C --workload {workload} --kernel {kernel} "
+        f"--commit {commit} --out <this file>",
+        "",
+        f"Kernel trace, the last {steps} timed dispatches of {kernel}:",
+        f"  mean {mean:.3f} us, median {med:.3f}, p10 {_pct(us, 0.1):.3f}, p90 {_pct(us, 0.9):.3f}, "
+        f"min {min(us):.3f}, max {max(us):.3f}",
+        f"  consecutive dispatches start {spacing:.3f} us apart (median) under the profiler",
+    ]
+    if alg is not None:
+        lines += [f"  algorithmic {'ops' if prefill else 'bytes'} {alg:,} per call -> over the mean {rate(mean)};",
+                  f"  over the median {rate(med)}"]
+    # Every other kernel the trace's last calls ran, by name.
+    for k, v in sorted(others.items()):
+        lines.append(f"  same span, {_short_name(k)}: {len(v)} dispatches, mean {statistics.mean(v):.3f} us, "
+                     f"median {statistics.median(v):.3f}")
+    if plain:
+        pu = plain["us"]
+        lines += [
+            "",
+            f"Without the profiler, same box: {pu:.3f} us per call over {plain['steps']} back-to-back calls "
+            f"(HIP events around the timed calls) -> {rate(pu)}.",
+            "  bench.py reports this figure.  It counts every kernel of a call and the boundary",
+            "  between calls, whose launches overlap the tail of the call before.  Under the profiler",
+            "  the host enqueues more slowly (the dispatch spacing above), so each dispatch starts on",
+            "  an idle GPU.  Profiled kernel time against the per-call time: mean "
+            f"{mean / pu:.3f}x, median {med / pu:.3f}x.",
+        ]
+    lines += ["", "rocprofv3 kernel_stats.csv (every dispatch of the run, set-up included):"]
+    lines += ["  " + x.rstrip() for x in open(os.path.join(d, "trace", "t_kernel_stats.csv"))][:12]
+    traffic = None
+    if cal and os.path.exists(os.path.join(d, "fetch")):
+        f_kib = _counter_median(os.path.join(d, "fetch", "p_counter_collection.csv"), kernel)
+        w_kib = _counter_median(os.path.join(d, "write", "p_counter_collection.csv"), kernel)
+        cf = _counter_median(os.path.join(cal, "fetch", "p_counter_collection.csv"), "MulFunctor", last=3)
+        cw = _counter_median(os.path.join(cal, "write", "p_counter_collection.csv"), "MulFunctor", last=3)
+        sf, sw = cf * 1024 / (256 << 20), cw * 1024 / (256 << 20)
+        traffic = int(round(f_kib * 1024 / sf + w_kib * 1024 / sw))
+        lines += [
+            "",
+            "HBM traffic per dispatch (medians of the last 50 dispatches, KiB as the counters report them):",
+            f"  FETCH_SIZE {f_kib:.1f}   WRITE_SIZE {w_kib:.1f}",
+            f"  copy calibration (256 MiB read and written per launch): FETCH_SIZE {cf:.1f} KiB, "
+            f"WRITE_SIZE {cw:.1f} KiB",
+            f"  -> scale factors (counter / true bytes) FETCH {sf:.5f}, WRITE {sw:.5f}",
+        ]
+        if not prefill:
+            lines.append(f"  HBM bytes per dispatch = {traffic:,} B against {alg:,} algorithmic ({traffic / alg:.4f}x)")
+        else:
+            lines.append(f"  HBM bytes per dispatch = {traffic:,} B")
+    extra = sorted(glob.glob(os.path.join(d, "pmc_*", "p_counter_collection.csv")))
+    if extra:
+        lines += ["", "Other counters per dispatch of the kernel (medians of the last 50 dispatches; each pass"
+                      " its own run,", "  rocprofv3 --pmc <counters> --output-format csv -d D/pmc_<n> -o p -- "
+                      f"python3 -u bench.py {wl} --steps 50 --warmup 2):"]
+        for path in extra:
+            names = sorted({x["Counter_Name"] for x in csv.DictReader(open(path))})
+            for cn in names:
+                per = {}
+                for x in csv.DictReader(open(path)):
+                    if kernel in x["Kernel_Name"] and x["Counter_Name"] == cn:
+                        per[int(x["Dispatch_Id"])] = per.get(int(x["Dispatch_Id"]), 0.0) + float(x["Counter_Value"])
+                vals = [per[k] for k in sorted(per)][-50:]
+                if vals:
+                    lines.append(f"  {cn:28s} {statistics.median(vals):,.0f}")
+    with open(out, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    if traffic_out:
+        rec = {
+            "bytes_per_launch": traffic,
+            "algorithmic_bytes": alg,
+            "kernel": _short_name(full),
+            "kernel_mean_us": round(mean, 3),
+            "kernel_median_us": round(med, 3),
+            "bench_us_same_box": plain["us"] if plain else None,
+            "sources_digest": digest,
+            "commit": commit,
+            "source": os.path.relpath(out, ROOT) + " (rocprofv3 kernel trace and FETCH_SIZE/WRITE_SIZE, "
+                                                  "copy-calibrated)",
+        }
+        with open(traffic_out, "w") as f:
+            json.dump(rec, f, indent=1)
+            f.write("\n")
+
+
 RMSNORM_H = 5120
 
 
@@ -325,9 +580,24 @@ def main():
     ap.add_argument("--workload", default=None,
                     help="time only this workload (w8_gemv, w4_gemv, w4_decode:ROWS, w8_lmhead, w8_prefill, "
                          "w4_prefill)")
+    ap.add_argument("--graph", action="store_true",
+                    help="with --workload: time one replay of a HIP graph of the timed calls")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 elementwise copy 5 times (counter calibration)")
+    ap.add_argument("--profile-summary", metavar="DIR", default=None,
+                    help="write the summary of the profile runs in DIR (with --workload, --kernel, --out)")
+    ap.add_argument("--calibration", metavar="DIR", default=None, help="counter calibration runs (fetch/, write/)")
+    ap.add_argument("--kernel", default=HEADLINE_KERNEL, help="dominant kernel of the profiled workload")
+    ap.add_argument("--commit", default="unknown", help="commit the profiled tree was at")
+    ap.add_argument("--out", default=None, help="summary file to write")
+    ap.add_argument("--traffic-out", default=None, help="also write the headline's traffic record here")
     args = ap.parse_args()
+    if args.profile_summary:
+        if not (args.workload and args.out):
+            raise SystemExit("bench.py: --profile-summary needs --workload and --out")
+        profile_summary(args.profile_summary, args.calibration, args.workload, args.kernel, args.steps,
+                        args.commit, args.out, args.traffic_out)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported. "
               "The path would shard by output columns (N) across GPUs with no reduction, "
@@ -375,8 +645,11 @@ def main():
         if name not in workloads.LABELS:
             raise SystemExit(f"bench.py: unknown workload {name!r}; one of {sorted(workloads.LABELS)}")
         rows = int(r) if r else None
-        t, m = time_workload(hb, torch, name, rows, args.steps, args.warmup, argmax=name == "w8_lmhead")
+        t, m = time_workload(hb, torch, name, rows, args.steps, args.warmup, argmax=name == "w8_lmhead",
+                             graph=args.graph)
         entry = {"workload": workloads.LABELS[name].format(M=m), "steps": args.steps, "us": round(t * 1e6, 3)}
+        if args.graph:
+            entry["graph"] = True
         if name.endswith("prefill"):
             tops = workloads.algorithmic_ops(name, m) / t / 1e12
             entry.update(tops=round(tops, 2), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
@@ -430,13 +703,8 @@ def main():
     nbytes = workloads.algorithmic_bytes(HEADLINE)
     gbs = nbytes / t_step / 1e9
 
-    traffic = None
-    traffic_note = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            tr = json.load(f)
-        traffic = tr.get("bytes_per_launch")
-        traffic_note = tr.get("source")
+    tr, stale = traffic_record()
+    tr = tr or {}
 
     result = {
         "metric": METRIC,
@@ -464,9 +732,17 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
+            "traffic": tr.get("bytes_per_launch"),
             "kernel": "dec_kernel (one launch per call)",
-            "traffic_source": traffic_note,
+            "traffic_source": tr.get("source"),
+            # The profile's kernel time and the same box's per-call time;
+            # stale: the profile was taken on other kernel sources.
+            "profiled_kernel_mean_us": tr.get("kernel_mean_us"),
+            "profiled_kernel_median_us": tr.get("kernel_median_us"),
+            "profiled_bench_us": tr.get("bench_us_same_box"),
+            "profile_sources_digest": tr.get("sources_digest"),
+            "sources_digest": kernel_sources_digest(),
+            "stale": stale,
         },
     }
     if rows is not None:

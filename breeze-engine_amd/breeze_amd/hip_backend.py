@@ -84,6 +84,8 @@ try:
     _lib.i4_rmsnorm_matmul_multi_dev.argtypes = [_vp, _vp, ctypes.c_float, _vp, _i, _i, _vp, _vp, _vp]
     _lib.i4_matmul_silu_mul_dev.restype = _i
     _lib.i4_matmul_silu_mul_dev.argtypes = [_vp, _vp, _vp, _i, _vp, _vp]
+    _lib.i4_silu_mul_dev.restype = _i
+    _lib.i4_silu_mul_dev.argtypes = [_vp, _vp, ctypes.c_size_t, _vp, _vp]
     _lib.i4_block_dots_dev.restype = _i
     _lib.i4_block_dots_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
     _lib.i4_handle_info.restype = _i
@@ -293,6 +295,22 @@ def matmul_silu_mul(gate, up, a2d, N):
     out = torch.empty((M, N), dtype=torch.float32, device=a.device)
     _check_rc(_lib.i4_matmul_silu_mul_dev(_vp(gate), _vp(up), _vp(a.data_ptr()), int(M), _vp(out.data_ptr()),
                                           _torch_stream(a)), "i4_matmul_silu_mul_dev")
+    return out
+
+
+def silu_mul(g, u):
+    """GPU torch tensors g, u (same shape, fp32) -> silu(g) * u, the decoder
+    MLP's elementwise step (kernel/qwen35_decoder.cpp:408) bit for bit,
+    asynchronous on the current stream."""
+    _require_lib()
+    import torch
+    g = g.to(torch.float32).contiguous()
+    u = u.to(torch.float32).contiguous()
+    if g.shape != u.shape:
+        raise ValueError(f"silu_mul: shapes {tuple(g.shape)} and {tuple(u.shape)} differ")
+    out = torch.empty_like(g)
+    _check_rc(_lib.i4_silu_mul_dev(_vp(g.data_ptr()), _vp(u.data_ptr()), g.numel(), _vp(out.data_ptr()),
+                                   _torch_stream(g)), "i4_silu_mul_dev")
     return out
 
 

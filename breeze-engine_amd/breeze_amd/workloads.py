@@ -16,8 +16,15 @@ CONFIGS = {
     "w4_decode": (4, 8, 12288, 4096, 4, 3, True),
     "w8_prefill": (8, 512, 5120, 17408, None, 4, False),
     "w8_lmhead": (8, 1, 5120, 151936, None, 5, False),
-    # Not a benchmark workload: the W4 counterpart of the prefill GEMM.
+    # Not benchmark workloads: the W4 counterpart of the prefill GEMM; two
+    # tall-skinny decode shapes (few column tiles over a long K: a 64-column
+    # projection of the MLP's 17408-wide activation, a 48-column one of a
+    # 12288-wide activation); and the decoder MLP's gate/up and down widths.
     "w4_prefill": (4, 512, 5120, 17408, 4, 6, False),
+    "w4_skinny_k17408": (4, 1, 17408, 64, 4, 7, False),
+    "w4_skinny_k12288": (4, 1, 12288, 48, 4, 8, False),
+    "w4_mlp_up": (4, 1, 5120, 17408, 4, 9, False),
+    "w4_mlp_down": (4, 1, 17408, 5120, 4, 10, False),
 }
 
 LABELS = {
@@ -27,6 +34,10 @@ LABELS = {
     "w8_prefill": "W8 prefill M={M} K=5120 N=17408, per-channel scales",
     "w8_lmhead": "W8 LM head M=1 K=5120 N=151936 + argmax, per-channel scales",
     "w4_prefill": "W4 prefill M={M} K=5120 N=17408, group-128 scales",
+    "w4_skinny_k17408": "W4 tall-skinny M={M} K=17408 N=64, group-128 scales",
+    "w4_skinny_k12288": "W4 tall-skinny M={M} K=12288 N=48, group-128 scales",
+    "w4_mlp_up": "W4 MLP gate/up width M={M} K=5120 N=17408, group-128 scales",
+    "w4_mlp_down": "W4 MLP down width M={M} K=17408 N=5120, group-128 scales",
 }
 
 
@@ -60,8 +71,11 @@ def make_config(name, rows=None):
     """Inputs of one workload: dict(qweight, scales, qzeros=None, A, bits, K, N).
 
     The W4 decode workload draws 8 rows (and its 1% x20 outliers) once and
-    keeps the first `rows`."""
+    keeps the first `rows`; the one-row shapes below the benchmark workloads
+    draw `rows` rows."""
     bits, M, K, N, group, seed, outliers = CONFIGS[name]
+    if rows is not None and rows > M:
+        M = rows
     rng = np.random.default_rng(seed)
     qweight, scales = make_weights(rng, bits, N, K, group)
     A = rng.standard_normal((M, K), dtype=np.float32)

@@ -22,37 +22,8 @@ namespace bq {
 // 128 * sum(b) of the two-pass product, which the four-row kernel takes from
 // two constant A rows, comes from a second MFMA per block of a constant A
 // operand with the same B operand.
-constexpr int kP8 = 14;
-constexpr int kRows8 = 8;
-
-// LDS: block scales and (INT4) -zp * sum(q) of the eight rows, row pitch
-// padded 16 B past a multiple of 256 B (the four rows a fold or epilogue
-// reads together fall on different banks), then the phase buffer
-// [2 buffers][2 rows][64 lanes][dec8_pitch(JG)] of f values, then (LREC) the
-// row group's activation records in their global layout.
-// Phase-buffer pitch (floats per lane) for 14 producers: JG-wide stores
-// and reads at this lane stride fall on distinct banks (60 l mod 64 are
-// distinct multiples of 4 over 16 lanes; 34 as in dec_kernel for JG = 2).
-__host__ __device__ constexpr int dec8_pitch(int JG) { return JG == 4 ? 60 : dec_pitch(JG); }
-static_assert(kP8 * 4 <= 60, "a producer's slot in the phase buffer");
-
-struct Dec8Lds {
-    int sa_pitch;         // elements per row
-    int sa, sq, fbuf, recs, total;  // byte offsets, bytes used
-};
-__host__ __device__ inline Dec8Lds dec8_lds(int nblk, int JG, bool lrec = false) {
-    Dec8Lds l;
-    l.sa_pitch = ((nblk + 3) / 4 * 4 + 59) / 64 * 64 + 4;
-    int off = 0;
-    l.sa = lds_take(off, kRows8 * l.sa_pitch * 4);
-    l.sq = lds_take(off, kRows8 * l.sa_pitch * 4);
-    l.fbuf = lds_take(off, 2 * 2 * 64 * dec8_pitch(JG) * 4);
-    l.recs = lds_take(off, lrec ? (nblk + JG - 1) / JG * JG * 512 : 0);
-    l.total = off;
-    return l;
-}
-// Records copied into LDS (LREC): at most this many uint4 per thread.
-constexpr int kRecCopy = 8;
+// kP8, kRows8, dec8_pitch, dec8_lds and kRecCopy are in qmm_common.h (the host
+// plans launches with them).
 
 // One weight chunk of a producer with its activation records (JG blocks of
 // 8 bytes per lane) and per-column metadata: one scale, or for EXTRA
@@ -343,7 +314,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
                     // silu(g) = g / (1 + exp(-g)) (qwen35_decoder.cpp:129),
                     // times the up projection (qwen35_decoder.cpp:408): the
                     // same expression as dec_kernel's.
-                    const float v = PAIR ? gate / (1.0f + expf(-gate)) * acc : acc;
+                    const float v = PAIR ? silu_mul(gate, acc) : acc;
                     const int gt = t_begin + pr_t;
                     if (MULTI) {
                         while (gt >= args.seg_end[pr_k]) ++pr_k;

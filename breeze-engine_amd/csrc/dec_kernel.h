@@ -463,7 +463,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 } else {
                     // silu(g) = g / (1 + exp(-g)) (qwen35_decoder.cpp:129),
                     // times the up projection (qwen35_decoder.cpp:408).
-                    const float v = PAIR ? gate / (1.0f + expf(-gate)) * acc : acc;
+                    const float v = PAIR ? silu_mul(gate, acc) : acc;
                     if (MULTI) {
                         // Tiles come in increasing order: step into the
                         // segment of this one.

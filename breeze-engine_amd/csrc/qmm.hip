@@ -42,7 +42,6 @@
 
 #include "../../include/breeze_qmm.h"
 #include "qmm_common.h"
-#include "dec8_kernel.h"
 
 using namespace bq;
 
@@ -722,17 +721,13 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     if (threadIdx.x == 0) part[(size_t)c * gridDim.y + m] = best;
 }
 
-// part [nparts][M] -> out[m].
-// u = silu(g) * u elementwise, silu(x) = x / (1 + exp(-x)) as in
-// kernel/qwen35_decoder.cpp:129 and 408; the same expression as the paired
-// decode kernel's epilogue, so both paths give the same bits.
-__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ g, float* __restrict__ u,
+// out = silu(g) * u elementwise (kernel/qwen35_decoder.cpp:128 and 408;
+// silu_mul, the paired decode kernels' epilogue, so every path gives the
+// reference's bits).  out may be u.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ g, const float* u, float* out,
                                                        size_t n) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
-    if (i < n) {
-        const float x = g[i];
-        u[i] = x / (1.0f + expf(-x)) * u[i];
-    }
+    if (i < n) out[i] = silu_mul(g[i], u[i]);
 }
 
 __global__ __launch_bounds__(256) void argmax_final_kernel(const unsigned long long* __restrict__ part,
@@ -1473,8 +1468,8 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     }
     if (!hip_ok(e, "matmul launch")) return -5;
 
-    if (dIdx && !dots && !dec) {
-        // The decode kernel merges its own argmax (last workgroup).
+    if (dIdx && !dots && !dec && !dec8) {
+        // Both decode kernels merge their own argmax (last workgroup).
         const int nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
         if (!grow(w, st, &s.parts, &s.parts_cap, (size_t)M * nparts, "argmax workspace", s.fixed)) return -4;
         argmax_partial_kernel<<<dim3(nparts, M), 256, 0, st>>>(dC, h->N, s.parts);
@@ -1532,6 +1527,15 @@ bool check_dims(int N, int K, int bits) {
     if (N <= 0 || K <= 0 || N % 16 || K % 32 || (bits != 4 && bits != 8)) {
         set_err("contract violation: need N>0, K>0, N%%16==0, K%%32==0, bits in {4,8} "
                 "(got N=%d K=%d bits=%d)", N, K, bits);
+        return false;
+    }
+    // The decode kernels address a handle's weights with 32-bit cursors in
+    // 16-byte chunks: at most 2^32 chunks (64 GiB of packed weights).
+    const uint64_t jg = bits == 8 ? 2 : 4;
+    const uint64_t chunks = (uint64_t)(N / 16) * ((uint64_t)(K / 32) + jg - 1) / jg * 64;
+    if (chunks > 0xFFFFFFFFull) {
+        set_err("weights of N=%d K=%d at %d bits take %llu 16-byte chunks; the kernels address at most 2^32 "
+                "(64 GiB)", N, K, bits, (unsigned long long)chunks);
         return false;
     }
     return true;
@@ -1746,9 +1750,25 @@ int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* 
         int rc = run(w, s, hg, dA, M, s.gate, nullptr, nullptr, st);
         if (rc == 0) rc = run(w, s, hu, dA, M, dC, nullptr, nullptr, st);
         if (rc) return rc;
-        silu_mul_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(s.gate, dC, n);
+        silu_mul_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(s.gate, dC, dC, n);
         return hip_ok(hipGetLastError(), "silu-mul launch") ? 0 : -5;
     });
+}
+
+int i4_silu_mul_dev(const float* dG, const float* dU, size_t n, float* dOut, void* stream) {
+    if (n == 0) return 0;
+    if (!dG || !dU || !dOut) {
+        set_err("null device pointer");
+        return -2;
+    }
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const size_t blocks = (n + 255) / 256;
+    if (blocks > 0x7FFFFFFFu) {
+        set_err("silu-mul: %zu elements are more than one launch covers", n);
+        return -2;
+    }
+    silu_mul_kernel<<<(unsigned)blocks, 256, 0, st>>>(dG, dU, dOut, n);
+    return hip_ok(hipGetLastError(), "silu-mul launch") ? 0 : -5;
 }
 
 int i4_matmul_multi_dev(void* const* handles, int n, const float* dA, int M, float* const* dC, void* stream) {

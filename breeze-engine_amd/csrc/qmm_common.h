@@ -256,6 +256,54 @@ struct Unit {
     int c;        // chunk to compute; nbg or more: none (past the end)
 };
 
+// ------------------------------------------------------------------ SiLU
+//
+// The reference's siluf (kernel/qwen35_decoder.cpp:128) is x / (1 + std::exp(-x))
+// in float, and std::exp(float) there is the host C library's expf: glibc's
+// table-driven expf (since glibc 2.27; x86-64 runs its FMA build), which is
+// not correctly rounded.  ref_expf restates that published method step for
+// step, in double: x * 32/ln2 = k + r with k = round(x * 32/ln2) and r from
+// fused multiply-adds, exp(x) = 2^(k/32) * (1 + c2 r + c1 r^2 + c0 r^3), the
+// 2^(i/32) factors (correctly rounded to double, exponent field offset by
+// -i/32) from a table, one rounding to float at the end; below and above the
+// range the library's own overflow and underflow results.  Equal to the host
+// expf on every float (the tests compare them exhaustively), so the fused
+// SiLU matches the reference bit for bit.
+__host__ __device__ inline float ref_expf(float x) {
+    static constexpr uint64_t kTab[32] = {
+        0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+        0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+        0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+        0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+        0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+        0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+        0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+        0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+    constexpr double kInvLn2N = 0x1.71547652b82fep+5;  // 32 / ln 2
+    constexpr double kShift = 0x1.8p+52;               // rounds to an integer in the low bits
+    constexpr double kC0 = 0x1.c6af84b912394p-20, kC1 = 0x1.ebfce50fac4f3p-13, kC2 = 0x1.62e42ff0c52d6p-6;
+    const uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    if (((ux >> 20) & 0x7ff) >= 0x42b) {  // |x| >= 88, inf or NaN
+        if (ux == 0xff800000u) return 0.0f;
+        if (((ux >> 20) & 0x7ff) >= 0x7f8) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();  // exp(x) above the float range
+        if (x < -0x1.9fe368p6f) return 0.0f;              // below half the smallest subnormal
+    }
+    const double xd = (double)x;
+    double kd = __builtin_fma(kInvLn2N, xd, kShift);
+    const uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= kShift;
+    const double r = __builtin_fma(kInvLn2N, xd, -kd);
+    const double s = __builtin_bit_cast(double, kTab[ki % 32] + (ki << 47));
+    const double z = __builtin_fma(kC0, r, kC1);
+    double y = __builtin_fma(kC2, r, 1.0);
+    y = __builtin_fma(z, r * r, y);
+    return (float)(y * s);
+}
+
+// silu(g) * u exactly as the reference's loop (qwen35_decoder.cpp:408) forms it.
+__host__ __device__ inline float silu_mul(float g, float u) { return g / (1.0f + ref_expf(-g)) * u; }
+
 __device__ inline unsigned long long argmax_key(float v, int idx) {
     uint32_t o;
     if (v != v) {
@@ -516,6 +564,42 @@ struct PfCfg {
 constexpr PfCfg kPfCfgs[] = {{4, 17, 2}, {4, 16, 2}, {4, 13, 2}, {4, 12, 2}, {4, 9, 2}, {4, 8, 2}, {4, 5, 2},
                              {4, 4, 2},  {2, 16, 2}, {2, 8, 3},  {2, 4, 3},  {1, 16, 2}, {1, 8, 3}};
 constexpr int kPfNumCfgs = sizeof(kPfCfgs) / sizeof(kPfCfgs[0]);
+
+// ------------------------------------------------------------------ decode in row groups of eight
+//
+// dec8_kernel (dec8_kernel.h): 14 producer waves (chunk 14p + w of phase p)
+// and two chain waves per workgroup of eight activation rows.
+constexpr int kP8 = 14;
+constexpr int kRows8 = 8;
+
+// LDS: block scales and (INT4) -zp * sum(q) of the eight rows, row pitch
+// padded 16 B past a multiple of 256 B (the four rows a fold or epilogue
+// reads together fall on different banks), then the phase buffer
+// [2 buffers][2 rows][64 lanes][dec8_pitch(JG)] of f values, then (LREC) the
+// row group's activation records in their global layout.
+// Phase-buffer pitch (floats per lane) for 14 producers: JG-wide stores
+// and reads at this lane stride fall on distinct banks (60 l mod 64 are
+// distinct multiples of 4 over 16 lanes; 34 as in dec_kernel for JG = 2).
+__host__ __device__ constexpr int dec8_pitch(int JG) { return JG == 4 ? 60 : dec_pitch(JG); }
+static_assert(kP8 * 4 <= 60, "a producer's slot in the phase buffer");
+
+struct Dec8Lds {
+    int sa_pitch;         // elements per row
+    int sa, sq, fbuf, recs, total;  // byte offsets, bytes used
+};
+__host__ __device__ inline Dec8Lds dec8_lds(int nblk, int JG, bool lrec = false) {
+    Dec8Lds l;
+    l.sa_pitch = ((nblk + 3) / 4 * 4 + 59) / 64 * 64 + 4;
+    int off = 0;
+    l.sa = lds_take(off, kRows8 * l.sa_pitch * 4);
+    l.sq = lds_take(off, kRows8 * l.sa_pitch * 4);
+    l.fbuf = lds_take(off, 2 * 2 * 64 * dec8_pitch(JG) * 4);
+    l.recs = lds_take(off, lrec ? (nblk + JG - 1) / JG * JG * 512 : 0);
+    l.total = off;
+    return l;
+}
+// Records copied into LDS (LREC): at most this many uint4 per thread.
+constexpr int kRecCopy = 8;
 
 // Launchers, one explicit instantiation per (bits, activation mode) in the
 // kernel units dec_w*.hip and pf_w*.hip.  attr_set / pf_attr: this device's

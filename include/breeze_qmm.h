@@ -94,11 +94,20 @@ int i4_matmul_argmax_dev(void* handle, const float* dA, int M, float* dC,
 /* Fused gate/up projection of a decoder MLP, replacing the two i4_matmul calls
  * and the SiLU loop of kernel/qwen35_decoder.cpp:406-408:
  *   dC[M,N] = silu(dA * Wgate) * (dA * Wup),  silu(x) = x / (1 + exp(-x)).
- * Both projections are bit-identical to i4_matmul_dev's; the SiLU uses the
- * device expf.  With M <= 8 and handles of the same layout it is one decode
- * launch (SiLU and product in the epilogue); otherwise two launches and an
- * elementwise kernel with the same arithmetic.  Returns as i4_matmul_dev. */
+ * Both projections are bit-identical to i4_matmul_dev's, and the SiLU and
+ * product are the reference's bit for bit (its expf, the host C library's,
+ * restated on the device).  When a decode launch takes both projections it
+ * is one launch (SiLU and product in the epilogue); otherwise two launches
+ * and i4_silu_mul_dev's kernel.  Returns as i4_matmul_dev. */
 int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* dC, void* stream);
+
+/* The decoder MLP's elementwise step on device pointers, replacing the loop
+ * g1[i] = siluf(g1[i]) * g2[i] of kernel/qwen35_decoder.cpp:408 (siluf at
+ * 128): dOut[i] = dG[i] / (1 + expf(-dG[i])) * dU[i] for i < n, bit for bit
+ * the reference's (its expf is the host C library's; the device restates
+ * it).  dOut may equal dG or dU.  Asynchronous on `stream`.  Returns 0, or a
+ * negative code with i4_last_error() set. */
+int i4_silu_mul_dev(const float* dG, const float* dU, size_t n, float* dOut, void* stream);
 
 /* i4_matmul_dev, or i4_matmul_argmax_dev when dIdx is not NULL, that
  * allocates nothing: no hipMalloc, hipFree or allocating library call.  It
@@ -106,8 +115,10 @@ int i4_matmul_silu_mul_dev(void* gate, void* up, const float* dA, int M, float* 
  * allocate, such as code under HIP graph capture or serving loops that
  * forbid it.  All of its device scratch is one static 16 MiB array per
  * device, so a call whose activation records do not fit is refused (-4,
- * i4_last_error() says why): about 72 bytes per row and 32-block of K when
- * the decode kernel stages its records (up to 32 rows, M*K above 16384), and
+ * i4_last_error() says why): 72 bytes per row and 32-block of K when
+ * the decode kernel stages its records (up to 32 rows, M*K above 16384), with
+ * K counted rounded up to a multiple of 128 and, from 5 to 32 rows, M rounded
+ * up to a multiple of 8 (the eight-row groups' records cover whole groups), and
  * about 68 bytes per 32-block of K per row, rows rounded up to 32, 64 or 128, for
  * the rows the prefill GEMM takes.  Calls that overlap on one device share the array and
  * race: serialize them.  Outputs are those of i4_matmul_dev /

@@ -3,11 +3,13 @@
 Times the reference CPU kernel (kernel/quantized_matmul.cpp of breeze-engine,
 compiled from its own source into oracle/_ref by oracle/Makefile) on this
 host's cores, for the benchmark workloads, as the reference's benchmark
-plan prescribes (benchmark_cpu_matmul.py:46-54, 64-66;
-benchmark_qwen35_cpu.py:132-135): two-pass INT16 activations, NUMA replica
-off, T OpenMP threads bound one per physical core, prepack untimed, 3
-warmup calls, then up to 20 timed calls (fewer when a call is long, so one
-workload's sample stays within a few seconds).  Without the reference build
+times it (benchmark_cpu_matmul.py:43-54, 64-66; benchmark_qwen35_cpu.py:
+132-135): two-pass INT16 activations set once, NUMA replica off, T OpenMP
+threads bound one per physical core, prepack untimed, the native i4_matmul
+on preallocated input and output, 3 warmup calls, then up to 20 timed calls
+(fewer when a call is long, so one workload's sample stays within a few
+seconds), reported as the mean (the reference benchmark's figure), median
+and minimum per call.  Without the reference build
 it times the oracle's scalar C restatement on one core instead.
 
 bench.py runs this file as a child process, so the OpenMP environment
@@ -68,14 +70,25 @@ def physical_cores(cpus):
 
 
 def cpu_model():
+    """The CPU's brand string (cpuid, as /proc/cpuinfo reports it) with its
+    family, model and stepping, which name the part where a virtual machine
+    shortens the brand string, and the AVX-512 features the reference kernel
+    needs."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if not line.strip():
+                    break  # the first logical CPU is enough
+                k, _, v = line.partition(":")
+                fields[k.strip()] = v.strip()
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = set(fields.get("flags", "").split())
+    isa = [x for x in ("avx512f", "avx512_vnni", "avx512vbmi", "avx512_bf16", "avx512_fp16") if x in flags]
+    return (f"{fields.get('model name', 'unknown')} (vendor {fields.get('vendor_id', '?')}, family "
+            f"{fields.get('cpu family', '?')}, model {fields.get('model', '?')}, stepping "
+            f"{fields.get('stepping', '?')}; {' '.join(isa) or 'no AVX-512'})")
 
 
 def main():
@@ -107,19 +120,29 @@ def main():
                 flags = f.read().strip()
         except OSError:
             pass
+    import ctypes
+
+    if ref is not None:
+        ref.lib.i4_set_hi_prec(1)  # two-pass INT16, once, outside the timed calls
     results = []
     for name, rows in todo:
         d = workloads.make_config(name, rows)
-        M = d["A"].shape[0]
+        A = np.ascontiguousarray(d["A"], np.float32)
+        M = A.shape[0]
+        C = np.empty((M, d["N"]), np.float32)
         h = None
         if ref is not None:
             h = ref.prepack(d["qweight"], d["scales"], None, d["N"], d["K"], d["bits"])
+            # The native entry point on preallocated input and output, as the
+            # reference's benchmark calls it (benchmark_cpu_matmul.py:43-54).
+            native = ref.lib.i4_matmul
+            args = (ctypes.c_void_p(h), A.ctypes.data_as(ctypes.c_void_p), M, C.ctypes.data_as(ctypes.c_void_p))
 
             def run():
-                ref.matmul(h, d["A"], d["N"], hi_prec=True)
+                native(*args)
         else:
             def run():
-                orc.matmul(d["qweight"], d["scales"], None, d["N"], d["K"], d["bits"], d["A"], True)
+                orc.matmul(d["qweight"], d["scales"], None, d["N"], d["K"], d["bits"], A, True)
         try:
             for _ in range(WARMUP):
                 run()
@@ -133,7 +156,9 @@ def main():
             if h is not None:
                 ref.free(h)
         dt = float(np.mean(times))
-        entry = {"workload": workloads.LABELS[name].format(M=M), "us": round(dt * 1e6, 1), "calls": len(times)}
+        entry = {"workload": workloads.LABELS[name].format(M=M), "us": round(dt * 1e6, 1),
+                 "us_median": round(float(np.median(times)) * 1e6, 1), "us_min": round(min(times) * 1e6, 1),
+                 "calls": len(times)}
         if name.endswith("prefill"):
             entry["tops"] = round(workloads.algorithmic_ops(name, M) / dt / 1e12, 3)
         else:

@@ -54,6 +54,8 @@ class _COracle:
         lib.orc_matmul_legacy.argtypes = [_vp] * 4 + [_i] * 4 + [_vp, _i, _i, _vp]
         lib.orc_rmsnorm.argtypes = [_vp, _vp, _i, _i, ctypes.c_float, _vp]
         lib.orc_sumsq.argtypes = [_vp, _i, _i, _vp]
+        lib.orc_silu_mul.argtypes = [_vp, _vp, ctypes.c_longlong, _vp]
+        lib.orc_silu_mul.restype = None
         self.lib = lib
 
     def half_to_float(self, h):
@@ -158,6 +160,16 @@ class _COracle:
         s, H = x.shape
         out = np.empty_like(x)
         self.lib.orc_rmsnorm(_p(x), _p(w), s, H, float(eps), _p(out))
+        return out
+
+    def silu_mul(self, g, u):
+        """g / (1 + expf(-g)) * u in float with the host C library's expf, as
+        the reference's decoder forms it (qwen35_decoder.cpp:128, 408)."""
+        g = np.ascontiguousarray(g, np.float32)
+        u = np.ascontiguousarray(u, np.float32)
+        assert g.shape == u.shape
+        out = np.empty_like(g)
+        self.lib.orc_silu_mul(_p(g), _p(u), g.size, _p(out))
         return out
 
     def sumsq(self, x):

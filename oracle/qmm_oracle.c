@@ -336,3 +336,12 @@ ORC_API void orc_sumsq(const float* x, int s, int H, double* ss_out) {
         ss_out[i] = ss;
     }
 }
+
+/* The decoder MLP's elementwise step (qwen35_decoder.cpp:408, siluf at 128):
+ * out[i] = g[i] / (1 + expf(-g[i])) * u[i] in float, where expf is the host
+ * C library's, the very function the reference's std::exp(float) calls.
+ * Rows are independent, so the loop is split over OpenMP threads. */
+ORC_API void orc_silu_mul(const float* g, const float* u, long long n, float* out) {
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < n; ++i) out[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+}

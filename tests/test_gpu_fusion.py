@@ -2,13 +2,14 @@
 replacing kernel/qwen35_decoder.cpp:406-408: g1 = i4_matmul(gate), g2 =
 i4_matmul(up), g1 = siluf(g1) * g2 with siluf(x) = x / (1 + exp(-x)).
 
-Both projections are the exact path (bit-identical to the oracle), so the
-result is compared with the oracle's projections through float32 SiLU and
-product: the only difference allowed is exp's last-place rounding (the
-device expf against numpy's), bounded here at 1e-6 relative.  The one-launch
-path (handles of the same layout; up to 16 rows on the four-row groups, 32 on
-the eight-row groups) and the two-launch fallback use the same device
-arithmetic and must agree bit for bit."""
+Both projections are the exact path (bit-identical to the oracle), and the
+SiLU and product are the reference's bit for bit: the expected values are
+the oracle's projections through the oracle's silu * u, which forms
+g / (1 + expf(-g)) * u with the host C library's expf, the function the
+reference's siluf calls.  The one-launch path (handles of the same layout; up
+to 16 rows on the four-row groups, 32 on the eight-row groups), the
+two-launch fallback and the elementwise entry point (i4_silu_mul_dev) are all
+held to those bits."""
 import numpy as np
 import pytest
 
@@ -18,8 +19,8 @@ pytestmark = pytest.mark.gpu
 
 
 def _silu_mul(g, u):
-    g = g.astype(np.float32)
-    return (g / (np.float32(1) + np.exp(-g))) * u.astype(np.float32)
+    from oracle import oracle
+    return oracle.c_oracle().silu_mul(g, u)
 
 
 def _group4(s):
@@ -59,7 +60,7 @@ def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, monkeypatc
             fused = {}
             for rows in (1, 2, 3, 5, 8, 12, 16):
                 got = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A[:rows]).cuda(), N).cpu().numpy()
-                np.testing.assert_allclose(got, want[:rows], rtol=1e-6, atol=1e-30, err_msg=f"{rows} rows")
+                assert bits_equal(got, want[:rows]), f"{rows} rows"
                 fused[rows] = got
             # Twenty rows: one launch where the eight-row groups take the
             # call (K past 4096, no per-block metadata), else the two-launch
@@ -73,7 +74,7 @@ def test_fused_gate_up_matches_the_composition(gpu, hb, orc, hi_prec, monkeypatc
             assert bits_equal(got20[:16], fused[16]), hp
             assert bits_equal(got20[:1], fused[1]), hp
             assert bits_equal(two, got20), hp
-            np.testing.assert_allclose(got20, want, rtol=1e-6, atol=1e-30)
+            assert bits_equal(got20, want), hp
     finally:
         hb.free(hg)
         hb.free(hu)
@@ -90,9 +91,36 @@ def test_fused_gate_up_with_different_layouts_and_bad_shapes(gpu, hb, orc, hi_pr
         A = rng.normal(size=(2, K)).astype(np.float32)
         got = hb.matmul_silu_mul(hg, hu, torch.from_numpy(A).cuda(), N).cpu().numpy()
         want = _silu_mul(orc.matmul(qg, sg, zg, N, K, 4, A, True), orc.matmul(qu, su, zu, N, K, 4, A, True))
-        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-30)
+        assert bits_equal(got, want)
         with pytest.raises(RuntimeError, match="differ in shape"):
             hb.matmul_silu_mul(hg, other, torch.from_numpy(A).cuda(), N)
     finally:
         for h in (hg, hu, other):
             hb.free(h)
+
+
+def _same(got, want):
+    """Bitwise equality, any NaN matching any NaN."""
+    nan = np.isnan(got) & np.isnan(want)
+    return np.array_equal(np.isnan(got), np.isnan(want)) and \
+        np.array_equal(got.view(np.uint32)[~nan], want.view(np.uint32)[~nan])
+
+
+def test_silu_mul_entry_point_is_the_reference_on_a_sweep_of_floats(gpu, hb, orc):
+    """i4_silu_mul_dev against the oracle (the C library's expf) on one in
+    16 float bit patterns (268 million gate values over all signs and
+    exponents, so the overflow and underflow branches and the subnormal
+    results too), each with a random up value, and on edge values."""
+    torch = gpu
+    rng = np.random.default_rng(12)
+    for start in range(0, 64, 16):
+        g = (np.arange(start, 1 << 32, 64, dtype=np.uint64) + rng.integers(0, 64)).astype(np.uint32).view(np.float32)
+        u = rng.normal(0, 1, g.size).astype(np.float32)
+        got = hb.silu_mul(torch.from_numpy(g).cuda(), torch.from_numpy(u).cuda()).cpu().numpy()
+        assert _same(got, orc.silu_mul(g, u)), start
+    hexes = ["0x1.62e42ep6", "0x1.62e430p6", "-0x1.9fe368p6", "-0x1.9fe36ap6", "0x1.60p6", "-0x1.60p6"]
+    edge = np.array([0.0, -0.0, 1e-45, -1e-45, 88.72, -88.72, 103.97, -103.97, 3.4e38, -3.4e38, np.inf, -np.inf,
+                     np.nan] + [float.fromhex(h) for h in hexes], np.float32)
+    ones = np.ones_like(edge)
+    got = hb.silu_mul(torch.from_numpy(edge).cuda(), torch.from_numpy(ones).cuda()).cpu().numpy()
+    assert _same(got, orc.silu_mul(edge, ones))

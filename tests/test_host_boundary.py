@@ -55,6 +55,24 @@ def test_native_prepack_rejects_contract_violations_without_a_device(hb):
     assert "zero" in hb.last_error()
 
 
+def test_native_prepack_refuses_weights_past_the_kernels_cursors(hb):
+    """The decode kernels address weights with 32-bit cursors over 16-byte
+    chunks: a handle of 64 GiB or more is refused before any buffer is read
+    (the tiny buffers here are never touched), by both packers."""
+    lib = hb._lib
+    qw = np.zeros(16, np.uint8)
+    sc = np.ones(16, np.float32)
+    # INT4: N * K / 2 bytes; 2^20 x 2^17 is exactly 64 GiB, one 32-block less fits.
+    assert not lib.i4_prepack_onnx(hb._p(qw), hb._p(sc), None, 1 << 20, 1 << 17, 4, 32)
+    assert "2^32" in hb.last_error()
+    # INT8: N * K bytes; 2^20 x 2^16 is 64 GiB.
+    assert not lib.i4_prepack_onnx(hb._p(qw), hb._p(sc), None, 1 << 20, 1 << 16, 8, 32)
+    assert "2^32" in hb.last_error()
+    corr = np.zeros(16, np.int32)
+    assert not lib.i4_prepack(hb._p(qw), hb._p(sc), None, hb._p(corr), 1 << 20, 1 << 16, 1 << 11, 8)
+    assert "2^32" in hb.last_error()
+
+
 def test_native_calls_reject_a_foreign_handle(hb):
     bogus = np.zeros(64, np.uint8)
     A = np.zeros((1, 32), np.float32)
@@ -150,6 +168,27 @@ def test_dequant_contract_matches_oracle():
         b = oracle.dequantize_matmul_nbits(qw, sc, qz, bits=bits, block_size=32, K=K, N=N)
         assert a.shape == (K, N)
         assert np.array_equal(a, b)
+
+
+def test_dequant_equals_the_oracles_unpacked_weights_times_scales(orc):
+    """breeze/quant.py:9-58 against the C oracle's unpacking (the one the
+    golden vectors pin through every matmul): W[k, n] = b[n, k] * s[n, k/32]
+    exactly, with b = nibble - zero point (explicit packed INT4 zero points,
+    low nibble first, odd block counts so the last zero-point byte is half
+    used) or byte - 128, fp16 and fp32 scales.  (q - zp) is an exact small
+    integer in float, so both sides round once."""
+    from breeze_amd import quant
+
+    rng = np.random.default_rng(15)
+    for bits, explicit in ((4, True), (4, False), (8, False)):
+        for dtype in (np.float16, np.float32):
+            N, K = 48, 32 * 7
+            qw, sc, qz = rng_weights(rng, N, K, bits, dtype, explicit)
+            W = quant.dequantize_matmul_nbits(qw, sc, qz, bits=bits, block_size=32, K=K, N=N)
+            b, sb = orc.unpack_nbits(qw, sc, qz, N, K, bits)
+            want = (b.astype(np.float32) * np.repeat(sb, 32, axis=1)).T
+            assert W.dtype == np.float32 and W.shape == (K, N)
+            assert np.array_equal(W.view(np.uint32), np.ascontiguousarray(want).view(np.uint32)), (bits, explicit)
 
 
 def test_linear_api_on_cpu():

@@ -102,3 +102,56 @@ def test_c_oracle_matches_compiled_reference_random(orc, bits, hp):
         A = (rng.normal(size=(rows, K)) * rng.choice([1e-3, 1.0, 100.0], size=(rows, 1))).astype(np.float32)
         want = ref.run(qw, sc, qz, N, K, bits, A, hp)
         assert bits_equal(orc.matmul(qw, sc, qz, N, K, bits, A, hp), want), (N, K, rows)
+
+
+NATIVE = os.path.join(os.path.dirname(GOLDEN), "..", "oracle", "_ref", "libref_qmm_native.so")
+NATIVE_HOST = os.path.join(os.path.dirname(NATIVE), "native_host.txt")
+
+
+def _this_cpu():
+    with open("/proc/cpuinfo") as f:
+        for line in f:
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    return None
+
+
+def _native_usable():
+    # The -march=native build runs only on the CPU it was built for.
+    return os.path.exists(NATIVE) and os.path.exists(NATIVE_HOST) and \
+        open(NATIVE_HOST).read().strip() == _this_cpu()
+
+
+@pytest.mark.skipif(not _native_usable(), reason="no -march=native reference build for this CPU "
+                                                 "(make -C oracle ref-native)")
+@pytest.mark.parametrize("name", sorted(META))
+def test_native_flag_build_gives_the_golden_bits(name):
+    """The golden vectors come from the reference built with an explicit ISA
+    level (-march=x86-64-v4 -mavx512vnni -mavx512vbmi -mf16c).  The
+    reference's own build line says -march=native (build_kernel.py:17); built
+    that way on this host, the same source gives the same bits on every
+    golden case: both activation modes, the quantizer's edge blocks, the
+    non-finite activations (the q = 0 rule) and the legacy layout."""
+    from oracle import oracle
+
+    ref = oracle.Ref(path=NATIVE, threads=2)
+    m = META[name]
+    N, K, bits = m["N"], m["K"], m["bits"]
+    A = _get(name, "A")
+    if name.startswith("legacy"):
+        B, scale, zp, corr = (_get(name, k) for k in ("B", "scale", "zp", "corr"))
+        h = ref.lib.i4_prepack(B.ctypes.data, scale.ctypes.data, None if zp is None else zp.ctypes.data,
+                               corr.ctypes.data, N, K, K // 32, bits)
+        assert h
+    else:
+        h = ref.prepack(_get(name, "qweight"), _get(name, "scales"), _get(name, "qzeros"), N, K, bits)
+    try:
+        for hp in (True, False):
+            want = _get(name, f"C_hp{int(hp)}")
+            if want is not None:
+                assert bits_equal(ref.matmul(h, A, N, hi_prec=hp), want), (name, hp)
+        want = _get(name, "C_hp1_row0")
+        if want is not None:
+            assert bits_equal(ref.matmul(h, A[:1], N, hi_prec=True), want), name
+    finally:
+        ref.free(h)
