@@ -377,7 +377,7 @@ def _pct(vals, q):
     return v[min(len(v) - 1, int(q * (len(v) - 1) + 0.5))]
 
 
-def profile_summary(d, cal, workload, kernel, steps, commit, out, traffic_out=None):
+def profile_summary(d, cal, workload, kernel, steps, commit, out, traffic_out=None, graph=False):
     """Writes the summary of the profile in directory d (see above) of one
     workload's dominant kernel (`kernel`: a substring of its name)."""
     from breeze_amd import workloads
@@ -434,7 +434,7 @@ def profile_summary(d, cal, workload, kernel, steps, commit, out, traffic_out=No
         "Commands (from the repository root, each its own process, all on one box; D and C are",
         "output directories):",
         f"  rocprofv3 --kernel-trace --stats --output-format csv -d D/trace -o t -- "
-        f"python3 -u bench.py {wl} --steps {steps} --warmup 5",
+        f"python3 -u bench.py {wl} --steps {steps} --warmup 5{' --graph' if graph else ''}",
         f"  rocprofv3 --pmc FETCH_SIZE --output-format csv -d D/fetch -o p -- python3 -u bench.py {wl} "
         "--steps 50 --warmup 2",
         f"  rocprofv3 --pmc WRITE_SIZE --output-format csv -d D/write -o p -- python3 -u bench.py {wl} "
@@ -442,10 +442,12 @@ def profile_summary(d, cal, workload, kernel, steps, commit, out, traffic_out=No
         "  rocprofv3 --pmc FETCH_SIZE (and WRITE_SIZE) --output-format csv -d C/fetch (C/write) -o p -- "
         "python3 -u bench.py --copy-calibration",
         f"  python3 -u bench.py {wl} --steps {steps} --warmup 20 > D/plain.json   (no profiler)",
-        f"  python3 bench.py --profile-summary D --calibration C --workload {workload} --kernel {kernel} "
-        f"--commit {commit} --out <this file>",
+        f"  python3 bench.py --profile-summary D --calibration C --workload {workload} --kernel '{kernel}' "
+        f"--commit {commit}{' --graph' if graph else ''} --out <this file>",
         "",
-        f"Kernel trace, the last {steps} timed dispatches of {kernel}:",
+        f"Kernel trace, the last {steps} timed dispatches of {kernel}"
+        + (" (one replay of a HIP graph of the timed calls, so the dispatches follow each other as in "
+           "bench.py's timed loop, whose host enqueue the profiler would otherwise slow down):" if graph else ":"),
         f"  mean {mean:.3f} us, median {med:.3f}, p10 {_pct(us, 0.1):.3f}, p90 {_pct(us, 0.9):.3f}, "
         f"min {min(us):.3f}, max {max(us):.3f}",
         f"  consecutive dispatches start {spacing:.3f} us apart (median) under the profiler",
@@ -463,11 +465,10 @@ def profile_summary(d, cal, workload, kernel, steps, commit, out, traffic_out=No
             "",
             f"Without the profiler, same box: {pu:.3f} us per call over {plain['steps']} back-to-back calls "
             f"(HIP events around the timed calls) -> {rate(pu)}.",
-            "  bench.py reports this figure.  It counts every kernel of a call and the boundary",
-            "  between calls, whose launches overlap the tail of the call before.  Under the profiler",
-            "  the host enqueues more slowly (the dispatch spacing above), so each dispatch starts on",
-            "  an idle GPU.  Profiled kernel time against the per-call time: mean "
-            f"{mean / pu:.3f}x, median {med / pu:.3f}x.",
+            "  bench.py reports this figure; it counts every kernel of a call and the boundary between",
+            f"  calls.  Profiled kernel time against it: mean {mean / pu:.3f}x, median {med / pu:.3f}x"
+            + ("." if graph else "; under the profiler the host enqueues more slowly (the dispatch "
+                                 "spacing above), so each dispatch starts on an idle GPU."),
         ]
     lines += ["", "rocprofv3 kernel_stats.csv (every dispatch of the run, set-up included):"]
     lines += ["  " + x.rstrip() for x in open(os.path.join(d, "trace", "t_kernel_stats.csv"))][:12]
@@ -596,7 +597,7 @@ def main():
         if not (args.workload and args.out):
             raise SystemExit("bench.py: --profile-summary needs --workload and --out")
         profile_summary(args.profile_summary, args.calibration, args.workload, args.kernel, args.steps,
-                        args.commit, args.out, args.traffic_out)
+                        args.commit, args.out, args.traffic_out, graph=args.graph)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported. "

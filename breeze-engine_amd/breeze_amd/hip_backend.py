@@ -88,6 +88,8 @@ try:
     _lib.i4_silu_mul_dev.argtypes = [_vp, _vp, ctypes.c_size_t, _vp, _vp]
     _lib.i4_block_dots_dev.restype = _i
     _lib.i4_block_dots_dev.argtypes = [_vp, _vp, _i, _vp, _vp]
+    _lib.i4_plan_query.restype = _i
+    _lib.i4_plan_query.argtypes = [_i, _i, _i, _i, _i, _i, _vp, _i]
     _lib.i4_handle_info.restype = _i
     _lib.i4_handle_info.argtypes = [_vp, _vp]
     _lib.i4_unpack.restype = _i
@@ -296,6 +298,28 @@ def matmul_silu_mul(gate, up, a2d, N):
     _check_rc(_lib.i4_matmul_silu_mul_dev(_vp(gate), _vp(up), _vp(a.data_ptr()), int(M), _vp(out.data_ptr()),
                                           _torch_stream(a)), "i4_matmul_silu_mul_dev")
     return out
+
+
+PLAN_FIELDS = ("route", "quant", "fused", "p64", "lrec", "rows_per_group", "row_groups", "tile_ranges", "pair_xcd",
+               "lds", "pf_rp", "pf_ct", "grid_x", "grid_y")
+ROUTES = {0: None, 1: "decode", 2: "decode8", 3: "prefill", 4: "rows"}
+QUANTIZERS = {0: None, 1: "staged", 2: "rows8", 3: "prefill"}
+
+
+def plan(bits, M, K, N, n_cu=256, dots=False, argmax=False, pair=False, multi=False, norm=False, extra=False,
+         legacy_corr=False):
+    """The library's routing decision for a call (i4_plan_query), without a
+    device: which kernel, which stand-alone quantizer and the launch shape."""
+    _require_lib()
+    flags = (1 * dots) | (2 * argmax) | (4 * pair) | (8 * multi) | (16 * norm) | (32 * extra) | (64 * legacy_corr)
+    out = np.zeros(len(PLAN_FIELDS), np.int32)
+    n = _lib.i4_plan_query(int(bits), int(M), int(K), int(N), flags, int(n_cu), _p(out), len(out))
+    if n < 0:
+        raise ValueError(f"i4_plan_query: {last_error()}")
+    d = dict(zip(PLAN_FIELDS, (int(v) for v in out)))
+    d["route"] = ROUTES[d["route"]]
+    d["quant"] = QUANTIZERS[d["quant"]]
+    return d
 
 
 def silu_mul(g, u):

@@ -1050,38 +1050,82 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
     a.ntiles = h->N / 16;
 }
 
-constexpr int kFusedMaxBlocks = kQuantPasses * 256;  // row-blocks the prologue quantizes
-constexpr int kNormFusedMaxBlocks = 3 * 128;  // with the RMSNorm in the prologue
-
-// LDS bytes of the decode kernel, or 0 if the activation records of a row
-// group do not fit (in LDS, or in the prologue's 6-uint4-per-thread record
-// copy).
-// Most rows the decode kernel takes (row groups, the workgroups of one tile
-// range on one XCD) before the prefill GEMM does.  Measured GEMM -> decode
-// (us): at 12 / 16 rows W4 K=12288 N=4096 119 -> 21 / 120 -> 22, W8
-// K=5120 N=5120 40 -> 17 / 40 -> 18; at 20 / 32 rows W4 K=12288 N=4096
-// 119 -> 28 / 120 -> 37, W8 K=12288 N=4096 87 -> 43 / 88 -> 50, W4 K=4096
-// N=12288 44 -> 29 / 44 -> 42, W4 K=5120 N=17408 56 -> 42 / 56 -> 63, W8
-// K=4096 N=12288 34 -> 40 / 35 -> 51, W8 K=5120 N=17408 at 16 rows 42 -> 46.
-// The GEMM gains with the column tiles it can spread over the CUs, the
-// decode kernel loses with every row group re-reading the weights, so the
-// limit falls with the width, and with INT8 (twice the bytes per weight).
-// With row groups of eight (dec8_kernel; `eight`: the call is one it takes)
-// the decode side reads the weights half as often and its limit rises on
-// two widths, measured GEMM -> dec8_kernel (us): W8 K=5120 N=17408 (1088
-// tiles) at 16 rows 41.4 -> 35.4 (at 24 rows 42.7 -> 46.9), W4 K=5120
-// N=17408 at 32 rows 53.5 -> 46.7; and stays where it was on W8 K=5120
-// N=151936 (16 rows: 180 -> 244), W8 K=4096 N=12288 (24 rows: 32.9 ->
-// 45.8) and W4 K=5120 N=27648 (32 rows: 54.5 -> 69.2).  From 2048 W8 tiles
-// the GEMM takes 9 rows and more (argmax calls): W8 K=5120 N=151936 at 9 /
-// 12 rows 193.8 / 188.8 us against 245.2 / 247.1, K=4096 N=151936 159.0 /
-// 159.7 against 253.9 / 253.4 (four-row groups), K=5120 N=65536 99.7 /
-// 100.6 against 111.1 / 111.3.  W4 past 1536 tiles stops at 16 rows on
-// the eight-row groups: K=5120 N=151936 at 16 / 24 rows 191.6 / 293.0 us
-// against the GEMM's 277.0 / 285.3, N=65536 90.7 / 128.3 against 97.5 /
-// 101.5.
-// BREEZE_HIP_DEC_ROWS sets it (1..kDecMaxRows) for tests and tuning.
+// ------------------------------------------------------------------ routing
+//
+// plan_call decides, from the handle's shape and the call alone, which kernel
+// serves a call and how it is launched; run() launches what the plan says
+// (i4_plan_query exposes the plan to tests).  Every threshold below is a
+// measured crossover on MI355X, in one table, with the measurement behind it
+// (us per call, before -> after the choice made):
+//
+//   kFusedMaxBlocks (512 row-blocks: rows x 32-blocks of K)  the decode
+//     prologue quantizes the activation itself up to here; past it the
+//     stand-alone quantizer stages records.  768 row-blocks (C3 at 2 rows)
+//     fused: 9.87 -> 9.75 us with the 4-lane quantizer, inside the spread,
+//     and 10.5 -> 11.3-11.7 with the 8-lane one.
+//   kNormFusedMaxBlocks (384)  the same with the RMSNorm in the prologue:
+//     q/k/v at K = 5120, 3 rows (480 row-blocks): 16.6 fused against 15.4
+//     for the norm kernel then the projections; 2 rows even.
+//   dec_max_rows  most rows the decode kernels take before the prefill GEMM
+//     does, falling with the width (the GEMM spreads more column tiles over
+//     the CUs, every decode row group re-reads the weights; INT8 moves twice
+//     the bytes per weight).  GEMM -> decode at 12 / 16 rows: W4 K=12288
+//     N=4096 119 -> 21 / 120 -> 22, W8 K=5120 N=5120 40 -> 17 / 40 -> 18; at
+//     20 / 32 rows: W4 K=12288 N=4096 119 -> 28 / 120 -> 37, W8 K=12288
+//     N=4096 87 -> 43 / 88 -> 50, W4 K=4096 N=12288 44 -> 29 / 44 -> 42, W4
+//     K=5120 N=17408 56 -> 42 / 56 -> 63, W8 K=4096 N=12288 34 -> 40 / 35 ->
+//     51; W8 K=5120 N=17408 at 16 rows 42 -> 46.  With the eight-row groups
+//     (which read the weights half as often) the limit rises on two widths:
+//     W8 K=5120 N=17408 (1088 tiles) at 16 rows 41.4 -> 35.4 (24 rows: 42.7
+//     -> 46.9), W4 K=5120 N=17408 at 32 rows 53.5 -> 46.7; it stays on W8
+//     K=5120 N=151936 (16 rows: 180 -> 244), W8 K=4096 N=12288 (24 rows:
+//     32.9 -> 45.8), W4 K=5120 N=27648 (32 rows: 54.5 -> 69.2).  From 2048
+//     W8 tiles the GEMM takes 9 rows and more: K=5120 N=151936 at 9 / 12
+//     rows 193.8 / 188.8 against 245.2 / 247.1, K=4096 N=151936 159.0 /
+//     159.7 against 253.9 / 253.4, K=5120 N=65536 99.7 / 100.6 against
+//     111.1 / 111.3.  W4 past 1536 tiles stops at 16 rows on the eight-row
+//     groups: K=5120 N=151936 at 16 / 24 rows 191.6 / 293.0 against the
+//     GEMM's 277.0 / 285.3, N=65536 90.7 / 128.3 against 97.5 / 101.5.
+//   kPairMaxRows4 (16)  paired and multi-projection calls on the four-row
+//     groups (kDec8MaxRows, 32, on the eight-row groups).
+//   dec8_prologue_call  where the four-row groups quantize in their own
+//     prologue (K <= 4096 at 4 rows), the eight-row groups' stand-alone
+//     quantizer costs a launch; they take such calls from 24 rows, from 12
+//     rows with K >= 3072, and from 8 rows with K >= 4096 over 768 tiles or
+//     more (four-row -> eight-row): W8 K=3072 N=8192 at 12 / 24 rows 15.3 /
+//     25.1 -> 12.3 / 16.9, W4 K=4096 N=12288 at 16 / 32 rows 20.6 / 36.2 ->
+//     17.4 / 27.6, W4 K=2048 N=8192 at 12 / 24 rows 9.05 / 14.3 -> 11.3 /
+//     13.0; at 8 rows W8 K=N=4096 9.4 -> 12.1 (kept on the four-row groups),
+//     W8 K=4096 N=12288 18.5 -> 14.7, W4 13.2 -> 13.1.  Elsewhere (staged
+//     records) the eight-row groups take 5-32 rows: W4 K=12288 N=4096 at 8 /
+//     16 / 32 rows 13.6 / 21.1 / 34.0 -> 13.1 / 18.6 / 29.2, W8 K=12288
+//     N=4096 at 24 rows 49.3 -> 34.3, W4 K=17408 N=5120 at 16 rows 54.0 ->
+//     30.6, at 9 / 12 rows W4 K=17408 N=5120 40.1 / 44.9 -> 26.9 / 27.1, W8
+//     K=5120 N=5120 16.4 / 16.4 -> 12.5 / 12.7 (W4 K=5120 N=5120 13.3 / 13.5
+//     -> 13.9 / 13.3, the one loss seen).
+//   kDec8LrecTiles (2)  the eight-row groups copy their records into LDS
+//     when the busiest workgroups have this many tiles: W8 K=5120 N=151936
+//     at 5 / 8 rows 173.7 / 171.9 -> 152.9 / 154.1, W8 K=5120 N=17408 at 8 /
+//     16 rows 25.0 / 34.6 -> 23.3 / 31.2.
+//   kPrefillMinRows (9)  the prefill GEMM takes what the decode kernels do
+//     not, from 9 rows (not with a legacy corr; the rows kernel serves those
+//     and the block-integer export).
+//   pick_pf_rp  32-row prefill workgroups up to 32 rows, 64 up to 64, then
+//     128 (the C4 shape's 512 rows fill the CUs with 128-row workgroups).
+//
+// Environment overrides for tests and tuning: BREEZE_HIP_DEC_ROWS (decode
+// row limit), BREEZE_HIP_DEC8 (0: never the eight-row groups; 2: they take
+// every prologue-quantized call), BREEZE_HIP_DEC8_ROWS (their row limit),
+// BREEZE_HIP_DEC8_LREC (0: records never in LDS; n: from n tiles),
+// BREEZE_HIP_PREFILL_RP / _CT (prefill workgroup shape).
+constexpr int kFusedMaxBlocks = kQuantPasses * 256;
+constexpr int kNormFusedMaxBlocks = 3 * 128;
 constexpr int kDecMaxRows = 32, kDecMaxGroups = 8;
+constexpr int kDec8MaxRows = 32;  // four row groups of eight
+constexpr int kPairMaxRows4 = 16;
+constexpr int kDec8LrecTiles = 2;
+constexpr int kPrefillMinRows = 9;
+
 int dec_max_rows(int bits, int ntiles, bool eight, const char* force) {
     if (force) {
         const int v = std::atoi(force);
@@ -1092,9 +1136,28 @@ int dec_max_rows(int bits, int ntiles, bool eight, const char* force) {
     return ntiles > 768 ? 24 : 32;
 }
 
-int plan_dec_lds(const GemvArgs& a, int Mr_max, int JG, bool p64 = false) {
-    if (Mr_max * a.nblk > kFusedMaxBlocks && Mr_max * a.nblk * 4 > 6 * kDecWaves * 64) return 0;
-    const int total = dec_lds(Mr_max, a.nblk, JG, p64).total;
+// Whether the eight-row groups take a call the four-row groups would quantize
+// in their own prologue (see dec8_prologue_call above).
+bool dec8_prologue_call(int M, int nblk, int ntiles) {
+    const char* d8 = std::getenv("BREEZE_HIP_DEC8");
+    return M >= 24 || (M >= 12 && nblk >= 96) || (M >= 8 && nblk >= 128 && ntiles >= 768) || (d8 && d8[0] == '2');
+}
+
+// What routing reads of a handle.
+struct Shape {
+    int bits, N, nblk, nblk4, nblk_pad;
+    bool extra, has_dl, has_ws;
+};
+Shape shape_of(const Handle* h) {
+    return Shape{h->bits, h->N, h->nblk, h->nblk4, h->nblk_pad, h->extra, h->has_dl, h->WS != nullptr};
+}
+
+// LDS bytes of the decode kernel for Mr_max rows per row group, or 0 if the
+// activation records of a row group do not fit (in LDS, or in the
+// prologue's 6-uint4-per-thread record copy).
+int plan_dec_lds(int nblk, int Mr_max, int JG, bool p64 = false) {
+    if (Mr_max * nblk > kFusedMaxBlocks && Mr_max * nblk * 4 > 6 * kDecWaves * 64) return 0;
+    const int total = dec_lds(Mr_max, nblk, JG, p64).total;
     return total <= kLdsMax ? total : 0;
 }
 
@@ -1115,31 +1178,141 @@ int device_cus(Workspace& w, int dev) {
     return w.n_cu;
 }
 
-// Tiles per workgroup from which dec8_kernel copies its records into LDS
-// (BREEZE_HIP_DEC8_LREC sets it; 0 never).
 int dec8_lrec_min_tiles() {
     if (const char* v = std::getenv("BREEZE_HIP_DEC8_LREC")) {
         const int t = std::atoi(v);
         return t > 0 ? t : std::numeric_limits<int>::max();
     }
-    return 2;
+    return kDec8LrecTiles;
 }
 // Rows of the eight-row groups that take M rows (M rounded up to 8).
 int dec8_rows(int M) { return (M + kRows8 - 1) / kRows8 * kRows8; }
-constexpr int kDec8MaxRows = 32;  // four row groups
-// Whether the decode kernel in row groups of eight takes a call: one
-// without the block-integer export (plain, argmax, gate/up pair or
-// multi-projection; the caller's own limits apply to the last two), with
-// its eight rows' block scales and sums within two uint4 per thread and its
-// LDS plan within the limit.
-bool dec8_takes(const Handle* h, int M, bool dots) {
+// Whether the decode kernel in row groups of eight can take a call: one
+// without the block-integer export, with its eight rows' block scales and
+// sums within two uint4 per thread and its LDS plan within the limit.
+bool dec8_takes(const Shape& h, int M, bool dots) {
     int max_rows = kDec8MaxRows;
     if (const char* r = std::getenv("BREEZE_HIP_DEC8_ROWS")) max_rows = std::min(kDec8MaxRows, std::max(5, std::atoi(r)));
     if (M < 5 || M > max_rows || dots) return false;
     const char* f = std::getenv("BREEZE_HIP_DEC8");
     if (f && f[0] == '0') return false;
-    if ((size_t)kRows8 * h->nblk4 / 4 > 2 * (size_t)kDecWaves * 64) return false;
-    return dec8_lds(h->nblk, h->bits == 8 ? 2 : 4).total <= kLdsMax;
+    if ((size_t)kRows8 * h.nblk4 / 4 > 2 * (size_t)kDecWaves * 64) return false;
+    return dec8_lds(h.nblk, h.bits == 8 ? 2 : 4).total <= kLdsMax;
+}
+
+// The kernel that serves a call.
+enum Route { kRouteNone = 0, kRouteDec = 1, kRouteDec8 = 2, kRoutePrefill = 3, kRouteRows = 4 };
+// The stand-alone quantizer launched ahead of it: none (the decode prologue
+// quantizes), records for the four-row groups or the rows kernel, records in
+// the eight-row groups' operand order, or the prefill GEMM's records.
+enum Quant { kQuantNone = 0, kQuantStaged = 1, kQuantRows8 = 2, kQuantPrefill = 3 };
+
+struct CallKind {
+    bool dots = false;    // block-integer export
+    bool argmax = false;  // per-row argmax
+    bool pair = false;    // gate/up pair in one launch
+    bool multi = false;   // several projections in one launch
+    bool norm = false;    // multi with the RMSNorm in the prologue
+    int tiles = 0;        // column tiles of the launch (all segments of a multi call)
+};
+
+struct Plan {
+    int route = kRouteNone;  // kRouteNone: a paired or multi call no decode launch takes
+    int quant = kQuantNone;
+    bool fused = false;      // the decode prologue quantizes
+    bool p64 = false;        // decode, one or two rows: block pairs on 16x16x64
+    bool lrec = false;       // eight-row groups: records in LDS
+    int rs = 4;              // rows per row group
+    int RG = 1, NG = 1;      // row groups, tile ranges
+    int pair_xcd = 0;        // the row groups of a tile range share an XCD
+    int lds = 0;             // dynamic LDS bytes (decode kernels)
+    int pf_rp = 0, pf_ct = 0, Mpad = 0;  // prefill: row pairs, column tiles, padded rows
+    int grid_x = 0, grid_y = 1;
+};
+
+Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
+    Plan p;
+    const int JG = h.bits == 8 ? 2 : 4;
+    const int ntiles = h.N / 16;
+    const bool fz = k.pair || k.multi;
+    int Mr_max = std::min(M, 4);
+    // One or two rows: block pairs per MFMA when that record layout fits.
+    const int lds_p64 = (M <= 2 && !k.dots) ? plan_dec_lds(h.nblk, Mr_max, JG, true) : 0;
+    p.p64 = lds_p64 > 0;
+    // Past four rows the row groups quantize in their prologue only when
+    // four rows of K fit one prologue's blocks; otherwise the eight-row
+    // groups take the call if they can.
+    const bool eight = 4 * h.nblk > kFusedMaxBlocks && dec8_takes(h, kRows8, k.dots);
+    const int dec_rows = std::min(fz ? (eight ? kDec8MaxRows : kPairMaxRows4) : kDecMaxRows,
+                                  dec_max_rows(h.bits, ntiles, eight, std::getenv("BREEZE_HIP_DEC_ROWS")));
+    int lds = p.p64 ? lds_p64 : (M <= dec_rows && !k.dots) ? plan_dec_lds(h.nblk, Mr_max, JG) : 0;
+    // Rows per row group: 4, or 2 or 1 where four rows of records do not
+    // fit (long K: the staged copy holds 1536 row-blocks, so two rows reach
+    // K = 24576 and one row K = 49152).  Eight row groups at most.
+    int rs = 4;
+    for (int r = 2; r >= 1 && !lds; r >>= 1) {
+        if (r >= Mr_max) continue;  // that plan did not fit
+        if (M > std::min(dec_rows, r * kDecMaxGroups) || k.dots || fz) break;
+        lds = plan_dec_lds(h.nblk, r, JG);
+        if (lds) {
+            rs = r;
+            Mr_max = r;
+        }
+    }
+    const bool dec = lds > 0;
+    if (k.multi && (h.extra || k.argmax)) return p;
+    const bool fused = dec && Mr_max * h.nblk <= kFusedMaxBlocks;
+    const bool dec8 = M <= dec_rows && (!fused || dec8_prologue_call(M, h.nblk, ntiles)) && !k.norm &&
+                      dec8_takes(h, M, k.dots);
+    if (fz && !(dec8 || (dec && M <= kPairMaxRows4))) return p;
+    if (k.norm && !(fused && Mr_max * h.nblk <= kNormFusedMaxBlocks)) return p;
+    const bool pre = !dec && !dec8 && !k.dots && M >= kPrefillMinRows && (h.bits == 4 || h.has_ws) && !h.has_dl;
+    const int tiles = k.tiles > 0 ? k.tiles : ntiles;
+    p.fused = fused;
+    if (pre) {
+        p.route = kRoutePrefill;
+        p.quant = kQuantPrefill;
+        p.pf_rp = pick_pf_rp(M, std::getenv("BREEZE_HIP_PREFILL_RP"));
+        const int rows = 32 * p.pf_rp;
+        p.Mpad = (M + rows - 1) / rows * rows;
+        p.grid_y = p.Mpad / rows;
+        p.pf_ct = pick_pf_ct(tiles, p.grid_y, p.pf_rp, n_cu, std::getenv("BREEZE_HIP_PREFILL_CT"));
+        p.grid_x = (tiles + p.pf_ct - 1) / p.pf_ct;
+    } else if (dec8) {
+        p.route = kRouteDec8;
+        p.quant = kQuantRows8;
+        p.rs = kRows8;
+        p.RG = dec8_rows(M) / kRows8;
+        p.NG = std::min(tiles, std::max(1, n_cu / p.RG));
+        p.pair_xcd = (p.RG > 1 && p.NG % 8 == 0) ? 1 : 0;
+        p.grid_x = p.NG * p.RG;
+        // Records in LDS where the busiest workgroups have several tiles (or
+        // paired tiles) and they fit: read once instead of once per tile.
+        const int tiles_wg = (tiles + p.NG - 1) / p.NG * (k.pair ? 2 : 1);
+        const int lrec_lds = dec8_lds(h.nblk, JG, true).total;
+        p.lrec = tiles_wg >= dec8_lrec_min_tiles() && lrec_lds <= kLdsMax &&
+                 h.nblk_pad * 32 <= kRecCopy * kDecWaves * 64;
+        p.lds = p.lrec ? lrec_lds : dec8_lds(h.nblk, JG).total;
+    } else if (dec) {
+        p.route = kRouteDec;
+        p.quant = fused ? kQuantNone : kQuantStaged;
+        p.rs = rs;
+        p.lds = lds;
+        p.RG = (M + rs - 1) / rs;
+        if (p.RG == 1) {
+            p.NG = std::min(tiles, n_cu);
+        } else {
+            p.NG = std::min(tiles, std::max(1, n_cu / p.RG));
+            p.pair_xcd = p.NG % 8 == 0 ? 1 : 0;
+        }
+        p.grid_x = p.NG * p.RG;
+    } else {
+        p.route = kRouteRows;
+        p.quant = kQuantStaged;
+        p.grid_x = tiles;
+        p.grid_y = (M + kRowsPerWG - 1) / kRowsPerWG;
+    }
+    return p;
 }
 
 // Quantize + block dots + epilogue for M rows on `st`.  Exactly one of
@@ -1201,7 +1374,6 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     }
     const bool hp = g_hi_prec != 0;
     const bool dots = dCs != nullptr;
-    const int JG = h->bits == 8 ? 2 : 4;
 
     GemvArgs a{};
     fill_args(h, a, M);
@@ -1209,94 +1381,32 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     a.C = dC;
     a.Cs = dCs;
 
-    // Decode kernel for M <= dec_rows (row groups: up to 32 rows, fewer for
-    // wide handles, 16 for the paired and multi-projection calls); the
-    // prefill GEMM and the rows kernel serve larger M, the rows kernel the
-    // block-integer export and shapes whose activation records do not fit in
-    // LDS.  The decode kernel quantizes small
-    // activations itself; larger ones go through the stand-alone quantizer
-    // once instead of once per workgroup.
-    int Mr_max = std::min(M, 4);
-    // One or two rows: block pairs per MFMA (P64) when its larger record
-    // layout fits in LDS.
-    const int lds_p64 = (M <= 2 && !dots) ? plan_dec_lds(a, Mr_max, JG, true) : 0;
-    const bool p64 = lds_p64 > 0;
-    // The paired and multi-projection calls take row groups of 4, at most 16
-    // rows.
-    // Past four rows the row groups quantize in their prologue only when
-    // four rows of K fit one prologue's blocks; otherwise dec8_kernel takes
-    // the call if it can.
-    const bool eight = 4 * h->nblk > kFusedMaxBlocks && dec8_takes(h, kRows8, dots);
-    // The paired and multi-projection calls take up to 16 rows on the
-    // four-row groups and up to 32 on the eight-row groups.
-    const int dec_rows = std::min((h2 || mp) ? (eight ? kDec8MaxRows : 16) : kDecMaxRows,
-                                  dec_max_rows(h->bits, a.ntiles, eight, std::getenv("BREEZE_HIP_DEC_ROWS")));
-    int lds = p64 ? lds_p64 : (M <= dec_rows && !dots) ? plan_dec_lds(a, Mr_max, JG) : 0;
-    // Rows per row group: 4, or 2 or 1 where four rows of records do not
-    // fit (long K: the staged copy holds 1536 row-blocks, so two rows reach
-    // K = 24576 and one row K = 49152).  Eight row groups at most.
-    int rs = 4;
-    for (int r = 2; r >= 1 && !lds; r >>= 1) {
-        if (r >= Mr_max) continue;  // that plan did not fit
-        if (M > std::min(dec_rows, r * kDecMaxGroups) || dots || h2 || mp) break;
-        lds = plan_dec_lds(a, r, JG);
-        if (lds) {
-            rs = r;
-            Mr_max = r;
-        }
+    CallKind kind;
+    kind.dots = dots;
+    kind.argmax = dIdx != nullptr;
+    kind.pair = h2 != nullptr;
+    kind.multi = mp != nullptr;
+    kind.norm = mp && mp->norm;
+    kind.tiles = a.ntiles;
+    if (mp) {
+        kind.tiles = 0;
+        for (int k = 0; k < mp->n; ++k) kind.tiles += mp->h[k]->N / 16;
     }
-    const bool dec = lds > 0;
-    if (mp && (h->extra || dIdx)) return kNotPairable;
-    const bool fused = dec && Mr_max * h->nblk <= kFusedMaxBlocks;
-    // 5-32 rows of a plain call, up to the decode kernel's row limit, whose
-    // four-row groups would copy staged records (or whose records do not fit
-    // them): row groups of eight (dec8_kernel), one workgroup per (tile
-    // range, eight rows), when its scale and sum rows fit (two uint4 per
-    // thread).  Both take the stand-alone quantizer; where the four-row
-    // groups quantize in their prologue (K <= 4096) they keep the call,
-    // which saves that launch (~2.5 us): W8 K=4096 N=4096 at 8 rows 9.7 us
-    // against 12.2 us.  Measured against the four-row groups (us): W4
-    // K=12288 N=4096 at 8 / 16 / 32 rows 13.6 / 21.1 / 34.0 -> 13.1 / 18.6 /
-    // 29.2, W8 K=12288 N=4096 at 24 rows 49.3 -> 34.3, W4 K=17408 N=5120 at
-    // 16 rows 54.0 -> 30.6 (at 24 and 32 rows the GEMM took 167 us).  At
-    // 9 / 12 rows (with the records in LDS): W4 K=17408 N=5120 40.1 / 44.9
-    // -> 26.9 / 27.1, W8 K=5120 N=5120 16.4 / 16.4 -> 12.5 / 12.7; W4
-    // K=5120 N=5120 13.3 / 13.5 -> 13.9 / 13.3 is the one loss seen.
-    // BREEZE_HIP_DEC8=0 keeps every call off it, =2 gives it every call the
-    // four-row groups quantize in their prologue (for measurements).
-    // Where the four-row groups quantize in their prologue, the eight-row
-    // groups take the call from 24 rows, and from 12 rows with K >= 3072
-    // (us, four-row -> eight-row): W8 K=3072 N=8192 at 12 / 24 rows 15.3 /
-    // 25.1 -> 12.3 / 16.9, W4 K=4096 N=12288 at 16 / 32 rows 20.6 / 36.2
-    // -> 17.4 / 27.6, W4 K=2048 N=8192 at 12 / 24 rows 9.05 / 14.3 ->
-    // 11.3 / 13.0; at 8 rows W8 K=N=4096 9.4 -> 12.1, but from 8 rows on
-    // wide K=4096 shapes W8 N=12288 18.5 -> 14.7, W4 N=12288 14.2 -> 13.1.
-    // Never a norm call: the norm runs in the four-row groups' prologue only.
-    const char* d8 = std::getenv("BREEZE_HIP_DEC8");
-    const bool dec8_fused = M >= 24 || (M >= 12 && h->nblk >= 96) ||
-                            (M >= 8 && h->nblk >= 128 && a.ntiles >= 768) || (d8 && d8[0] == '2');
-    const bool dec8 = M <= dec_rows && (!fused || dec8_fused) && !(mp && mp->norm) && dec8_takes(h, M, dots);
-    if ((h2 || mp) && !(dec8 || (dec && M <= 16))) return kNotPairable;
-    // The norm in the prologue pays for itself up to 384 row-blocks (q/k/v
-    // at K = 5120: M = 3, 480 row-blocks, 16.6 us against 15.4 us for the
-    // norm kernel then the projections; M = 2, 320 row-blocks: even).
-    if (mp && mp->norm && !(fused && Mr_max * h->nblk <= kNormFusedMaxBlocks)) return kNotPairable;
-    // Prefill GEMM: more than 8 rows without a legacy corr.
-    const bool pre = !dec && !dec8 && !dots && M > 8 && (h->bits == 4 || h->WS) && !h->has_dl;
-    const int pf_rp = pick_pf_rp(M, std::getenv("BREEZE_HIP_PREFILL_RP"));
-    const int pf_rows = 32 * pf_rp;  // rows per prefill workgroup
-    const int Mpad = (M + pf_rows - 1) / pf_rows * pf_rows;
-    const int nch_rec = (h->nblk + 1) / 2;  // record chunks of two blocks
-    if (pre) {
+    const Plan p = plan_call(shape_of(h), M, kind, device_cus(w, dev));
+    if (p.route == kRouteNone) return kNotPairable;
+
+    // The stand-alone quantizer ahead of the matmul kernel.
+    if (p.quant == kQuantPrefill) {
         // Records in MFMA operand order for the prefill GEMM.
-        if (!grow(w, st, &s.rec, &s.rec_cap, (size_t)(Mpad / 16) * nch_rec * kRecBytes, "workspace alloc", s.fixed))
+        const int nch_rec = (h->nblk + 1) / 2;  // record chunks of two blocks
+        if (!grow(w, st, &s.rec, &s.rec_cap, (size_t)(p.Mpad / 16) * nch_rec * kRecBytes, "workspace alloc", s.fixed))
             return -4;
-        const size_t threads = (size_t)(Mpad / 16) * nch_rec * 2 * 64;  // a wave per (16 rows, block)
+        const size_t threads = (size_t)(p.Mpad / 16) * nch_rec * 2 * 64;  // a wave per (16 rows, block)
         const unsigned qb = (unsigned)((threads + 255) / 256);
-        if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);
-        else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, Mpad, s.rec);
+        if (hp) quantize_rec_kernel<true><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, p.Mpad, s.rec);
+        else quantize_rec_kernel<false><<<qb, 256, 0, st>>>(dA, M, h->K, h->nblk, nch_rec, p.Mpad, s.rec);
         if (!hip_ok(hipGetLastError(), "quantize launch")) return -5;
-    } else if (dec8) {
+    } else if (p.quant == kQuantRows8) {
         const int rows8 = dec8_rows(M);
         if (!ensure_quant(w, s, st, rows8, h->nblk4)) return -4;
         const size_t threads = (size_t)rows8 * h->nblk_pad * 4;
@@ -1315,7 +1425,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.Aq = s.aq;
         a.Sa = s.sa;
         a.Sq = s.sq;
-    } else if (!fused) {
+    } else if (p.quant == kQuantStaged) {
         if (!ensure_quant(w, s, st, M, h->nblk4)) return -4;
         const size_t threads = (size_t)M * h->nblk * 4;
         const unsigned qb = (unsigned)((threads + 255) / 256);
@@ -1361,9 +1471,10 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.D2 = h2->D;
     }
     const int fz = pair ? kFusePair : mp ? (mp->norm ? kFuseNormMulti : kFuseMulti) : kFusePlain;
+    const bool decode = p.route == kRouteDec || p.route == kRouteDec8;
     // The decode kernels' in-kernel argmax merges into per-stream state
     // (a ticket, then kDecMaxRows row keys), zero between calls.
-    if ((dec8 || dec) && dIdx) {
+    if (decode && dIdx) {
         if (!s.ticket && s.fixed) {
             set_err("internal: fixed scratch without argmax state");
             return -5;
@@ -1391,84 +1502,63 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.key = reinterpret_cast<unsigned long long*>(s.ticket) + 1;
         a.idx = dIdx;
     }
-    if (dec8) {
-        const int n_cu = device_cus(w, dev);
-        a.RS = kRows8;
-        a.RG = dec8_rows(M) / kRows8;
-        a.NG = std::min(a.ntiles, std::max(1, n_cu / a.RG));
-        a.pair_xcd = (a.RG > 1 && a.NG % 8 == 0) ? 1 : 0;
-        const int grid = a.NG * a.RG;
-        // Records in LDS where the busiest workgroups have several tiles (or
-        // paired tiles) and they fit: read once instead of once per tile.
-        const int tiles_wg = (a.ntiles + a.NG - 1) / a.NG * (pair ? 2 : 1);
-        const int lrec_lds = dec8_lds(h->nblk, JG, true).total;
-        const bool lrec = tiles_wg >= dec8_lrec_min_tiles() && lrec_lds <= kLdsMax &&
-                          h->nblk_pad * 32 <= kRecCopy * kDecWaves * 64;
-        const int lds8 = lrec ? lrec_lds : dec8_lds(h->nblk, JG).total;
+    if (decode) {
+        a.RS = p.rs;
+        a.RG = p.RG;
+        a.NG = p.NG;
+        a.pair_xcd = p.pair_xcd;
+    }
+    const bool x = h->extra;
+    if (p.route == kRouteDec8) {
         const uint4* rec = reinterpret_cast<const uint4*>(s.aq);
         bool* at = &w.dec8_attr[12 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
-        const bool x = h->extra;
-        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, grid, lds8, fz, x, lrec, st)
-                                 : launch_dec8<8, false>(at, a, rec, grid, lds8, fz, x, lrec, st);
-        else e = hp ? launch_dec8<4, true>(at, a, rec, grid, lds8, fz, x, lrec, st)
-                    : launch_dec8<4, false>(at, a, rec, grid, lds8, fz, x, lrec, st);
-    } else if (dec) {
-        const int n_cu = device_cus(w, dev);
-        a.RS = rs;
-        a.RG = (M + rs - 1) / rs;
-        if (a.RG == 1) {
-            a.NG = std::min(a.ntiles, n_cu);
-            a.pair_xcd = 0;
-        } else {
-            const int ng = std::min(a.ntiles, std::max(1, n_cu / a.RG));
-            a.pair_xcd = ng % 8 == 0 ? 1 : 0;
-            a.NG = ng;
-        }
-        const int grid = a.NG * a.RG;
-        const bool x = h->extra;
-        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)
-                                 : launch_dec_bits<8, false>(w.attr_set, a, grid, lds, fz, p64, fused, x, st);
-        else e = hp ? launch_dec_bits<4, true>(w.attr_set, a, grid, lds, fz, p64, fused, x, st)
-                    : launch_dec_bits<4, false>(w.attr_set, a, grid, lds, fz, p64, fused, x, st);
-    } else if (pre) {
-        PfArgs p{};
-        p.W = reinterpret_cast<const char*>(h->W);
-        p.WS = reinterpret_cast<const char*>(h->WS);
-        p.S = reinterpret_cast<const char*>(h->S);
-        p.Z = reinterpret_cast<const char*>(h->Z);
-        p.R = reinterpret_cast<const char*>(s.rec);
-        p.C = dC;
-        p.M = M;
-        p.N = h->N;
-        p.nblk = h->nblk;
-        p.nch = nch_rec;
-        p.ngrp = h->ngrp;
-        p.sc_shift = h->sc_shift;
-        p.ntiles = h->N / 16;
-        p.nbg = h->nbg;
+        if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, p.grid_x, p.lds, fz, x, p.lrec, st)
+                                 : launch_dec8<8, false>(at, a, rec, p.grid_x, p.lds, fz, x, p.lrec, st);
+        else e = hp ? launch_dec8<4, true>(at, a, rec, p.grid_x, p.lds, fz, x, p.lrec, st)
+                    : launch_dec8<4, false>(at, a, rec, p.grid_x, p.lds, fz, x, p.lrec, st);
+    } else if (p.route == kRouteDec) {
+        const bool fu = p.fused, p64 = p.p64;
+        if (h->bits == 8) e = hp ? launch_dec_bits<8, true>(w.attr_set, a, p.grid_x, p.lds, fz, p64, fu, x, st)
+                                 : launch_dec_bits<8, false>(w.attr_set, a, p.grid_x, p.lds, fz, p64, fu, x, st);
+        else e = hp ? launch_dec_bits<4, true>(w.attr_set, a, p.grid_x, p.lds, fz, p64, fu, x, st)
+                    : launch_dec_bits<4, false>(w.attr_set, a, p.grid_x, p.lds, fz, p64, fu, x, st);
+    } else if (p.route == kRoutePrefill) {
+        PfArgs pa{};
+        pa.W = reinterpret_cast<const char*>(h->W);
+        pa.WS = reinterpret_cast<const char*>(h->WS);
+        pa.S = reinterpret_cast<const char*>(h->S);
+        pa.Z = reinterpret_cast<const char*>(h->Z);
+        pa.R = reinterpret_cast<const char*>(s.rec);
+        pa.C = dC;
+        pa.M = M;
+        pa.N = h->N;
+        pa.nblk = h->nblk;
+        pa.nch = (h->nblk + 1) / 2;
+        pa.ngrp = h->ngrp;
+        pa.sc_shift = h->sc_shift;
+        pa.ntiles = h->N / 16;
+        pa.nbg = h->nbg;
         const int scm = h->sc_blk ? 2 : (h->sc_shift == 31 ? 0 : 1);
         if (h->bits == 4 && scm == 2 && !h->Z) {
             set_err("internal: INT4 handle with per-block scales has no zero points");
             return -5;
         }
-        const int gy = Mpad / pf_rows;
-        const int ct = pick_pf_ct(p.ntiles, gy, pf_rp, device_cus(w, dev), std::getenv("BREEZE_HIP_PREFILL_CT"));
-        const dim3 grid((unsigned)((p.ntiles + ct - 1) / ct), (unsigned)gy);
+        const dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
         if (h->bits == 8)
-            e = hp ? launch_pf<8, true>(w.pf_attr, p, scm, pf_rp, ct, grid, st)
-                   : launch_pf<8, false>(w.pf_attr, p, scm, pf_rp, ct, grid, st);
+            e = hp ? launch_pf<8, true>(w.pf_attr, pa, scm, p.pf_rp, p.pf_ct, grid, st)
+                   : launch_pf<8, false>(w.pf_attr, pa, scm, p.pf_rp, p.pf_ct, grid, st);
         else
-            e = hp ? launch_pf<4, true>(w.pf_attr, p, scm, pf_rp, ct, grid, st)
-                   : launch_pf<4, false>(w.pf_attr, p, scm, pf_rp, ct, grid, st);
+            e = hp ? launch_pf<4, true>(w.pf_attr, pa, scm, p.pf_rp, p.pf_ct, grid, st)
+                   : launch_pf<4, false>(w.pf_attr, pa, scm, p.pf_rp, p.pf_ct, grid, st);
     } else {
-        const dim3 grid(a.ntiles, (M + kRowsPerWG - 1) / kRowsPerWG);
+        const dim3 grid((unsigned)p.grid_x, (unsigned)p.grid_y);
         if (h->bits == 8) e = hp ? launch_rows_bits<8, true>(a, grid, dots, st)
                                  : launch_rows_bits<8, false>(a, grid, dots, st);
         else e = hp ? launch_rows_bits<4, true>(a, grid, dots, st) : launch_rows_bits<4, false>(a, grid, dots, st);
     }
     if (!hip_ok(e, "matmul launch")) return -5;
 
-    if (dIdx && !dots && !dec && !dec8) {
+    if (dIdx && !dots && !decode) {
         // Both decode kernels merge their own argmax (last workgroup).
         const int nparts = (h->N + kArgmaxChunk - 1) / kArgmaxChunk;
         if (!grow(w, st, &s.parts, &s.parts_cap, (size_t)M * nparts, "argmax workspace", s.fixed)) return -4;
@@ -1932,6 +2022,37 @@ void i4_matmul(void* handle, const float* A, int M, float* C) {
 
 void i4_matmul_region(void* handle, const float* A, int M, float* C, uint8_t*, float*) {
     i4_matmul(handle, A, M, C);
+}
+
+int i4_plan_query(int bits, int M, int K, int N, int flags, int n_cu, int32_t* out, int nout) {
+    if (!out || nout < 1 || M < 1 || n_cu < 1) {
+        set_err("plan query: needs out, nout >= 1, M >= 1 and n_cu >= 1");
+        return -1;
+    }
+    if (!check_dims(N, K, bits)) return -1;
+    const int JG = bits == 8 ? 2 : 4;
+    Shape h{};
+    h.bits = bits;
+    h.N = N;
+    h.nblk = K / 32;
+    h.nblk4 = (h.nblk + 3) / 4 * 4;
+    h.nblk_pad = (h.nblk + JG - 1) / JG * JG;
+    h.extra = (flags & 32) != 0 || (flags & 64) != 0;
+    h.has_dl = (flags & 64) != 0;
+    h.has_ws = bits == 8;  // every INT8 handle carries its weight sums
+    CallKind k;
+    k.dots = (flags & 1) != 0;
+    k.argmax = (flags & 2) != 0;
+    k.pair = (flags & 4) != 0;
+    k.multi = (flags & 8) != 0;
+    k.norm = (flags & 16) != 0;
+    k.tiles = N / 16;
+    const Plan p = plan_call(h, M, k, n_cu);
+    const int32_t v[] = {p.route, p.quant, p.fused, p.p64, p.lrec, p.rs, p.RG, p.NG, p.pair_xcd, p.lds,
+                         p.pf_rp, p.pf_ct, p.grid_x, p.grid_y};
+    const int n = std::min(nout, (int)(sizeof(v) / sizeof(v[0])));
+    for (int i = 0; i < n; ++i) out[i] = v[i];
+    return n;
 }
 
 int i4_handle_info(void* handle, int64_t* out) {
