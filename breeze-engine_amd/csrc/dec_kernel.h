@@ -73,25 +73,27 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // contiguous too: a block index is an offset, with no row/column split.
     const int nb_rows = Mr * a.nblk;
     // Lane q = tid & 3 of a quad holds k = 8q..8q+7 of its block: two uint4
-    // per pass, in named registers (arrays indexed under the passes' early
-    // exits were placed in scratch).
-    static_assert(kQuantPasses == 2, "the prologue spells out two passes");
-    Oct av0, av1;
-    Oct wn0, wn1;  // NORM: the norm weights of those elements
+    // per pass, every pass's loads in flight before the first is quantized.
+    // The array is indexed only by constants after unrolling, so it stays in
+    // registers.
+    Oct av[kQuantPasses];
+    Oct wn0, wn1;  // NORM (at most two passes): the norm weights of those elements
     uint4 r0, r1, r2, r3, r4, r5, rsa, rsq;  // named: an indexed array would live in scratch
     if (FUSED) {
         if (nb_rows > kQuantEarlyBlocks || wave < 8) {
             const float* arow = a.A + (size_t)m0 * a.K + 8 * (tid & 3);
             const bool all = nb_rows > kQuantEarlyBlocks;
             const int qb = all ? 256 : 128;  // blocks per pass
-            const bool two = all && nb_rows > 256;
+            const int npass = all ? (nb_rows + 255) >> 8 : 1;
+            const bool two = npass > 1;
             auto ld = [&](int p, Oct& v) {
                 const int blk = min(p * qb + (tid >> 2), nb_rows - 1);
                 v.x = *reinterpret_cast<const uint4*>(arow + 32 * blk);
                 v.y = *reinterpret_cast<const uint4*>(arow + 32 * blk + 4);
             };
-            ld(0, av0);
-            if (two) ld(1, av1);
+#pragma unroll
+            for (int p = 0; p < kQuantPasses; ++p)
+                if (p < npass) ld(p, av[p]);
             if (NORM) {
                 auto ldw = [&](int p, Oct& v) {
                     const int blk = min(p * qb + (tid >> 2), nb_rows - 1);
@@ -237,7 +239,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         if (FUSED) {
             const bool all = nb_rows > kQuantEarlyBlocks;
             const int qb = all ? 256 : 128;  // blocks per pass
-            const int npass = all ? (nb_rows + 255) >> 8 : wave < 8 ? 1 : 0;  // 0, 1 or 2
+            const int npass = all ? (nb_rows + 255) >> 8 : wave < 8 ? 1 : 0;  // 0 to kQuantPasses
             // NORM: the decoder's RMSNorm of each row first, hn = (x * inv) * w
             // with inv = 1 / sqrtf((float)(ss / K) + eps)
             // (kernel/qwen35_decoder.cpp:134-140), bit for bit.  The block
@@ -268,8 +270,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     t += dpp_f64(t, 0x4E);  // lane ^ 2
                     if ((tid & 3) == 0 && blk < nb_rows) nsq[blk] = t;
                 };
-                if (npass > 0) sumsq(0, av0);
-                if (npass > 1) sumsq(1, av1);
+                if (npass > 0) sumsq(0, av[0]);
+                if (npass > 1) sumsq(1, av[1]);
                 lds_barrier();
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -335,8 +337,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                     }
                 }
             };
-            if (npass > 0) qpass(0, av0, wn0);
-            if (npass > 1) qpass(1, av1, wn1);
+#pragma unroll
+            for (int p = 0; p < kQuantPasses; ++p)
+                if (p < npass) qpass(p, av[p], p == 0 ? wn0 : wn1);
         } else {
             // Rows land at the padded LDS pitches.
             const int nrec = nb_rows * 4, nmeta = Mr * a.nblk4 / 4;

@@ -1058,11 +1058,17 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 // measured crossover on MI355X, in one table, with the measurement behind it
 // (us per call, before -> after the choice made):
 //
-//   kFusedMaxBlocks (512 row-blocks: rows x 32-blocks of K)  the decode
-//     prologue quantizes the activation itself up to here; past it the
-//     stand-alone quantizer stages records.  768 row-blocks (C3 at 2 rows)
-//     fused: 9.87 -> 9.75 us with the 4-lane quantizer, inside the spread,
-//     and 10.5 -> 11.3-11.7 with the 8-lane one.
+//   kFusedMaxBlocks2 (768 row-blocks: rows x 32-blocks of K; one or two
+//   rows) and kFusedMaxBlocks (512; more rows)  the decode prologue
+//   quantizes the activation itself up to here (passes of 256 row-blocks
+//   over the sixteen waves); past it the stand-alone quantizer stages
+//   records.  Staged -> fused: W4 K=12288 N=4096 at 2 rows (768) 9.75 ->
+//     9.07, W4 K=17408 at 1 row (544) N=64 9.14 -> 8.43, N=5120 15.79 ->
+//     14.80; W4 K=5120 N=17408 at 4 rows (640) 15.09 -> 15.13; past them,
+//     W4 K=17408 N=64 at 2 rows (1088) 10.38 -> 10.76, W4 K=12288 N=4096 at
+//     3 / 4 / 8 rows (1152 / 1536 / 2 x 1536) 10.39 / 10.40 / 12.96 ->
+//     11.11 / 12.27 / 16.56: each pass of 256 row-blocks costs ~0.55 us on
+//     every CU.
 //   kNormFusedMaxBlocks (384)  the same with the RMSNorm in the prologue:
 //     q/k/v at K = 5120, 3 rows (480 row-blocks): 16.6 fused against 15.4
 //     for the norm kernel then the projections; 2 rows even.
@@ -1117,14 +1123,26 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 // row limit), BREEZE_HIP_DEC8 (0: never the eight-row groups; 2: they take
 // every prologue-quantized call), BREEZE_HIP_DEC8_ROWS (their row limit),
 // BREEZE_HIP_DEC8_LREC (0: records never in LDS; n: from n tiles),
-// BREEZE_HIP_PREFILL_RP / _CT (prefill workgroup shape).
-constexpr int kFusedMaxBlocks = kQuantPasses * 256;
+// BREEZE_HIP_PREFILL_RP / _CT (prefill workgroup shape), BREEZE_HIP_FUSED_MAX_BLOCKS
+// (row-blocks the decode prologue quantizes).
+constexpr int kFusedMaxBlocks = 512, kFusedMaxBlocks2 = 768;
+constexpr int kFusedCapBlocks = kQuantPasses * 256;  // what the prologue can quantize
 constexpr int kNormFusedMaxBlocks = 3 * 128;
 constexpr int kDecMaxRows = 32, kDecMaxGroups = 8;
 constexpr int kDec8MaxRows = 32;  // four row groups of eight
 constexpr int kPairMaxRows4 = 16;
 constexpr int kDec8LrecTiles = 2;
 constexpr int kPrefillMinRows = 9;
+
+// Row-blocks the decode prologue quantizes itself for calls of M rows
+// (BREEZE_HIP_FUSED_MAX_BLOCKS sets it for every M, up to kFusedCapBlocks).
+int fused_max_blocks(int M) {
+    if (const char* v = std::getenv("BREEZE_HIP_FUSED_MAX_BLOCKS")) {
+        const int b = std::atoi(v);
+        if (b >= 0) return std::min(b, kFusedCapBlocks);
+    }
+    return M <= 2 ? kFusedMaxBlocks2 : kFusedMaxBlocks;
+}
 
 int dec_max_rows(int bits, int ntiles, bool eight, const char* force) {
     if (force) {
@@ -1156,7 +1174,7 @@ Shape shape_of(const Handle* h) {
 // activation records of a row group do not fit (in LDS, or in the
 // prologue's 6-uint4-per-thread record copy).
 int plan_dec_lds(int nblk, int Mr_max, int JG, bool p64 = false) {
-    if (Mr_max * nblk > kFusedMaxBlocks && Mr_max * nblk * 4 > 6 * kDecWaves * 64) return 0;
+    if (Mr_max * nblk > kFusedCapBlocks && Mr_max * nblk * 4 > 6 * kDecWaves * 64) return 0;
     const int total = dec_lds(Mr_max, nblk, JG, p64).total;
     return total <= kLdsMax ? total : 0;
 }
@@ -1242,7 +1260,8 @@ Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
     // Past four rows the row groups quantize in their prologue only when
     // four rows of K fit one prologue's blocks; otherwise the eight-row
     // groups take the call if they can.
-    const bool eight = 4 * h.nblk > kFusedMaxBlocks && dec8_takes(h, kRows8, k.dots);
+    const int fused_max = fused_max_blocks(M);
+    const bool eight = 4 * h.nblk > fused_max_blocks(4) && dec8_takes(h, kRows8, k.dots);
     const int dec_rows = std::min(fz ? (eight ? kDec8MaxRows : kPairMaxRows4) : kDecMaxRows,
                                   dec_max_rows(h.bits, ntiles, eight, std::getenv("BREEZE_HIP_DEC_ROWS")));
     int lds = p.p64 ? lds_p64 : (M <= dec_rows && !k.dots) ? plan_dec_lds(h.nblk, Mr_max, JG) : 0;
@@ -1261,7 +1280,7 @@ Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
     }
     const bool dec = lds > 0;
     if (k.multi && (h.extra || k.argmax)) return p;
-    const bool fused = dec && Mr_max * h.nblk <= kFusedMaxBlocks;
+    const bool fused = dec && Mr_max * h.nblk <= fused_max;
     const bool dec8 = M <= dec_rows && (!fused || dec8_prologue_call(M, h.nblk, ntiles)) && !k.norm &&
                       dec8_takes(h, M, k.dots);
     if (fz && !(dec8 || (dec && M <= kPairMaxRows4))) return p;

@@ -90,25 +90,47 @@ __device__ inline void quant4x8(float4 v0, float4 v1, float& s_out, uint2& ph, u
     am = max(am, dpp_xor2(am));
     amax = __int_as_float(am);
     constexpr int qmax = HP ? 32767 : 127;
-    const float s = amax / (float)qmax;
-    const float inv = s > 0.0f ? 1.0f / s : 0.0f;
-    uint32_t w0[2] = {0u, 0u}, w1[2] = {0u, 0u};
-    int sum = 0;
+    // s = amax / qmax, correctly rounded: the product with fl(1 / qmax) and
+    // one FMA correction, which equals the IEEE quotient for every finite
+    // amax >= +0 (checked exhaustively against division for both qmax;
+    // the subnormals included).  amax = inf keeps the quotient inf.
+    constexpr float kInvQ = 1.0f / (float)qmax;
+    const float q0 = amax * kInvQ;
+    const float s = __builtin_isinf(amax) ? amax : __builtin_fmaf(__builtin_fmaf(-q0, (float)qmax, amax), kInvQ, q0);
+    float inv = s > 0.0f ? 1.0f / s : 0.0f;
+    // The reference gives q = 0 for a non-finite product (its lrint).  An
+    // infinite inv (a block scale too small for its reciprocal) makes every
+    // product of the block infinite or NaN, so inv = 0 gives the same
+    // zeros.  With inv finite, the only non-finite products are NaN (a NaN
+    // element, or an infinite one times inv = 1 / inf = 0), and
+    // v_cvt_i32_f32 converts NaN to 0.  The reference's clamp to +-qmax
+    // never binds when inv is finite: |x| <= amax, and rint(amax * inv) <=
+    // qmax for every finite amax (checked exhaustively for both qmax).
+    if (__builtin_isinf(inv)) inv = 0.0f;
+    int q[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float prod = x[i] * inv;
-        int q = 0;
-        if (__builtin_isfinite(prod)) {
-            q = (int)rintf(prod);
-            q = q > qmax ? qmax : (q < -qmax ? -qmax : q);
-        }
-        sum += q;
+        // Hardware conversion (NaN -> 0), which C's conversion does not promise.
+        asm("v_cvt_i32_f32 %0, %1" : "=v"(q[i]) : "v"(__builtin_rintf(x[i] * inv)));
+    }
+    int sum = (q[0] + q[1] + q[2]) + (q[3] + q[4] + q[5]) + (q[6] + q[7]);
+    // Bytes by v_perm_b32 (selector byte k picks byte k of the second
+    // operand for 0-3, of the first for 4-7).  q as 16-bit two's complement
+    // is u - 32768 for u = q + 32768, so its high byte is the reference's
+    // (u >> 8) - 128 and its low byte (u & 255) - 128 after flipping bit 7.
+    uint32_t w0[2], w1[2] = {0u, 0u};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t* qq = reinterpret_cast<const uint32_t*>(q + 4 * h);
         if (HP) {
-            const uint32_t u = (uint32_t)(q + 32768);
-            w0[i >> 2] |= (((u >> 8) ^ 0x80u) & 0xFFu) << (8 * (i & 3));
-            w1[i >> 2] |= (((u & 0xFFu) ^ 0x80u) & 0xFFu) << (8 * (i & 3));
+            const uint32_t p01 = __builtin_amdgcn_perm(qq[1], qq[0], 0x05040100u);  // q1.lo16 : q0.lo16
+            const uint32_t p23 = __builtin_amdgcn_perm(qq[3], qq[2], 0x05040100u);
+            w0[h] = __builtin_amdgcn_perm(p23, p01, 0x07050301u);                 // high bytes
+            w1[h] = __builtin_amdgcn_perm(p23, p01, 0x06040200u) ^ 0x80808080u;   // low bytes
         } else {
-            w0[i >> 2] |= ((uint32_t)q & 0xFFu) << (8 * (i & 3));
+            const uint32_t p01 = __builtin_amdgcn_perm(qq[1], qq[0], 0x05040400u);  // q1.b0 : q0.b0 in bytes 0-1
+            const uint32_t p23 = __builtin_amdgcn_perm(qq[3], qq[2], 0x05040400u);
+            w0[h] = __builtin_amdgcn_perm(p23, p01, 0x05040100u);
         }
     }
     s_out = s;
@@ -190,7 +212,7 @@ constexpr int kProducers = kDecWaves - 1;
 // waves of a workgroup start up to ~0.3 us after the first, and the prologue
 // barrier waits for the slowest quantizer.  More blocks take all sixteen
 // waves (at most kQuantPasses passes of 256).
-constexpr int kQuantEarlyBlocks = 128, kQuantPasses = 2;
+constexpr int kQuantEarlyBlocks = 128, kQuantPasses = 6;
 
 struct GemvArgs {
     const uint4* W;

@@ -613,3 +613,32 @@ def test_decode_one_row_groups_longer_k(gpu, hb, orc, hi_prec, monkeypatch, bits
                 assert idx.cpu().numpy().tolist() == np.argmax(want, axis=1).tolist(), (hp, rows)
     finally:
         hb.free(h)
+
+
+# The decode prologue quantizes up to 768 row-blocks of one or two rows
+# itself (three passes of 256 over its sixteen waves) and up to 512 of more
+# rows; BREEZE_HIP_FUSED_MAX_BLOCKS raises the limit to the prologue's six
+# passes (1536 row-blocks), which the routing does not use by default, so the
+# longer prologues are checked here too.  Row counts and K cover every pass
+# count from one to six, partial last passes and padded last chunks.
+@pytest.mark.parametrize("bits,explicit_zeros", [(4, False), (4, True), (8, False)])
+@pytest.mark.parametrize("M,K,limit", [(1, 17408, None), (1, 24576, None), (2, 12288, None), (2, 8224, None),
+                                       (3, 12288, 1536), (4, 12288, 1536), (4, 10272, 1536), (1, 49120, 1536)])
+def test_decode_prologue_passes(gpu, hb, orc, hi_prec, monkeypatch, bits, explicit_zeros, M, K, limit):
+    torch = gpu
+    if limit:
+        monkeypatch.setenv("BREEZE_HIP_FUSED_MAX_BLOCKS", str(limit))
+    N = 64
+    assert hb.plan(bits, M, K, N, extra=explicit_zeros)["quant"] is None  # the prologue quantizes
+    rng = np.random.default_rng(M * 7 + K + bits)
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        for hp in (True, False):
+            hb.set_hi_prec(hp)
+            A = (rng.normal(size=(M, K)) * rng.choice([1e-3, 1.0, 50.0], size=(M, 1))).astype(np.float32)
+            A[0, 5] = np.float32(0.0)
+            got = hb.matmul(h, torch.from_numpy(A).cuda(), N).cpu().numpy()
+            assert bits_equal(got, orc.matmul(qw, sc, qz, N, K, bits, A, hp)), (M, K, hp)
+    finally:
+        hb.free(h)

@@ -18,7 +18,8 @@ TABLE = [
     ("C1 W8 GEMV", (8, 1, 4096, 4096, {}), dict(route="decode", quant=None, p64=1, tile_ranges=256, grid_x=256)),
     ("C2 W4 GEMV", (4, 1, 4096, 12288, {}), dict(route="decode", quant=None, p64=1, tile_ranges=256)),
     ("C3 1 row", (4, 1, 12288, 4096, {}), dict(route="decode", quant=None, p64=1)),
-    ("C3 2 rows", (4, 2, 12288, 4096, {}), dict(route="decode", quant="staged", p64=1, row_groups=1)),
+    ("C3 2 rows", (4, 2, 12288, 4096, {}), dict(route="decode", quant=None, p64=1, row_groups=1)),
+    ("C3 3 rows", (4, 3, 12288, 4096, {}), dict(route="decode", quant="staged", p64=0, row_groups=1)),
     ("C3 4 rows", (4, 4, 12288, 4096, {}), dict(route="decode", quant="staged", p64=0, rows_per_group=4,
                                                  row_groups=1)),
     ("C3 8 rows", (4, 8, 12288, 4096, {}), dict(route="decode8", quant="rows8", row_groups=1, lrec=0)),
@@ -48,7 +49,10 @@ TABLE = [
     ("W4 K=17408 3 rows", (4, 3, 17408, 5120, {}), dict(route="decode", quant="staged", rows_per_group=2,
                                                         row_groups=2)),
     # Tall-skinny: few column tiles over a long K.
-    ("W4 K=17408 N=64", (4, 1, 17408, 64, {}), dict(route="decode", quant="staged", tile_ranges=4, grid_x=4)),
+    ("W4 K=17408 N=64", (4, 1, 17408, 64, {}), dict(route="decode", quant=None, tile_ranges=4, grid_x=4)),
+    ("W4 K=17408 N=64 2 rows", (4, 2, 17408, 64, {}), dict(route="decode", quant="staged")),
+    ("W4 K=24576 1 row", (4, 1, 24576, 4096, {}), dict(route="decode", quant=None)),
+    ("W4 K=25600 1 row", (4, 1, 25600, 4096, {}), dict(route="decode", quant="staged")),
     # The export of block integers, and a legacy corr past the decode rows.
     ("block dots", (4, 4, 1024, 256, dict(dots=True)), dict(route="rows", quant="staged", grid_x=16, grid_y=1)),
     ("legacy corr 40 rows", (8, 40, 1024, 256, dict(legacy_corr=True)), dict(route="rows", grid_y=5)),
