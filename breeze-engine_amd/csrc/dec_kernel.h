@@ -286,7 +286,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                          __builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 48)));
                     float mean;
                     if (a.norm_exact || !(v - v == 0.0) || !norm_mean_from_bound(v, a.K, 0, &mean))
-                        mean = (float)(norm_sumsq_inorder(a.A + (size_t)(m0 + r) * a.K, a.K) / (double)a.K);
+                        mean = (float)(norm_sumsq_inorder<8>(a.A + (size_t)(m0 + r) * a.K, a.K) / (double)a.K);
                     inv_r[r] = 1.0f / sqrtf(mean + a.norm_eps);
                 }
             }

@@ -674,7 +674,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* __re
             }
         } else if (tid < 64) {
             // Too many specials for the walk: wave 0 sums in element order.
-            const double acc = norm_sumsq_inorder(x, H);
+            const double acc = norm_sumsq_inorder<64>(x, H);
             if (tid == 0) ss_s = acc;
         }
     }

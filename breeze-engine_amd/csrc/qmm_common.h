@@ -398,6 +398,12 @@ __device__ inline double sum16_f64(double v) {
 
 // The reference's in-order double sum of squares of x[0..H), by one wave
 // (every lane returns it): the slow way, for rows the bound does not decide.
+// UNROLL: lane reads unrolled per 64-element step.  Fully unrolled (64) the
+// stand-alone norm kernel's fallback takes 42 us a row of 5120, unrolled by
+// 8 it takes 110 us; but fully unrolled inside the decode kernel the 128
+// lane reads were hoisted into scalar registers and spilled (239 SGPRs),
+// so the decode kernel's prologue, where this is a rare path, unrolls by 8.
+template <int UNROLL>
 __device__ inline double norm_sumsq_inorder(const float* x, int H) {
     // Every lane of the wave holds the same running sum; the wave squares 64
     // elements at a time (exactly, in double) and each term enters the sum
@@ -408,7 +414,7 @@ __device__ inline double norm_sumsq_inorder(const float* x, int H) {
     for (; c + 64 <= H; c += 64) {
         const float v = x[c + lane];
         const long long tb = __builtin_bit_cast(long long, (double)v * (double)v);
-#pragma unroll
+#pragma unroll UNROLL
         for (int l = 0; l < 64; ++l) ss += __builtin_bit_cast(double, readlane64(tb, l));
     }
     if (c < H) {
