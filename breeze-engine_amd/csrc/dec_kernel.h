@@ -17,6 +17,16 @@ namespace bq {
 // share an XCD).  PAIR: gate and up projections
 // in one launch; each output tile is the gate tile then the up tile of the
 // same columns, and C = silu(gate) * up.
+//
+// SPLIT (split-K, one row group): workgroup b takes piece b % S of tile
+// b / S, where S = prem_t and the S pieces are balanced ranges of the
+// tile's phases.  It quantizes only its piece's blocks, stores each block's
+// value f = (float)cs * scale and the activation scales to the tile's
+// region of sf instead of folding them, and takes a ticket.  The last of
+// the tile's S workgroups folds every block in order, acc = fma(sa, f,
+// acc) as in the unsplit fold (quantized_matmul.cpp:311-315), so the
+// output is the same bits, and re-arms the ticket.  No workgroup waits for
+// another.
 
 template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64>
 __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, const uint4* pW, const float* pS,
@@ -40,6 +50,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     a.pair_xcd = (misc >> 12) & 1;
     constexpr bool PAIR = FUSE == kFusePair, NORM = FUSE == kFuseNormMulti;
     constexpr bool MULTI = FUSE == kFuseMulti || NORM;
+    constexpr bool SPLIT = FUSE == kFuseSplit;
+    static_assert(!SPLIT || FUSED, "split-K quantizes its pieces in the prologue");
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int PP = dec_pitch(JG);
     typedef float fvec __attribute__((ext_vector_type(JG)));
@@ -48,8 +60,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    int g, rg;
-    if (a.RG == 1) {
+    const int npw = misc >> 16;  // phases per tile: ceil(nbg / 15)
+    const int nsplit = SPLIT ? prem_t : 1;
+    int g, rg, piece = 0;
+    if (SPLIT) {
+        g = blockIdx.x / nsplit;
+        piece = blockIdx.x - g * nsplit;
+        rg = 0;
+    } else if (a.RG == 1) {
         g = blockIdx.x;
         rg = 0;
     } else if (a.pair_xcd) {
@@ -64,6 +82,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     }
     const int m0 = rg * a.RS;
     const int Mr = min(a.RS, a.M - m0);
+    // Phases [pa, pb) of each tile; with SPLIT the piece's blocks
+    // [qb0, qb0 + nbr) of each row are the ones quantized, and LDS holds
+    // them (records, scales, sums) from the piece's first block and chunk
+    // coff on.
+    const int pa = SPLIT ? piece * npw / nsplit : 0, pb = SPLIT ? (piece + 1) * npw / nsplit : npw;
+    const int qb0 = SPLIT ? pa * kProducers * JG : 0;
+    const int coff = SPLIT ? pa * kProducers : 0;
+    const int nbr = SPLIT ? min(pb * kProducers * JG, pnblk) - qb0 : pnblk;
 
     // Activation loads, ahead of all other set-up in program order: at kernel
     // start the prologue's instructions are fetched cold, and timestamps put
@@ -71,7 +97,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // K is a multiple of 32, so the rows m0.. of A are nb_rows contiguous
     // 32-float blocks, and the staged scale and sum rows (pitch nblk4) are
     // contiguous too: a block index is an offset, with no row/column split.
-    const int nb_rows = Mr * a.nblk;
+    const int nb_rows = Mr * nbr;
     // Lane q = tid & 3 of a quad holds k = 8q..8q+7 of its block: two uint4
     // per pass, every pass's loads in flight before the first is quantized.
     // The array is indexed only by constants after unrolling, so it stays in
@@ -87,7 +113,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             const int npass = all ? (nb_rows + 255) >> 8 : 1;
             const bool two = npass > 1;
             auto ld = [&](int p, Oct& v) {
-                const int blk = min(p * qb + (tid >> 2), nb_rows - 1);
+                int blk = min(p * qb + (tid >> 2), nb_rows - 1);
+                if (SPLIT) {
+                    // Row m's piece starts at block qb0 of that row.
+                    const int m = (blk >= nbr) + (blk >= 2 * nbr) + (blk >= 3 * nbr);
+                    blk += qb0 + m * (pnblk - nbr);
+                }
                 v.x = *reinterpret_cast<const uint4*>(arow + 32 * blk);
                 v.y = *reinterpret_cast<const uint4*>(arow + 32 * blk + 4);
             };
@@ -128,14 +159,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    const int base_t = pbase_t, rem_t = prem_t;
+    const int base_t = pbase_t, rem_t = SPLIT ? 0 : prem_t;
     const int t_begin = g * base_t + min(g, rem_t);
     const int nT = base_t + (g < rem_t ? 1 : 0);
     const int nbg = a.nbg;
-    const int npw = misc >> 16;                // phases per tile: ceil(nbg / 15)
-    const int U = nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
+    const int U = SPLIT ? pb - pa : nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
 
-    const DecLds lay = dec_lds(min(a.M, a.RS), a.nblk, JG, P64);
+    const DecLds lay = dec_lds(min(a.M, a.RS), SPLIT ? split_piece_blocks(npw, nsplit, a.nbg, JG) : a.nblk, JG, P64);
     uint8_t* recs = smem + lay.recs;
     float* sa_l = reinterpret_cast<float*>(smem + lay.sa);
     int* sq_l = reinterpret_cast<int*>(smem + lay.sq);
@@ -143,6 +173,34 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
 
     const int col = lane & 15, grp = lane >> 4;
     const int me = min(grp, Mr - 1);
+
+    // SPLIT: the folding workgroup copies its tile's region of sf to LDS
+    // (pitch split_pitch) with device-scope loads, which see every piece's
+    // device-scope stores; sixteen in flight per thread (128 KB a round).
+    auto split_stage = [&]() {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(a.sf + (size_t)g * a.M * 17 * a.nblk4);
+        const int q2 = a.nblk4 >> 1, n2 = a.M * 17 * q2, P = split_pitch(a.nblk4);
+        float* st = reinterpret_cast<float*>(smem);
+        constexpr int kIn = 16;
+        for (int i0 = 0; i0 < n2; i0 += kIn * kDecWaves * 64) {
+            uint64_t v[kIn];  // indexed by constants only: registers
+            // Groups wholly past the region are skipped (a uniform branch);
+            // the last group's extra threads re-read its last element.
+#pragma unroll
+            for (int k = 0; k < kIn; ++k)
+                if (i0 + k * kDecWaves * 64 < n2)
+                    v[k] = __hip_atomic_load(src + min(i0 + k * kDecWaves * 64 + tid, n2 - 1), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int k = 0; k < kIn; ++k) {
+                const int i = i0 + k * kDecWaves * 64 + tid;
+                if (i < n2) {
+                    const int r = i / q2, q = i - r * q2;
+                    *reinterpret_cast<uint64_t*>(st + r * P + 2 * q) = v[k];
+                }
+            }
+        }
+    };
 
     // Load cursor, kept incrementally: one scalar unit serves the CU's
     // sixteen waves, which reach their scalar work together after each
@@ -164,7 +222,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // With several projections (MULTI) the weights and scales of segment
     // ld_k are at lw and ls; the cursor moves to the next segment's arrays
     // when a tile crosses into it, and the idle loads never leave a tile.
-    int ld_c = wave, ld_rem = npw, ld_t = 0, ld_sel = 0;  // ld_sel: up tile of a pair
+    int ld_c = wave + kProducers * pa, ld_rem = pb - pa, ld_t = 0, ld_sel = 0;  // ld_sel: up tile of a pair
     int ld_k = 0, t_off = 0;  // MULTI: segment of the next tile, and its first tile
     if (MULTI) {
         ld_k = (t_begin >= args.seg_end[0]) + (t_begin >= args.seg_end[1]) + (t_begin >= args.seg_end[2]);
@@ -316,7 +374,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 }
                 quant4x8<HP>(x0, x1, s, ph, pl, sum);
                 if (blk < nb_rows) {
-                    const int m = (blk >= a.nblk) + (blk >= 2 * a.nblk) + (blk >= 3 * a.nblk), j = blk - m * a.nblk;
+                    const int m = (blk >= nbr) + (blk >= 2 * nbr) + (blk >= 3 * nbr), j = blk - m * nbr;
                     if (P64) {
                         // Lane e holds k-octet e: its slot is the zero
                         // half, then the octet.
@@ -392,7 +450,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 // closing zero slot.
                 if (tid < 128) cst[tid] = (tid == 2 || tid == 3) ? 0x40404040u : 0u;
                 if (tid < 4 * Mr) {
-                    uint32_t* z = reinterpret_cast<uint32_t*>(recs + (tid >> 2) * lay.rec_pitch + a.nblk * 128);
+                    uint32_t* z = reinterpret_cast<uint32_t*>(recs + (tid >> 2) * lay.rec_pitch + nbr * 128);
                     z[tid & 3] = 0u;
                 }
             } else if (tid < 128) {
@@ -413,12 +471,32 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         const bool tail_pad = a.nblk != nbg * JG;  // the last chunk has padding blocks
         float acc = 0.0f, gate = 0.0f;
         unsigned long long best = 0;
-        int pr_t = 0, pr_p = 0, pr_sel = 0, pr_k = 0;
+        int pr_t = 0, pr_p = pa, pr_sel = 0, pr_k = 0;
         for (int u = 0; u < U; ++u) {
             lds_barrier();
             const float* fp = fbuf + ((u & 1) * 64 + lane) * PP;
             const int c0 = kProducers * pr_p;
-            const float* sp = sa_row + c0 * JG;
+            const float* sp = sa_row + (c0 - coff) * JG;
+            if constexpr (SPLIT) {
+                // The phase's block values (whole chunks: padding blocks of
+                // a last chunk land inside the row's nblk4 and are never
+                // folded), and the block scales from the column-0 lanes,
+                // written through to device scope.
+                if (grp < Mr) {
+                    float* fo = a.sf + ((size_t)g * a.M + grp) * 17 * a.nblk4 + c0 * JG;
+                    const int nch = min(kProducers, nbg - c0);
+#pragma unroll
+                    for (int i = 0; i < kProducers; ++i)
+                        if (i < nch) store_agent<JG>(fo + col * a.nblk4 + i * JG, fp + i * JG);
+                    if (col == 0) {
+#pragma unroll
+                        for (int i = 0; i < kProducers; ++i)
+                            if (i < nch) store_agent<JG>(fo + 16 * a.nblk4 + i * JG, sp + i * JG);
+                    }
+                }
+                ++pr_p;
+                continue;
+            }
             if (c0 + kProducers < nbg || (c0 + kProducers == nbg && !tail_pad)) {
                 // Full phase: every block is real.  All fifteen chunks'
                 // reads, then the FMAs: right after the barrier the reads
@@ -491,6 +569,92 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 pr_p = 0;
             }
         }
+        if constexpr (SPLIT) {
+            // The device-scope stores above complete before the ticket is
+            // taken (the fence keeps the compiler from moving them past the
+            // wait).  The holder of the last ticket folds the tile, reading
+            // every piece's stores with device-scope loads.  No cache-wide
+            // write-back or invalidation is needed: only these stores and
+            // loads cross workgroups.
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            __builtin_amdgcn_s_waitcnt(0);
+            unsigned int tk = 0;
+            if (lane == 0) tk = atomicAdd(a.stick + g, 1u);
+            tk = __shfl(tk, 0);
+            const bool last = tk == (unsigned int)(nsplit - 1);
+            int* flag = reinterpret_cast<int*>(smem + split_flag_off(a.M, a.nblk4, lay.total));
+            if (lane == 0) *flag = last ? 1 : 0;
+            lds_barrier();
+            if (!last) return;
+            split_stage();
+            lds_barrier();
+            if (grp < Mr) {
+                // One dependent FMA per block; in whole batches of 16 the
+                // next batch's reads are issued before the current batch's
+                // FMAs (a read past the batches is clamped into the row:
+                // its values are not used), then the rest block by block.
+                const int P = split_pitch(a.nblk4);
+                const float* st = reinterpret_cast<const float*>(smem);
+                const float* fr = st + (grp * 17 + col) * P;
+                const float* sr = st + (grp * 17 + 16) * P;
+                float v = 0.0f;
+                const int nfull = a.nblk & ~15;
+                int b = 0;
+                if (nfull > 0) {
+                    float4 f0, f1, f2, f3, s0, s1, s2, s3;
+                    auto rd = [&](int o, float4& x0, float4& x1, float4& x2, float4& x3, float4& y0, float4& y1,
+                                  float4& y2, float4& y3) {
+                        x0 = *reinterpret_cast<const float4*>(fr + o);
+                        x1 = *reinterpret_cast<const float4*>(fr + o + 4);
+                        x2 = *reinterpret_cast<const float4*>(fr + o + 8);
+                        x3 = *reinterpret_cast<const float4*>(fr + o + 12);
+                        y0 = *reinterpret_cast<const float4*>(sr + o);
+                        y1 = *reinterpret_cast<const float4*>(sr + o + 4);
+                        y2 = *reinterpret_cast<const float4*>(sr + o + 8);
+                        y3 = *reinterpret_cast<const float4*>(sr + o + 12);
+                    };
+                    auto fma4 = [&](const float4& x, const float4& y) {
+                        v = __builtin_fmaf(y.x, x.x, v);
+                        v = __builtin_fmaf(y.y, x.y, v);
+                        v = __builtin_fmaf(y.z, x.z, v);
+                        v = __builtin_fmaf(y.w, x.w, v);
+                    };
+                    float4 g0, g1, g2, g3, t0, t1, t2, t3;
+                    rd(0, f0, f1, f2, f3, s0, s1, s2, s3);
+                    // Two batches an iteration: each half reads the batch
+                    // after next while the FMAs consume the one read before.
+                    for (; b + 32 <= nfull; b += 32) {
+                        rd(b + 16, g0, g1, g2, g3, t0, t1, t2, t3);
+                        fma4(f0, s0);
+                        fma4(f1, s1);
+                        fma4(f2, s2);
+                        fma4(f3, s3);
+                        rd(min(b + 32, P - 16), f0, f1, f2, f3, s0, s1, s2, s3);
+                        fma4(g0, t0);
+                        fma4(g1, t1);
+                        fma4(g2, t2);
+                        fma4(g3, t3);
+                        // Keep each half's reads ahead of its FMAs (the
+                        // scheduler would move them next to their uses).
+                        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 16, 0);
+                    }
+                    if (b < nfull) {  // one batch left, already read
+                        fma4(f0, s0);
+                        fma4(f1, s1);
+                        fma4(f2, s2);
+                        fma4(f3, s3);
+                        b += 16;
+                    }
+                }
+                for (; b < a.nblk; ++b) v = __builtin_fmaf(sr[b], fr[b], v);
+                a.C[(size_t)grp * a.N + g * 16 + col] = v;
+            }
+            if (lane == 0) (void)atomicExch(a.stick + g, 0u);
+            return;
+        }
         if (!PAIR && !MULTI && a.idx) {
             // Row maximum over the lanes of each row (lanes 16r..16r+15).
 #pragma unroll
@@ -559,10 +723,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     auto consume = [&](const Unit<JG, EXTRA>& cur, int buf) {
         const int c = cur.c;
         if (P64 && c < nbg) {
-            const int abase = p_data ? p_data_base + c * JG * 128 : p_const_base;
+            const int abase = p_data ? p_data_base + (c - coff) * JG * 128 : p_const_base;
             int2 nsq2 = make_int2(0, 0);  // this lane's block in each pair
             if (BITS == 4) {
-                const int* q = sq_l + o_row * lay.sa_pitch + c * 4 + o_sel;
+                const int* q = sq_l + o_row * lay.sa_pitch + (c - coff) * 4 + o_sel;
                 nsq2 = make_int2(q[0], q[2]);
             }
             float fo[JG / 2];
@@ -601,13 +765,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
 #pragma unroll
             for (int mi = 0; mi < JG / 2; ++mi) p_fout[buf * 64 * PP + 2 * mi] = fo[mi];
         } else if (!P64 && c < nbg) {
-            const int abase = is_data ? data_base + c * JG * 64 : const_base;
+            const int abase = is_data ? data_base + (c - coff) * JG * 64 : const_base;
             // The chunk's JG A operands of this lane: 8 JG contiguous bytes.
             uint4 av4[JG / 2];
 #pragma unroll
             for (int h = 0; h < JG / 2; ++h) av4[h] = *reinterpret_cast<const uint4*>(smem + abase + 16 * h);
             int4 sqv = make_int4(0, 0, 0, 0);
-            if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * lay.sa_pitch + c * 4);
+            if (BITS == 4) sqv = *reinterpret_cast<const int4*>(sq_l + me * lay.sa_pitch + (c - coff) * 4);
             fvec fo;
 #pragma unroll
             for (int jb = 0; jb < JG; ++jb) {
@@ -639,6 +803,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             if (live) lds_barrier();
         }
     }
+    if constexpr (SPLIT) {
+        // The chain wave's ticket says whether this workgroup folds.
+        lds_barrier();
+        if (!*reinterpret_cast<const int*>(smem + split_flag_off(a.M, a.nblk4, lay.total))) return;
+        split_stage();
+        lds_barrier();
+    }
 }
 
 template <int BITS, bool HP, bool FUSED, bool EXTRA, int R, int FUSE, bool P64>
@@ -655,7 +826,7 @@ hipError_t launch_dec_t(bool* attr_set, const GemvArgs& a, int grid, int lds, hi
     const void* act = FUSED ? static_cast<const void*>(a.A) : static_cast<const void*>(a.Aq);
     const int npw = (a.nbg + kProducers - 1) / kProducers;
     const int misc = a.sc_shift | (a.RS == 1 ? 2 : a.RS == 2 ? 1 : 0) << 5 | a.RG << 8 | a.pair_xcd << 12 | npw << 16;
-    const int base_t = a.ntiles / a.NG, rem_t = a.ntiles - base_t * a.NG;
+    const int base_t = a.ntiles / a.NG, rem_t = FUSE == kFuseSplit ? a.split : a.ntiles - base_t * a.NG;
     kern<<<grid, kDecWaves * 64, lds, st>>>(act, a.W, a.S, base_t, a.nblk, a.M, a.nbg, rem_t, a.NG, a.ngrp, misc, a);
     return hipGetLastError();
 }
@@ -664,6 +835,10 @@ template <int BITS, bool HP, bool FUSED, bool EXTRA, bool P64>
 hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, hipStream_t st) {
     if (fuse == kFusePair)
         return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePair, P64>(attr_set, a, grid, lds, st);
+    if (fuse == kFuseSplit) {
+        if constexpr (FUSED) return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseSplit, P64>(attr_set, a, grid, lds, st);
+        return hipErrorInvalidValue;  // split pieces quantize in the prologue
+    }
     if constexpr (!EXTRA) {
         if (fuse == kFuseMulti)
             return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseMulti, P64>(attr_set, a, grid, lds, st);

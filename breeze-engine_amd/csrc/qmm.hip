@@ -764,6 +764,10 @@ struct Scratch {
     size_t gate_cap = 0;
     float* hn = nullptr;  // normalized rows when the norm runs as its own launch
     size_t hn_cap = 0;
+    unsigned int* stick = nullptr;  // split-K: per-tile tickets, zero between calls
+    size_t stick_cap = 0;
+    float* sf = nullptr;  // split-K: per-tile block values and scales
+    size_t sf_cap = 0;
     // Set for i4_matmul_noalloc_dev: the buffers above are carved from the
     // device's static scratch array and can never grow.
     bool fixed = false;
@@ -778,7 +782,7 @@ struct Workspace {
     size_t hA_cap = 0, hC_cap = 0;
     hipStream_t stream = nullptr;
     int n_cu = 0;
-    bool attr_set[256] = {};  // decode kernel variants with the kernel attribute set
+    bool attr_set[512] = {};  // decode kernel variants with the kernel attribute set
     bool dec8_attr[48] = {};  // the same for dec8_kernel, per (bits, mode) and (FUSE mode, metadata, LDS records)
     bool pf_attr[256] = {};
 };
@@ -1118,13 +1122,25 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 //     and the block-integer export).
 //   pick_pf_rp  32-row prefill workgroups up to 32 rows, 64 up to 64, then
 //     128 (the C4 shape's 512 rows fill the CUs with 128-row workgroups).
+//   kSplitMaxTiles (8), kSplitMinPhases (20)  split-K takes plain decode
+//     calls of at most 8 column tiles whose tiles have 20 phases or more
+//     (15 chunks a phase: W8 K >= 17440, W4 K >= 34880).  The unsplit
+//     kernel spends ~0.45 (W8) / ~0.68 (W4) us a phase on one CU; the split
+//     launch spends ~3 us handing the pieces' block values across CUs
+//     (device-scope stores, a ticket, device-scope loads) and folds nblk
+//     blocks on one wave.  64 columns, one row, unsplit -> split: W8 K=12288
+//     / 17408 / 24576 / 32768 7.65 / 10.12 / 12.96 / 17.10 -> 8.91 / 10.17 /
+//     11.98 / 13.92; W4 K=24576 / 32768 10.26 / 14.20 -> 12.76 / 13.97; two
+//     rows: W8 K=17408 11.94 -> 11.48, W4 K=17408 10.51 -> 12.71; W4
+//     K=32768 N=256 (16 tiles, 256 pieces) 14.46 -> 16.33; W4 K=4096 N=1024
+//     3.81 -> 8.41.
 //
 // Environment overrides for tests and tuning: BREEZE_HIP_DEC_ROWS (decode
 // row limit), BREEZE_HIP_DEC8 (0: never the eight-row groups; 2: they take
 // every prologue-quantized call), BREEZE_HIP_DEC8_ROWS (their row limit),
 // BREEZE_HIP_DEC8_LREC (0: records never in LDS; n: from n tiles),
 // BREEZE_HIP_PREFILL_RP / _CT (prefill workgroup shape), BREEZE_HIP_FUSED_MAX_BLOCKS
-// (row-blocks the decode prologue quantizes).
+// (row-blocks the decode prologue quantizes), BREEZE_HIP_SPLIT (split-K).
 constexpr int kFusedMaxBlocks = 512, kFusedMaxBlocks2 = 768;
 constexpr int kFusedCapBlocks = kQuantPasses * 256;  // what the prologue can quantize
 constexpr int kNormFusedMaxBlocks = 3 * 128;
@@ -1133,6 +1149,7 @@ constexpr int kDec8MaxRows = 32;  // four row groups of eight
 constexpr int kPairMaxRows4 = 16;
 constexpr int kDec8LrecTiles = 2;
 constexpr int kPrefillMinRows = 9;
+constexpr int kSplitMaxTiles = 8, kSplitMinPhases = 20;
 
 // Row-blocks the decode prologue quantizes itself for calls of M rows
 // (BREEZE_HIP_FUSED_MAX_BLOCKS sets it for every M, up to kFusedCapBlocks).
@@ -1246,12 +1263,58 @@ struct Plan {
     int lds = 0;             // dynamic LDS bytes (decode kernels)
     int pf_rp = 0, pf_ct = 0, Mpad = 0;  // prefill: row pairs, column tiles, padded rows
     int grid_x = 0, grid_y = 1;
+    int split = 0;           // decode split-K: workgroups per tile (0: none)
 };
+
+// Split-K for a plain decode call of at most four rows (one row group): the
+// workgroups per tile (S pieces of the tile's phases), or 0.  S fills the
+// CUs, at most one phase a piece.  A piece's LDS holds only its own blocks,
+// so any K fits whose rows of a piece fit one prologue and whose fold
+// staging fits the LDS; *lds receives the launch's LDS bytes.  Taken by
+// default for tall-skinny calls: at most kSplitMaxTiles tiles and at least
+// kSplitMinPhases phases a tile (see the routing table).  BREEZE_HIP_SPLIT:
+// 0 never, 1 wherever it fits, n >= 2 forces n pieces (at most one per
+// phase).
+int split_pieces(const Shape& h, int M, const CallKind& k, int n_cu, int* lds) {
+    if (M > 4 || k.dots || k.argmax || k.pair || k.multi || k.norm) return 0;
+    const int JG = h.bits == 8 ? 2 : 4;
+    const int ntiles = h.N / 16;
+    const int nbg = (h.nblk + JG - 1) / JG;
+    const int npw = (nbg + kProducers - 1) / kProducers;
+    if (npw < 2) return 0;
+    int S = std::min(npw, n_cu / ntiles);
+    const char* env = std::getenv("BREEZE_HIP_SPLIT");
+    const int force = env ? std::atoi(env) : -1;
+    if (force == 0) return 0;
+    if (force >= 2) S = std::min(force, npw);
+    else if (force != 1 && (ntiles > kSplitMaxTiles || npw < kSplitMinPhases)) return 0;
+    if (S < 2) return 0;
+    const int lblk = split_piece_blocks(npw, S, nbg, JG);
+    if (M * std::min(lblk, h.nblk) > kFusedCapBlocks) return 0;
+    const int total = dec_lds(M, lblk, JG, M <= 2).total;
+    const int need = split_flag_off(M, h.nblk4, total) + 16;
+    if (need > kLdsMax) return 0;
+    *lds = need;
+    return S;
+}
 
 Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
     Plan p;
     const int JG = h.bits == 8 ? 2 : 4;
     const int ntiles = h.N / 16;
+    int split_lds = 0;
+    if (const int S = split_pieces(h, M, k, n_cu, &split_lds)) {
+        // Split-K: one row group, the prologue quantizes each piece.
+        p.route = kRouteDec;
+        p.fused = true;
+        p.p64 = M <= 2;
+        p.rs = 4;
+        p.NG = ntiles;
+        p.grid_x = ntiles * S;
+        p.lds = split_lds;
+        p.split = S;
+        return p;
+    }
     const bool fz = k.pair || k.multi;
     int Mr_max = std::min(M, 4);
     // One or two rows: block pairs per MFMA when that record layout fits.
@@ -1489,8 +1552,42 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.Z2 = h2->Z;
         a.D2 = h2->D;
     }
-    const int fz = pair ? kFusePair : mp ? (mp->norm ? kFuseNormMulti : kFuseMulti) : kFusePlain;
+    const int fz = p.split ? kFuseSplit : pair ? kFusePair : mp ? (mp->norm ? kFuseNormMulti : kFuseMulti) : kFusePlain;
     const bool decode = p.route == kRouteDec || p.route == kRouteDec8;
+    if (p.split) {
+        // Split-K scratch: a ticket per tile (zero between calls; the
+        // folding workgroup re-arms it) and each tile's block values.
+        const size_t nt = (size_t)a.ntiles, nf = nt * M * 17 * h->nblk4;
+        if (s.fixed) {
+            // Carved from the call's record region (a split call stages no
+            // records); the region holds other data between calls, so a
+            // kernel clears the tickets every time.
+            const size_t tb = (nt * sizeof(unsigned int) + 255) / 256 * 256;
+            if (tb + nf * sizeof(float) > s.rec_cap) {
+                set_err("no-allocation scratch: split-K over %zu tiles needs %zu bytes, more than %zu", nt,
+                        tb + nf * sizeof(float), s.rec_cap);
+                return -4;
+            }
+            a.stick = reinterpret_cast<unsigned int*>(s.rec);
+            a.sf = reinterpret_cast<float*>(s.rec + tb);
+            fill_u32_kernel<<<(unsigned)((nt + 63) / 64), 64, 0, st>>>(a.stick, (int)nt, 0u);
+            if (!hip_ok(hipGetLastError(), "split ticket clear")) return -5;
+        } else {
+            const unsigned int* before = s.stick;
+            if (!grow(w, st, &s.stick, &s.stick_cap, nt, "split-K workspace") ||
+                !grow(w, st, &s.sf, &s.sf_cap, nf, "split-K workspace"))
+                return -4;
+            if (s.stick != before) {
+                // Zeroed once per allocation, on st (a non-blocking stream
+                // does not wait for the null stream).
+                fill_u32_kernel<<<(unsigned)((s.stick_cap + 63) / 64), 64, 0, st>>>(s.stick, (int)s.stick_cap, 0u);
+                if (!hip_ok(hipGetLastError(), "split ticket clear")) return -5;
+            }
+            a.stick = s.stick;
+            a.sf = s.sf;
+        }
+        a.split = p.split;
+    }
     // The decode kernels' in-kernel argmax merges into per-stream state
     // (a ticket, then kDecMaxRows row keys), zero between calls.
     if (decode && dIdx) {
@@ -2068,7 +2165,7 @@ int i4_plan_query(int bits, int M, int K, int N, int flags, int n_cu, int32_t* o
     k.tiles = N / 16;
     const Plan p = plan_call(h, M, k, n_cu);
     const int32_t v[] = {p.route, p.quant, p.fused, p.p64, p.lrec, p.rs, p.RG, p.NG, p.pair_xcd, p.lds,
-                         p.pf_rp, p.pf_ct, p.grid_x, p.grid_y};
+                         p.pf_rp, p.pf_ct, p.grid_x, p.grid_y, p.split};
     const int n = std::min(nout, (int)(sizeof(v) / sizeof(v[0])));
     for (int i = 0; i < n; ++i) out[i] = v[i];
     return n;

@@ -253,13 +253,22 @@ struct GemvArgs {
     float* normOut;
     float norm_eps;
     int norm_exact;  // always take the in-order sum (tests)
+    // Split-K (kFuseSplit): split workgroups per tile; sf receives each
+    // tile's per-block values and activation scales ([tile][M][17][nblk4]
+    // floats: columns 0..15, then the scales), stick counts the workgroups
+    // of each tile that are done (0 between calls).
+    float* sf;
+    unsigned int* stick;
+    int split;
 };
 constexpr int kMaxSeg = 4;
 
 // Decode kernel modes: one weight set, the gate/up pair with the SiLU
-// epilogue, several projections of one activation, and the same with the
-// decoder's RMSNorm applied to the activation in the prologue.
-constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3;
+// epilogue, several projections of one activation, the same with the
+// decoder's RMSNorm applied to the activation in the prologue, and one
+// weight set split along K (each workgroup takes a range of one tile's
+// phases; the last to finish folds the tile).
+constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3, kFuseSplit = 4;
 
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
 // (explicit zero points, legacy corr, scale groups smaller than a chunk)
@@ -476,6 +485,38 @@ __host__ __device__ inline DecLds dec_lds(int Mr_max, int nblk, int JG, bool p64
     l.fbuf = lds_take(off, 2 * 64 * dec_pitch(JG) * 4);
     l.total = off;
     return l;
+}
+
+// Split-K block values cross workgroups (and XCDs, whose L2 caches are not
+// coherent for ordinary stores) as device-scope atomic stores of JG floats,
+// two at a time: written through to the device's coherence point.
+template <int JG>
+__device__ inline void store_agent(float* dst, const float* src_lds) {
+#pragma unroll
+    for (int h = 0; h < JG / 2; ++h) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src_lds + 2 * h);
+        __hip_atomic_store(reinterpret_cast<uint64_t*>(dst) + h, (uint64_t)v.y << 32 | v.x, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Blocks of LDS records (and scales) a split-K workgroup holds: its piece's
+// chunks, at most ceil(npw / S) phases of 15 and at most the tile's nbg,
+// indexed from the piece's first block.
+__host__ __device__ inline int split_piece_blocks(int npw, int S, int nbg, int JG) {
+    const int ch = (npw + S - 1) / S * kProducers;
+    return (ch < nbg ? ch : nbg) * JG;
+}
+
+// Split-K fold staging: the tile's [M][17][nblk4] floats copied to LDS at
+// offset 0 (over the records and phase buffers, dead by then) with a row
+// pitch of nblk4 + 4 floats, so the 16 columns' rows start 16 B apart in the
+// banks; a flag word follows the larger of that and the kernel's layout.
+__host__ __device__ inline int split_pitch(int nblk4) { return nblk4 + 4; }
+__host__ __device__ inline int split_flag_off(int M, int nblk4, int layout_total) {
+    const int stage = M * 17 * split_pitch(nblk4) * 4;
+    const int end = stage > layout_total ? stage : layout_total;
+    return (end + 15) / 16 * 16;
 }
 
 // Ring depth R (weight units in flight per wave).  Two units per producer

@@ -49,7 +49,22 @@ TABLE = [
     ("W4 K=17408 3 rows", (4, 3, 17408, 5120, {}), dict(route="decode", quant="staged", rows_per_group=2,
                                                         row_groups=2)),
     # Tall-skinny: few column tiles over a long K.
-    ("W4 K=17408 N=64", (4, 1, 17408, 64, {}), dict(route="decode", quant=None, tile_ranges=4, grid_x=4)),
+    ("W4 K=17408 N=64", (4, 1, 17408, 64, {}), dict(route="decode", quant=None, tile_ranges=4, grid_x=4,
+                                                     split=0)),
+    # Split-K: at most 8 tiles with at least 20 phases (15 chunks) a tile,
+    # S workgroups a tile filling the CUs, at most one phase each.
+    ("split W8 K=24576 N=64", (8, 1, 24576, 64, {}), dict(route="decode", quant=None, split=26, grid_x=104,
+                                                           tile_ranges=4, row_groups=1)),
+    ("split W8 K=32768 N=128 2 rows", (8, 2, 32768, 128, {}), dict(route="decode", quant=None, p64=1, split=32,
+                                                                   grid_x=256)),
+    ("split W4 K=40960 N=64", (4, 1, 40960, 64, {}), dict(route="decode", quant=None, split=22, grid_x=88)),
+    ("split W8 K=18432 N=16 4 rows", (8, 4, 18432, 16, {}), dict(route="decode", quant=None, p64=0, split=20,
+                                                                 rows_per_group=4, row_groups=1)),
+    ("no split: 19 phases", (8, 1, 17408, 64, {}), dict(split=0, grid_x=4)),
+    ("no split: 9 tiles", (8, 1, 32768, 144, {}), dict(split=0)),
+    ("no split: fold staging past LDS", (8, 4, 20480, 16, {}), dict(split=0)),
+    ("no split: argmax", (8, 1, 32768, 64, dict(argmax=True)), dict(split=0)),
+    ("no split: 5 rows", (8, 5, 32768, 64, {}), dict(split=0)),
     ("W4 K=17408 N=64 2 rows", (4, 2, 17408, 64, {}), dict(route="decode", quant="staged")),
     ("W4 K=24576 1 row", (4, 1, 24576, 4096, {}), dict(route="decode", quant=None)),
     ("W4 K=25600 1 row", (4, 1, 25600, 4096, {}), dict(route="decode", quant="staged")),
@@ -87,6 +102,24 @@ def test_overrides_steer_the_route(hb, monkeypatch):
     monkeypatch.setenv("BREEZE_HIP_DEC_ROWS", "4")
     assert hb.plan(4, 5, 4096, 4096)["route"] == "rows"  # past the decode rows, under the GEMM's 9
     assert hb.plan(4, 9, 4096, 4096)["route"] == "prefill"
+
+
+def test_split_overrides(hb, monkeypatch):
+    """BREEZE_HIP_SPLIT: 0 never, 1 wherever it fits, n >= 2 forces n pieces
+    (at most one a phase)."""
+    assert hb.plan(8, 1, 24576, 64)["split"] == 26
+    monkeypatch.setenv("BREEZE_HIP_SPLIT", "0")
+    assert hb.plan(8, 1, 24576, 64)["split"] == 0
+    monkeypatch.setenv("BREEZE_HIP_SPLIT", "1")
+    assert hb.plan(4, 1, 17408, 64)["split"] == 10  # 10 phases, 4 tiles
+    assert hb.plan(4, 1, 4096, 1024)["split"] == 3  # 64 tiles: 256 / 64 = 4 pieces, 3 phases
+    assert hb.plan(4, 1, 4096, 4096)["split"] == 0  # one workgroup a tile already fills the CUs
+    assert hb.plan(4, 1, 1024, 64)["split"] == 0  # one phase a tile
+    monkeypatch.setenv("BREEZE_HIP_SPLIT", "3")
+    p = hb.plan(4, 1, 17408, 64)
+    assert (p["split"], p["grid_x"]) == (3, 12)
+    monkeypatch.setenv("BREEZE_HIP_SPLIT", "64")
+    assert hb.plan(4, 1, 17408, 64)["split"] == 10
 
 
 def test_plan_follows_the_device_size(hb):

@@ -4,7 +4,8 @@ makes two calls in a row, the second with a smaller input, so the second
 runs on the scratch contents the first left behind.  Cases cover every
 kernel route that uses scratch: the decode kernels with staged activation
 records (four-row groups, and eight-row groups at 24 then 9 rows), the
-decode argmax state, the prefill GEMM's records, the rows
+decode argmax state, split-K's tickets and block values (cleared and
+overwritten on every call), the prefill GEMM's records, the rows
 kernel (legacy corr) and the argmax partials after it; plus a shape that
 needs no scratch and one too large for the fixed scratch, which is refused.
 """
@@ -40,20 +41,25 @@ def _reference_call(hb, torch, h, A, N, argmax):
     return c.cpu().numpy(), None
 
 
-@pytest.mark.parametrize("case", ["fused", "staged", "argmax", "row_groups_argmax", "eight_row_groups", "prefill",
-                                  "prefill_argmax"])
+@pytest.mark.parametrize("case", ["fused", "staged", "argmax", "row_groups_argmax", "eight_row_groups", "split",
+                                  "prefill", "prefill_argmax"])
 @pytest.mark.parametrize("bits", [4, 8])
-def test_noalloc_matches_allocating_entry(gpu, hb, hi_prec, case, bits):
+def test_noalloc_matches_allocating_entry(gpu, hb, hi_prec, monkeypatch, case, bits):
     torch = gpu
+    if case == "split":
+        monkeypatch.setenv("BREEZE_HIP_SPLIT", "1")
     K, N, rows, argmax = {
         "fused": (512, 256, (3, 1), False),
         "staged": (4608, 256, (8, 4), False),
         "argmax": (1024, 16 * 600, (2, 1), True),
         "row_groups_argmax": (1024, 16 * 320, (16, 12), True),
         "eight_row_groups": (4608, 256, (24, 9), True),
+        "split": (17408, 64, (2, 1), False),
         "prefill": (1056, 304, (130, 20), False),
         "prefill_argmax": (640, 16 * 300, (40, 17), True),
     }[case]
+    if case == "split":
+        assert all(hb.plan(bits, m, K, N, extra=bits == 4)["split"] >= 2 for m in rows)
     rng = np.random.default_rng(sum(map(ord, case)) + bits)
     qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, bits == 4)
     h = hb.prepack(qw, sc, qz, K, N, bits=bits)
