@@ -1124,7 +1124,7 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 //     128 (the C4 shape's 512 rows fill the CUs with 128-row workgroups).
 //   kSplitMaxTiles (8), kSplitMinPhases (20)  split-K takes plain decode
 //     calls of at most 8 column tiles whose tiles have 20 phases or more
-//     (15 chunks a phase: W8 K >= 17440, W4 K >= 34880).  The unsplit
+//     (15 chunks a phase: W8 K >= 18272, W4 K >= 36512).  The unsplit
 //     kernel spends ~0.45 (W8) / ~0.68 (W4) us a phase on one CU; the split
 //     launch spends ~3 us handing the pieces' block values across CUs
 //     (device-scope stores, a ticket, device-scope loads) and folds nblk

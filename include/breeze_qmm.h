@@ -120,8 +120,10 @@ int i4_silu_mul_dev(const float* dG, const float* dU, size_t n, float* dOut, voi
  * K counted rounded up to a multiple of 128 and, from 5 to 32 rows, M rounded
  * up to a multiple of 8 (the eight-row groups' records cover whole groups), and
  * about 68 bytes per 32-block of K per row, rows rounded up to 32, 64 or 128, for
- * the rows the prefill GEMM takes.  Calls that overlap on one device share the array and
- * race: serialize them.  Outputs are those of i4_matmul_dev /
+ * the rows the prefill GEMM takes; a split-K call (few column tiles over a long
+ * K) takes 4 bytes per 16-column tile rounded up to 256, plus 68 bytes per row
+ * and 32-block of K (K rounded up to a multiple of 128) per tile.  Calls that
+ * overlap on one device share the array and race: serialize them.  Outputs are those of i4_matmul_dev /
  * i4_matmul_argmax_dev, bit for bit. */
 int i4_matmul_noalloc_dev(void* handle, const float* dA, int M, float* dC, int64_t* dIdx, void* stream);
 
