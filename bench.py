@@ -671,8 +671,9 @@ def main():
         # The prefill shape also at 16 and 128 rows (32- and 128-row
         # workgroups of other widths).
         for name, r in (("w8_gemv", None), ("w4_gemv", None), ("w4_decode", 1), ("w4_decode", 2),
-                        ("w4_decode", 4), ("w4_decode", 8), ("w8_lmhead", None), ("w8_prefill", None),
-                        ("w4_prefill", None), ("w8_prefill", 16), ("w4_prefill", 16), ("w8_prefill", 128)):
+                        ("w4_decode", 4), ("w4_decode", 8), ("w8_skinny_k32768", None), ("w8_lmhead", None),
+                        ("w8_prefill", None), ("w4_prefill", None), ("w8_prefill", 16), ("w4_prefill", 16),
+                        ("w8_prefill", 128)):
             long_call = name in ("w8_lmhead", "w8_prefill", "w4_prefill")
             t, m = time_workload(hb, torch, name, r, max(10, args.steps // 4) if long_call else args.steps,
                                  max(3, args.warmup // 4) if long_call else args.warmup,

@@ -19,12 +19,14 @@ CONFIGS = {
     # Not benchmark workloads: the W4 counterpart of the prefill GEMM; two
     # tall-skinny decode shapes (few column tiles over a long K: a 64-column
     # projection of the MLP's 17408-wide activation, a 48-column one of a
-    # 12288-wide activation); and the decoder MLP's gate/up and down widths.
+    # 12288-wide activation, and a W8 64-column one over K = 32768, long
+    # enough for split-K); and the decoder MLP's gate/up and down widths.
     "w4_prefill": (4, 512, 5120, 17408, 4, 6, False),
     "w4_skinny_k17408": (4, 1, 17408, 64, 4, 7, False),
     "w4_skinny_k12288": (4, 1, 12288, 48, 4, 8, False),
     "w4_mlp_up": (4, 1, 5120, 17408, 4, 9, False),
     "w4_mlp_down": (4, 1, 17408, 5120, 4, 10, False),
+    "w8_skinny_k32768": (8, 1, 32768, 64, None, 11, False),
 }
 
 LABELS = {
@@ -38,6 +40,7 @@ LABELS = {
     "w4_skinny_k12288": "W4 tall-skinny M={M} K=12288 N=48, group-128 scales",
     "w4_mlp_up": "W4 MLP gate/up width M={M} K=5120 N=17408, group-128 scales",
     "w4_mlp_down": "W4 MLP down width M={M} K=17408 N=5120, group-128 scales",
+    "w8_skinny_k32768": "W8 tall-skinny M={M} K=32768 N=64 (split-K), per-channel scales",
 }
 
 
