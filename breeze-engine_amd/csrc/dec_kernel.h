@@ -51,6 +51,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     constexpr bool PAIR = FUSE == kFusePair, NORM = FUSE == kFuseNormMulti;
     constexpr bool MULTI = FUSE == kFuseMulti || NORM;
     constexpr bool SPLIT = FUSE == kFuseSplit;
+    // Weight chunks are read once per call: with STREAM the loads carry the
+    // non-temporal hint, which streams faster where a workgroup reads many
+    // tiles (the host decides; the idle loads' L2 re-reads then miss more,
+    // which costs where it has few).
+    constexpr bool STREAM = FUSE == kFuseStream;
     static_assert(!SPLIT || FUSED, "split-K quantizes its pieces in the prologue");
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int PP = dec_pitch(JG);
@@ -246,7 +251,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         // uniform-address copies on branches of their own.
         asm("" : "+v"(wi), "+v"(mi), "+v"(si));
         const bool up = PAIR && ld_sel;
-        p.w = (up ? a.W2 : lw)[wi];
+        if constexpr (STREAM) {
+            typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+            const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(lw + wi));
+            p.w = make_uint4(t.x, t.y, t.z, t.w);
+        } else {
+            p.w = (up ? a.W2 : lw)[wi];
+        }
         if (EXTRA) {
             const fvec sv = *reinterpret_cast<const fvec*>((up ? a.S2 : a.S) + (size_t)mi * JG);
             const ivec dv = *reinterpret_cast<const ivec*>((up ? a.D2 : a.D) + (size_t)mi * JG);
@@ -839,6 +850,8 @@ hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, in
         if constexpr (FUSED) return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseSplit, P64>(attr_set, a, grid, lds, st);
         return hipErrorInvalidValue;  // split pieces quantize in the prologue
     }
+    if (fuse == kFuseStream)
+        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseStream, P64>(attr_set, a, grid, lds, st);
     if constexpr (!EXTRA) {
         if (fuse == kFuseMulti)
             return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseMulti, P64>(attr_set, a, grid, lds, st);

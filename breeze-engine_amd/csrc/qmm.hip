@@ -1122,6 +1122,19 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 //     and the block-integer export).
 //   pick_pf_rp  32-row prefill workgroups up to 32 rows, 64 up to 64, then
 //     128 (the C4 shape's 512 rows fill the CUs with 128-row workgroups).
+//   kStreamIdleDiv (8)  plain decode calls read their weight chunks with
+//     non-temporal loads when at most one in 8 of a tile's producer slots
+//     (15 a phase) is idle.  Weights are read once a call; the hint streams
+//     them faster (a plain copy kernel over 1 GiB: 6.0-6.4 -> 7.0-7.2 TB/s),
+//     but the idle slots' loads, which re-read a tile's last chunk or warm
+//     L2 for the next tile's, then miss more.  Plain -> non-temporal: idle
+//     1/10-1/9 of the slots (W4 K=12288, W8 and W4 K=5120): C3 M=1 7.89 ->
+//     7.47, W8 K=5120 N=151936 (C5) 134.1 -> 122.8, N=17408 19.05 -> 17.57,
+//     N=16384 16.68 -> 15.61, W4 K=5120 N=17408 11.70 -> 11.53, W4 K=17408
+//     N=5120 14.97 -> 14.74; idle 11/75 (W8 K=4096): N=4096 (C1) 4.89 ->
+//     5.39, N=8192 7.74 -> 7.42, N=12288 10.56 -> 9.99; idle 13/45 (W4
+//     K=4096): N=12288 (C2) 7.19 -> 7.31, N=24576 12.39 -> 13.16, N=32768
+//     16.0 -> 15.9, N=65536 35.5 -> 35.2.
 //   kSplitMaxTiles (8), kSplitMinPhases (20)  split-K takes plain decode
 //     calls of at most 8 column tiles whose tiles have 20 phases or more
 //     (15 chunks a phase: W8 K >= 18272, W4 K >= 36512).  The unsplit
@@ -1140,7 +1153,8 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 // every prologue-quantized call), BREEZE_HIP_DEC8_ROWS (their row limit),
 // BREEZE_HIP_DEC8_LREC (0: records never in LDS; n: from n tiles),
 // BREEZE_HIP_PREFILL_RP / _CT (prefill workgroup shape), BREEZE_HIP_FUSED_MAX_BLOCKS
-// (row-blocks the decode prologue quantizes), BREEZE_HIP_SPLIT (split-K).
+// (row-blocks the decode prologue quantizes), BREEZE_HIP_SPLIT (split-K),
+// BREEZE_HIP_STREAM (non-temporal weight loads).
 constexpr int kFusedMaxBlocks = 512, kFusedMaxBlocks2 = 768;
 constexpr int kFusedCapBlocks = kQuantPasses * 256;  // what the prologue can quantize
 constexpr int kNormFusedMaxBlocks = 3 * 128;
@@ -1150,6 +1164,7 @@ constexpr int kPairMaxRows4 = 16;
 constexpr int kDec8LrecTiles = 2;
 constexpr int kPrefillMinRows = 9;
 constexpr int kSplitMaxTiles = 8, kSplitMinPhases = 20;
+constexpr int kStreamIdleDiv = 8;
 
 // Row-blocks the decode prologue quantizes itself for calls of M rows
 // (BREEZE_HIP_FUSED_MAX_BLOCKS sets it for every M, up to kFusedCapBlocks).
@@ -1264,7 +1279,22 @@ struct Plan {
     int pf_rp = 0, pf_ct = 0, Mpad = 0;  // prefill: row pairs, column tiles, padded rows
     int grid_x = 0, grid_y = 1;
     int split = 0;           // decode split-K: workgroups per tile (0: none)
+    bool stream = false;     // decode: weight chunks read with non-temporal loads
 };
+
+// Non-temporal weight loads (kFuseStream) for a plain decode call whose
+// tiles leave at most one in kStreamIdleDiv ring slots idle (15 chunks a
+// phase: the last phase's empty slots re-read or prefetch chunks through
+// L2, which non-temporal fills serve worse; see the routing table).
+// BREEZE_HIP_STREAM=0 / 1 turns them off / on for every plain decode call.
+bool stream_loads(const Shape& h, const CallKind& k, const Plan& p) {
+    if (k.pair || k.multi || k.norm || k.dots || p.split) return false;
+    if (const char* env = std::getenv("BREEZE_HIP_STREAM")) return env[0] == '1';
+    const int JG = h.bits == 8 ? 2 : 4;
+    const int nbg = (h.nblk + JG - 1) / JG;
+    const int slots = (nbg + kProducers - 1) / kProducers * kProducers;
+    return (slots - nbg) * kStreamIdleDiv <= slots;
+}
 
 // Split-K for a plain decode call of at most four rows (one row group): the
 // workgroups per tile (S pieces of the tile's phases), or 0.  S fills the
@@ -1388,6 +1418,7 @@ Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
             p.pair_xcd = p.NG % 8 == 0 ? 1 : 0;
         }
         p.grid_x = p.NG * p.RG;
+        p.stream = stream_loads(h, k, p);
     } else {
         p.route = kRouteRows;
         p.quant = kQuantStaged;
@@ -1552,7 +1583,11 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.Z2 = h2->Z;
         a.D2 = h2->D;
     }
-    const int fz = p.split ? kFuseSplit : pair ? kFusePair : mp ? (mp->norm ? kFuseNormMulti : kFuseMulti) : kFusePlain;
+    const int fz = p.split ? kFuseSplit
+                   : pair  ? kFusePair
+                   : mp    ? (mp->norm ? kFuseNormMulti : kFuseMulti)
+                   : p.stream ? kFuseStream
+                              : kFusePlain;
     const bool decode = p.route == kRouteDec || p.route == kRouteDec8;
     if (p.split) {
         // Split-K scratch: a ticket per tile (zero between calls; the
@@ -2165,7 +2200,7 @@ int i4_plan_query(int bits, int M, int K, int N, int flags, int n_cu, int32_t* o
     k.tiles = N / 16;
     const Plan p = plan_call(h, M, k, n_cu);
     const int32_t v[] = {p.route, p.quant, p.fused, p.p64, p.lrec, p.rs, p.RG, p.NG, p.pair_xcd, p.lds,
-                         p.pf_rp, p.pf_ct, p.grid_x, p.grid_y, p.split};
+                         p.pf_rp, p.pf_ct, p.grid_x, p.grid_y, p.split, p.stream};
     const int n = std::min(nout, (int)(sizeof(v) / sizeof(v[0])));
     for (int i = 0; i < n; ++i) out[i] = v[i];
     return n;

@@ -265,10 +265,11 @@ constexpr int kMaxSeg = 4;
 
 // Decode kernel modes: one weight set, the gate/up pair with the SiLU
 // epilogue, several projections of one activation, the same with the
-// decoder's RMSNorm applied to the activation in the prologue, and one
-// weight set split along K (each workgroup takes a range of one tile's
-// phases; the last to finish folds the tile).
-constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3, kFuseSplit = 4;
+// decoder's RMSNorm applied to the activation in the prologue, one weight
+// set split along K (each workgroup takes a range of one tile's phases; the
+// last to finish folds the tile), and one weight set whose chunks are read
+// with non-temporal loads (kFuseStream: the plain kernel otherwise).
+constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3, kFuseSplit = 4, kFuseStream = 5;
 
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
 // (explicit zero points, legacy corr, scale groups smaller than a chunk)

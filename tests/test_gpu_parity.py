@@ -642,3 +642,27 @@ def test_decode_prologue_passes(gpu, hb, orc, hi_prec, monkeypatch, bits, explic
             assert bits_equal(got, orc.matmul(qw, sc, qz, N, K, bits, A, hp)), (M, K, hp)
     finally:
         hb.free(h)
+
+
+# Non-temporal weight loads (the decode kernel's stream mode) change only how
+# the weight chunks are fetched: with the mode forced on and off, on shapes it
+# takes by default and shapes it does not, every output is the oracle's.
+@pytest.mark.parametrize("bits,M,K,N,explicit_zeros", [(4, 1, 12288, 256, False), (4, 3, 12288, 256, True),
+                                                       (8, 1, 5120, 512, False), (8, 2, 4096, 256, False),
+                                                       (4, 4, 4096, 512, False)])
+def test_stream_loads_are_the_same_bits(gpu, hb, orc, hi_prec, monkeypatch, bits, M, K, N, explicit_zeros):
+    torch = gpu
+    rng = np.random.default_rng(M * 11 + K + N + bits)
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        hb.set_hi_prec(True)
+        A = (rng.normal(size=(M, K)) * 3).astype(np.float32)
+        want = orc.matmul(qw, sc, qz, N, K, bits, A, True)
+        for mode in ("1", "0"):
+            monkeypatch.setenv("BREEZE_HIP_STREAM", mode)
+            assert hb.plan(bits, M, K, N, extra=explicit_zeros)["stream"] == int(mode)
+            got = hb.matmul(h, torch.from_numpy(A).cuda(), N).cpu().numpy()
+            assert bits_equal(got, want), mode
+    finally:
+        hb.free(h)

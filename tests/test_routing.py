@@ -65,6 +65,17 @@ TABLE = [
     ("no split: fold staging past LDS", (8, 4, 20480, 16, {}), dict(split=0)),
     ("no split: argmax", (8, 1, 32768, 64, dict(argmax=True)), dict(split=0)),
     ("no split: 5 rows", (8, 5, 32768, 64, {}), dict(split=0)),
+    # Non-temporal weight loads: plain decode calls whose tiles leave at most
+    # one in eight producer slots idle.
+    ("stream C3 1 row", (4, 1, 12288, 4096, {}), dict(route="decode", stream=1)),
+    ("stream C3 4 rows", (4, 4, 12288, 4096, {}), dict(route="decode", quant="staged", stream=1)),
+    ("stream C5 (argmax)", (8, 1, 5120, 151936, dict(argmax=True)), dict(route="decode", stream=1)),
+    ("stream W4 K=5120", (4, 1, 5120, 17408, {}), dict(stream=1)),
+    ("no stream C1: 11 of 75 slots idle", (8, 1, 4096, 4096, {}), dict(stream=0)),
+    ("no stream C2: 13 of 45 slots idle", (4, 1, 4096, 12288, {}), dict(stream=0)),
+    ("no stream: gate/up pair", (4, 1, 5120, 17408, dict(pair=True)), dict(stream=0)),
+    ("no stream: split-K", (8, 1, 24576, 64, {}), dict(split=26, stream=0)),
+    ("no stream: eight-row groups", (4, 8, 12288, 4096, {}), dict(route="decode8", stream=0)),
     ("W4 K=17408 N=64 2 rows", (4, 2, 17408, 64, {}), dict(route="decode", quant="staged")),
     ("W4 K=24576 1 row", (4, 1, 24576, 4096, {}), dict(route="decode", quant=None)),
     ("W4 K=25600 1 row", (4, 1, 25600, 4096, {}), dict(route="decode", quant="staged")),
@@ -120,6 +131,18 @@ def test_split_overrides(hb, monkeypatch):
     assert (p["split"], p["grid_x"]) == (3, 12)
     monkeypatch.setenv("BREEZE_HIP_SPLIT", "64")
     assert hb.plan(4, 1, 17408, 64)["split"] == 10
+
+
+def test_stream_override(hb, monkeypatch):
+    """BREEZE_HIP_STREAM: 0 / 1 turn non-temporal weight loads off / on for
+    every plain decode call (never for fused calls or split-K)."""
+    assert hb.plan(8, 1, 5120, 151936, argmax=True)["stream"] == 1
+    monkeypatch.setenv("BREEZE_HIP_STREAM", "0")
+    assert hb.plan(8, 1, 5120, 151936, argmax=True)["stream"] == 0
+    monkeypatch.setenv("BREEZE_HIP_STREAM", "1")
+    assert hb.plan(8, 1, 4096, 4096)["stream"] == 1
+    assert hb.plan(4, 1, 5120, 17408, pair=True)["stream"] == 0
+    assert hb.plan(4, 1, 5120, 10240, multi=True)["stream"] == 0
 
 
 def test_plan_follows_the_device_size(hb):
