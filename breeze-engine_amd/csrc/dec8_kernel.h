@@ -60,7 +60,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
     // then up projection, C = silu(gate) * up), or several projections of
     // the activation (tiles concatenated over the segment table).
     constexpr bool PAIR = FUSE == kFusePair, MULTI = FUSE == kFuseMulti;
-    static_assert(FUSE == kFusePlain || PAIR || MULTI, "no norm in this kernel's prologue");
+    // STREAM: the plain kernel with non-temporal weight loads (the host takes
+    // it where each tile is read by at most two row groups: more share the
+    // weights through L2, which non-temporal fills serve worse).
+    constexpr bool STREAM = FUSE == kFuseStream;
+    static_assert(FUSE == kFusePlain || PAIR || MULTI || STREAM, "no norm in this kernel's prologue");
     typedef float fvec __attribute__((ext_vector_type(JG)));
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -203,7 +207,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
         uint32_t mi = ld_m + c * 16 + col;
         asm("" : "+v"(wi), "+v"(si), "+v"(ri), "+v"(mi));
         const bool up = PAIR && ld_sel;
-        p.w = (up ? args.W2 : lw)[wi];
+        if constexpr (STREAM) {
+            typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+            const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(lw + wi));
+            p.w = make_uint4(t.x, t.y, t.z, t.w);
+        } else {
+            p.w = (up ? args.W2 : lw)[wi];
+        }
         if constexpr (!LREC) {
 #pragma unroll
             for (int h = 0; h < NA; ++h) p.a[h] = pR[ri + 64 * h];
@@ -453,7 +463,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec8_kernel(const uint4* pW, c
 template <int BITS, bool HP, bool EXTRA, int FUSE, bool LREC>
 hipError_t launch_dec8_f(bool* attr_set, const GemvArgs& a, const uint4* rec, int grid, int lds, hipStream_t st) {
     auto kern = dec8_kernel<BITS, HP, EXTRA, FUSE, LREC>;
-    bool& set = attr_set[FUSE + (EXTRA ? 3 : 0) + (LREC ? 6 : 0)];
+    bool& set = attr_set[(FUSE == kFuseStream ? 3 : FUSE) + (EXTRA ? 4 : 0) + (LREC ? 8 : 0)];
     if (!set) {
         const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, kLdsMax);
@@ -468,7 +478,7 @@ hipError_t launch_dec8_f(bool* attr_set, const GemvArgs& a, const uint4* rec, in
 }
 
 // attr_set: this device's flags for the (bits, mode) pair, one per (FUSE
-// mode, per-block metadata, records in LDS) variant.  Handles with per-block
+// mode, per-block metadata, records in LDS) variant (16 a pair).  Handles with per-block
 // metadata take the plain and paired calls (the multi-projection launch
 // sends them one by one).
 template <int BITS, bool HP, bool LREC>
@@ -476,11 +486,13 @@ hipError_t launch_dec8_l(bool* attr_set, const GemvArgs& a, const uint4* rec, in
                          hipStream_t st) {
     if (extra) {
         if (fuse == kFusePair) return launch_dec8_f<BITS, HP, true, kFusePair, LREC>(attr_set, a, rec, grid, lds, st);
+        if (fuse == kFuseStream) return launch_dec8_f<BITS, HP, true, kFuseStream, LREC>(attr_set, a, rec, grid, lds, st);
         if (fuse != kFusePlain) return hipErrorInvalidValue;
         return launch_dec8_f<BITS, HP, true, kFusePlain, LREC>(attr_set, a, rec, grid, lds, st);
     }
     if (fuse == kFusePair) return launch_dec8_f<BITS, HP, false, kFusePair, LREC>(attr_set, a, rec, grid, lds, st);
     if (fuse == kFuseMulti) return launch_dec8_f<BITS, HP, false, kFuseMulti, LREC>(attr_set, a, rec, grid, lds, st);
+    if (fuse == kFuseStream) return launch_dec8_f<BITS, HP, false, kFuseStream, LREC>(attr_set, a, rec, grid, lds, st);
     if (fuse != kFusePlain) return hipErrorInvalidValue;
     return launch_dec8_f<BITS, HP, false, kFusePlain, LREC>(attr_set, a, rec, grid, lds, st);
 }

@@ -783,7 +783,7 @@ struct Workspace {
     hipStream_t stream = nullptr;
     int n_cu = 0;
     bool attr_set[512] = {};  // decode kernel variants with the kernel attribute set
-    bool dec8_attr[48] = {};  // the same for dec8_kernel, per (bits, mode) and (FUSE mode, metadata, LDS records)
+    bool dec8_attr[64] = {};  // the same for dec8_kernel, per (bits, mode) and (FUSE mode, metadata, LDS records)
     bool pf_attr[256] = {};
 };
 
@@ -1134,7 +1134,10 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 //     N=5120 14.97 -> 14.74; idle 11/75 (W8 K=4096): N=4096 (C1) 4.89 ->
 //     5.39, N=8192 7.74 -> 7.42, N=12288 10.56 -> 9.99; idle 13/45 (W4
 //     K=4096): N=12288 (C2) 7.19 -> 7.31, N=24576 12.39 -> 13.16, N=32768
-//     16.0 -> 15.9, N=65536 35.5 -> 35.2.
+//     16.0 -> 15.9, N=65536 35.5 -> 35.2.  Eight-row groups (14 chunks a
+//     phase), kStreamMaxGroups (2): W4 K=12288 N=4096 at 8 / 16 / 24 rows
+//     (one / two / three row groups) 13.13 / 19.12 / 29.75 -> 12.65 / 18.99 /
+//     31.79, W8 K=5120 N=17408 at 16 rows 33.13 -> 31.27, W4 28.77 -> 28.50.
 //   kSplitMaxTiles (8), kSplitMinPhases (20)  split-K takes plain decode
 //     calls of at most 8 column tiles whose tiles have 20 phases or more
 //     (15 chunks a phase: W8 K >= 18272, W4 K >= 36512).  The unsplit
@@ -1164,7 +1167,7 @@ constexpr int kPairMaxRows4 = 16;
 constexpr int kDec8LrecTiles = 2;
 constexpr int kPrefillMinRows = 9;
 constexpr int kSplitMaxTiles = 8, kSplitMinPhases = 20;
-constexpr int kStreamIdleDiv = 8;
+constexpr int kStreamIdleDiv = 8, kStreamMaxGroups = 2;
 
 // Row-blocks the decode prologue quantizes itself for calls of M rows
 // (BREEZE_HIP_FUSED_MAX_BLOCKS sets it for every M, up to kFusedCapBlocks).
@@ -1283,17 +1286,19 @@ struct Plan {
 };
 
 // Non-temporal weight loads (kFuseStream) for a plain decode call whose
-// tiles leave at most one in kStreamIdleDiv ring slots idle (15 chunks a
-// phase: the last phase's empty slots re-read or prefetch chunks through
-// L2, which non-temporal fills serve worse; see the routing table).
-// BREEZE_HIP_STREAM=0 / 1 turns them off / on for every plain decode call.
-bool stream_loads(const Shape& h, const CallKind& k, const Plan& p) {
+// tiles leave at most one in kStreamIdleDiv producer slots idle
+// (`producers` chunks a phase: the last phase's empty slots re-read or
+// prefetch chunks through L2, which non-temporal fills serve worse) and
+// whose tiles are read by at most kStreamMaxGroups row groups (more share
+// the weights through L2); see the routing table.  BREEZE_HIP_STREAM=0 / 1
+// turns them off / on for every plain decode call.
+bool stream_loads(const Shape& h, const CallKind& k, const Plan& p, int producers) {
     if (k.pair || k.multi || k.norm || k.dots || p.split) return false;
     if (const char* env = std::getenv("BREEZE_HIP_STREAM")) return env[0] == '1';
     const int JG = h.bits == 8 ? 2 : 4;
     const int nbg = (h.nblk + JG - 1) / JG;
-    const int slots = (nbg + kProducers - 1) / kProducers * kProducers;
-    return (slots - nbg) * kStreamIdleDiv <= slots;
+    const int slots = (nbg + producers - 1) / producers * producers;
+    return p.RG <= kStreamMaxGroups && (slots - nbg) * kStreamIdleDiv <= slots;
 }
 
 // Split-K for a plain decode call of at most four rows (one row group): the
@@ -1405,6 +1410,7 @@ Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
         p.lrec = tiles_wg >= dec8_lrec_min_tiles() && lrec_lds <= kLdsMax &&
                  h.nblk_pad * 32 <= kRecCopy * kDecWaves * 64;
         p.lds = p.lrec ? lrec_lds : dec8_lds(h.nblk, JG).total;
+        p.stream = stream_loads(h, k, p, kP8);
     } else if (dec) {
         p.route = kRouteDec;
         p.quant = fused ? kQuantNone : kQuantStaged;
@@ -1418,7 +1424,7 @@ Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
             p.pair_xcd = p.NG % 8 == 0 ? 1 : 0;
         }
         p.grid_x = p.NG * p.RG;
-        p.stream = stream_loads(h, k, p);
+        p.stream = stream_loads(h, k, p, kProducers);
     } else {
         p.route = kRouteRows;
         p.quant = kQuantStaged;
@@ -1662,7 +1668,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     const bool x = h->extra;
     if (p.route == kRouteDec8) {
         const uint4* rec = reinterpret_cast<const uint4*>(s.aq);
-        bool* at = &w.dec8_attr[12 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
+        bool* at = &w.dec8_attr[16 * ((h->bits == 8 ? 1 : 0) | (hp ? 2 : 0))];
         if (h->bits == 8) e = hp ? launch_dec8<8, true>(at, a, rec, p.grid_x, p.lds, fz, x, p.lrec, st)
                                  : launch_dec8<8, false>(at, a, rec, p.grid_x, p.lds, fz, x, p.lrec, st);
         else e = hp ? launch_dec8<4, true>(at, a, rec, p.grid_x, p.lds, fz, x, p.lrec, st)

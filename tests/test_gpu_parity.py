@@ -649,7 +649,8 @@ def test_decode_prologue_passes(gpu, hb, orc, hi_prec, monkeypatch, bits, explic
 # takes by default and shapes it does not, every output is the oracle's.
 @pytest.mark.parametrize("bits,M,K,N,explicit_zeros", [(4, 1, 12288, 256, False), (4, 3, 12288, 256, True),
                                                        (8, 1, 5120, 512, False), (8, 2, 4096, 256, False),
-                                                       (4, 4, 4096, 512, False)])
+                                                       (4, 4, 4096, 512, False), (4, 8, 12288, 256, False),
+                                                       (8, 12, 5120, 512, False), (4, 16, 12288, 256, True)])
 def test_stream_loads_are_the_same_bits(gpu, hb, orc, hi_prec, monkeypatch, bits, M, K, N, explicit_zeros):
     torch = gpu
     rng = np.random.default_rng(M * 11 + K + N + bits)

@@ -75,7 +75,10 @@ TABLE = [
     ("no stream C2: 13 of 45 slots idle", (4, 1, 4096, 12288, {}), dict(stream=0)),
     ("no stream: gate/up pair", (4, 1, 5120, 17408, dict(pair=True)), dict(stream=0)),
     ("no stream: split-K", (8, 1, 24576, 64, {}), dict(split=26, stream=0)),
-    ("no stream: eight-row groups", (4, 8, 12288, 4096, {}), dict(route="decode8", stream=0)),
+    ("stream C3 8 rows (eight-row groups, one row group)", (4, 8, 12288, 4096, {}),
+     dict(route="decode8", row_groups=1, stream=1)),
+    ("stream W8 16 rows (two row groups)", (8, 16, 5120, 17408, {}), dict(route="decode8", row_groups=2, stream=1)),
+    ("no stream: three row groups", (4, 24, 12288, 4096, {}), dict(route="decode8", row_groups=3, stream=0)),
     ("W4 K=17408 N=64 2 rows", (4, 2, 17408, 64, {}), dict(route="decode", quant="staged")),
     ("W4 K=24576 1 row", (4, 1, 24576, 4096, {}), dict(route="decode", quant=None)),
     ("W4 K=25600 1 row", (4, 1, 25600, 4096, {}), dict(route="decode", quant="staged")),
