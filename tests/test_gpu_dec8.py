@@ -262,3 +262,26 @@ def test_dec8_records_in_lds(gpu, hb, orc, hi_prec, bits, K):
     finally:
         hb.free(h)
         hb.free(hu)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_dec8_argmax_long_k(gpu, hb, orc, hi_prec, bits):
+    """24 rows over K = 17408 with the argmax: the eight-row groups take the
+    call (four rows of records would not fit the four-row groups), and the
+    index is the one their in-kernel merge writes (no second argmax launch
+    follows the eight-row kernel)."""
+    K, N, M = 17408, 16 * 40, 24
+    assert hb.plan(bits, M, K, N, argmax=True)["route"] == "decode8"
+    rng = np.random.default_rng(90 + bits)
+    qw, sc, _ = rng_weights(rng, N, K, bits)
+    h = hb.prepack(qw, sc, None, K, N, bits=bits)
+    try:
+        hb.set_hi_prec(True)
+        A = rng.normal(size=(M, K)).astype(np.float32)
+        want = orc.matmul(qw, sc, None, N, K, bits, A, True)
+        c, idx = hb.matmul_argmax(h, gpu.from_numpy(A).cuda(), N)
+        gpu.cuda.synchronize()
+        assert bits_equal(c.cpu().numpy(), want)
+        assert idx.cpu().tolist() == np.argmax(want, axis=1).tolist()
+    finally:
+        hb.free(h)
