@@ -301,7 +301,7 @@ def matmul_silu_mul(gate, up, a2d, N):
 
 
 PLAN_FIELDS = ("route", "quant", "fused", "p64", "lrec", "rows_per_group", "row_groups", "tile_ranges", "pair_xcd",
-               "lds", "pf_rp", "pf_ct", "grid_x", "grid_y", "split", "stream")
+               "lds", "pf_rp", "pf_ct", "grid_x", "grid_y", "split", "stream", "flow")
 ROUTES = {0: None, 1: "decode", 2: "decode8", 3: "prefill", 4: "rows"}
 QUANTIZERS = {0: None, 1: "staged", 2: "rows8", 3: "prefill"}
 

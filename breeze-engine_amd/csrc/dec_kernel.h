@@ -55,7 +55,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     // non-temporal hint, which streams faster where a workgroup reads many
     // tiles (the host decides; the idle loads' L2 re-reads then miss more,
     // which costs where it has few).
-    constexpr bool STREAM = FUSE == kFuseStream;
+    constexpr bool STREAM = FUSE == kFuseStream || FUSE == kFuseFlowStream;
+    // FLOW: phases run across tile boundaries (the host takes it where
+    // workgroups hold several tiles of at least 15 chunks).
+    constexpr bool FLOW = FUSE == kFuseFlow || FUSE == kFuseFlowStream;
     static_assert(!SPLIT || FUSED, "split-K quantizes its pieces in the prologue");
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int PP = dec_pitch(JG);
@@ -168,7 +171,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int t_begin = g * base_t + min(g, rem_t);
     const int nT = base_t + (g < rem_t ? 1 : 0);
     const int nbg = a.nbg;
-    const int U = SPLIT ? pb - pa : nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
+    const int U = SPLIT  ? pb - pa
+                  : FLOW ? (nT * nbg + kProducers - 1) / kProducers
+                         : nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
 
     const DecLds lay = dec_lds(min(a.M, a.RS), SPLIT ? split_piece_blocks(npw, nsplit, a.nbg, JG) : a.nblk, JG, P64);
     uint8_t* recs = smem + lay.recs;
@@ -239,7 +244,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     uint32_t ld_s = (uint32_t)(t_begin - t_off) * a.ngrp * 16;
     uint32_t ld_m = (uint32_t)t_begin * nbg * 16;
     const int pf_c = nbg + kProducers + wave;
-    const bool pf = !PAIR && !MULTI && npw >= 2 && wave + kProducers < nbg;
+    const bool pf = !PAIR && !MULTI && !FLOW && npw >= 2 && wave + kProducers < nbg;
     int ld_idle = (pf && nT > 1) ? pf_c : nbg - 1;  // weight chunk of a load with no work
     auto load_unit = [&](Unit<JG, EXTRA>& p) {
         const int c = min(ld_c, nbg - 1);
@@ -272,7 +277,20 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         }
         p.c = ld_c;
         ld_c += kProducers;
-        if (--ld_rem == 0) {
+        if constexpr (FLOW) {
+            // One stream of chunks over the tiles (nbg >= 15: one wrap at
+            // most); past the last tile the loads re-read its last chunk.
+            if (ld_c >= nbg) {
+                if (++ld_t < nT) {
+                    ld_c -= nbg;
+                    ld_w += nbg * 64;
+                    ld_s += a.ngrp * 16;
+                    ld_m += nbg * 16;
+                } else {
+                    ld_c = 1 << 24;
+                }
+            }
+        } else if (--ld_rem == 0) {
             ld_rem = npw;
             if (PAIR && ld_sel == 0 && ld_t < nT) {
                 ld_sel = 1;  // the same tile's up projection
@@ -483,9 +501,85 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         float acc = 0.0f, gate = 0.0f;
         unsigned long long best = 0;
         int pr_t = 0, pr_p = pa, pr_sel = 0, pr_k = 0;
+        int tb = 0;  // FLOW: the stream's chunk index where tile pr_t starts
+        // FLOW: a finished tile's outputs (and argmax keys).
+        auto emit = [&](float v) {
+            if (grp < Mr) {
+                const int n = (t_begin + pr_t) * 16 + col;
+                a.C[(size_t)(m0 + grp) * a.N + n] = v;
+                if (a.idx) {
+                    const unsigned long long k = argmax_key(v, n);
+                    best = k > best ? k : best;
+                }
+            }
+        };
         for (int u = 0; u < U; ++u) {
             lds_barrier();
             const float* fp = fbuf + ((u & 1) * 64 + lane) * PP;
+            if constexpr (FLOW) {
+                // Slot i holds chunk kProducers u + i of the stream: chunk
+                // c0 + i of tile pr_t while that lasts.
+                const int c0 = kProducers * u - tb, rem = nbg - c0;
+                const float* sp = sa_row + c0 * JG;
+                if (rem >= kProducers) {
+                    // The phase lies in one tile, no padding: as the
+                    // unsplit kernel's full phase.
+                    fvec fv[kProducers], sv[kProducers];
+#pragma unroll
+                    for (int i = 0; i < kProducers; ++i) {
+                        fv[i] = *reinterpret_cast<const fvec*>(fp + i * JG);
+                        sv[i] = *reinterpret_cast<const fvec*>(sp + i * JG);
+                    }
+#pragma unroll
+                    for (int i = 0; i < kProducers; ++i) {
+#pragma unroll
+                        for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[i][jb], fv[i][jb], acc);
+                    }
+                    if (rem == kProducers) {
+                        emit(acc);
+                        acc = 0.0f;
+                        ++pr_t;
+                        tb += nbg;
+                    }
+                } else {
+                    // Tile pr_t ends at slot rem - 1 (no padding: the host
+                    // takes FLOW only where nblk is whole chunks); the next
+                    // tile's chunks 0.. follow from slot rem, or nothing
+                    // after the last tile (those slots are folded into no
+                    // output).  In two halves of slots (fewer registers
+                    // live than the full phase), the tile's sum taken when
+                    // slot rem begins.
+                    float out = 0.0f;
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        constexpr int kH = (kProducers + 1) / 2;
+                        fvec fv[kH], sv[kH];
+#pragma unroll
+                        for (int k = 0; k < kH; ++k) {
+                            const int i = h * kH + k;
+                            if (i < kProducers) {
+                                const int so = i < rem ? c0 + i : i - rem;
+                                fv[k] = *reinterpret_cast<const fvec*>(fp + i * JG);
+                                sv[k] = *reinterpret_cast<const fvec*>(sa_row + so * JG);
+                            }
+                        }
+#pragma unroll
+                        for (int k = 0; k < kH; ++k) {
+                            const int i = h * kH + k;
+                            if (i < kProducers) {
+                                out = i == rem ? acc : out;
+                                acc = i == rem ? 0.0f : acc;
+#pragma unroll
+                                for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[k][jb], fv[k][jb], acc);
+                            }
+                        }
+                    }
+                    emit(out);
+                    ++pr_t;
+                    tb += nbg;
+                }
+                continue;
+            }
             const int c0 = kProducers * pr_p;
             const float* sp = sa_row + (c0 - coff) * JG;
             if constexpr (SPLIT) {
@@ -852,6 +946,10 @@ hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, in
     }
     if (fuse == kFuseStream)
         return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseStream, P64>(attr_set, a, grid, lds, st);
+    if (fuse == kFuseFlow)
+        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseFlow, P64>(attr_set, a, grid, lds, st);
+    if (fuse == kFuseFlowStream)
+        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseFlowStream, P64>(attr_set, a, grid, lds, st);
     if constexpr (!EXTRA) {
         if (fuse == kFuseMulti)
             return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseMulti, P64>(attr_set, a, grid, lds, st);

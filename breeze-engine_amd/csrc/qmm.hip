@@ -1157,7 +1157,8 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 // BREEZE_HIP_DEC8_LREC (0: records never in LDS; n: from n tiles),
 // BREEZE_HIP_PREFILL_RP / _CT (prefill workgroup shape), BREEZE_HIP_FUSED_MAX_BLOCKS
 // (row-blocks the decode prologue quantizes), BREEZE_HIP_SPLIT (split-K),
-// BREEZE_HIP_STREAM (non-temporal weight loads).
+// BREEZE_HIP_STREAM (non-temporal weight loads), BREEZE_HIP_FLOW (phases
+// across tile boundaries).
 constexpr int kFusedMaxBlocks = 512, kFusedMaxBlocks2 = 768;
 constexpr int kFusedCapBlocks = kQuantPasses * 256;  // what the prologue can quantize
 constexpr int kNormFusedMaxBlocks = 3 * 128;
@@ -1283,7 +1284,23 @@ struct Plan {
     int grid_x = 0, grid_y = 1;
     int split = 0;           // decode split-K: workgroups per tile (0: none)
     bool stream = false;     // decode: weight chunks read with non-temporal loads
+    bool flow = false;       // decode: phases run across the tiles of a workgroup
 };
+
+// Phases across tile boundaries (kFuseFlow) for a plain decode call whose
+// busiest workgroups hold two tiles or more of at least 15 whole chunks
+// (no padded last chunk) that do not fill whole phases (see the routing
+// table).  BREEZE_HIP_FLOW=0 / 1
+// turns it off / on wherever it applies.
+bool flow_phases(const Shape& h, const CallKind& k, const Plan& p, int tiles) {
+    if (k.pair || k.multi || k.norm || k.dots || p.split) return false;
+    const int JG = h.bits == 8 ? 2 : 4;
+    const int nbg = (h.nblk + JG - 1) / JG;
+    if (nbg < kProducers || h.nblk % JG) return false;  // one tile end a phase; no padded chunk
+    const int per_wg = (tiles + p.NG - 1) / p.NG;
+    if (const char* env = std::getenv("BREEZE_HIP_FLOW")) return env[0] == '1';
+    return per_wg >= 2 && nbg % kProducers != 0;
+}
 
 // Non-temporal weight loads (kFuseStream) for a plain decode call whose
 // tiles leave at most one in kStreamIdleDiv producer slots idle
@@ -1292,11 +1309,12 @@ struct Plan {
 // whose tiles are read by at most kStreamMaxGroups row groups (more share
 // the weights through L2); see the routing table.  BREEZE_HIP_STREAM=0 / 1
 // turns them off / on for every plain decode call.
-bool stream_loads(const Shape& h, const CallKind& k, const Plan& p, int producers) {
+bool stream_loads(const Shape& h, const CallKind& k, const Plan& p, int producers, int tiles) {
     if (k.pair || k.multi || k.norm || k.dots || p.split) return false;
     if (const char* env = std::getenv("BREEZE_HIP_STREAM")) return env[0] == '1';
     const int JG = h.bits == 8 ? 2 : 4;
-    const int nbg = (h.nblk + JG - 1) / JG;
+    int nbg = (h.nblk + JG - 1) / JG;
+    if (p.flow) nbg *= (tiles + p.NG - 1) / p.NG;  // one stream over the busiest workgroup's tiles
     const int slots = (nbg + producers - 1) / producers * producers;
     return p.RG <= kStreamMaxGroups && (slots - nbg) * kStreamIdleDiv <= slots;
 }
@@ -1410,7 +1428,7 @@ Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
         p.lrec = tiles_wg >= dec8_lrec_min_tiles() && lrec_lds <= kLdsMax &&
                  h.nblk_pad * 32 <= kRecCopy * kDecWaves * 64;
         p.lds = p.lrec ? lrec_lds : dec8_lds(h.nblk, JG).total;
-        p.stream = stream_loads(h, k, p, kP8);
+        p.stream = stream_loads(h, k, p, kP8, tiles);
     } else if (dec) {
         p.route = kRouteDec;
         p.quant = fused ? kQuantNone : kQuantStaged;
@@ -1424,7 +1442,8 @@ Plan plan_call(const Shape& h, int M, const CallKind& k, int n_cu) {
             p.pair_xcd = p.NG % 8 == 0 ? 1 : 0;
         }
         p.grid_x = p.NG * p.RG;
-        p.stream = stream_loads(h, k, p, kProducers);
+        p.flow = flow_phases(h, k, p, tiles);
+        p.stream = stream_loads(h, k, p, kProducers, tiles);
     } else {
         p.route = kRouteRows;
         p.quant = kQuantStaged;
@@ -1592,6 +1611,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
     const int fz = p.split ? kFuseSplit
                    : pair  ? kFusePair
                    : mp    ? (mp->norm ? kFuseNormMulti : kFuseMulti)
+                   : p.flow   ? (p.stream ? kFuseFlowStream : kFuseFlow)
                    : p.stream ? kFuseStream
                               : kFusePlain;
     const bool decode = p.route == kRouteDec || p.route == kRouteDec8;
@@ -2206,7 +2226,7 @@ int i4_plan_query(int bits, int M, int K, int N, int flags, int n_cu, int32_t* o
     k.tiles = N / 16;
     const Plan p = plan_call(h, M, k, n_cu);
     const int32_t v[] = {p.route, p.quant, p.fused, p.p64, p.lrec, p.rs, p.RG, p.NG, p.pair_xcd, p.lds,
-                         p.pf_rp, p.pf_ct, p.grid_x, p.grid_y, p.split, p.stream};
+                         p.pf_rp, p.pf_ct, p.grid_x, p.grid_y, p.split, p.stream, p.flow};
     const int n = std::min(nout, (int)(sizeof(v) / sizeof(v[0])));
     for (int i = 0; i < n; ++i) out[i] = v[i];
     return n;

@@ -269,7 +269,12 @@ constexpr int kMaxSeg = 4;
 // set split along K (each workgroup takes a range of one tile's phases; the
 // last to finish folds the tile), and one weight set whose chunks are read
 // with non-temporal loads (kFuseStream: the plain kernel otherwise).
-constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3, kFuseSplit = 4, kFuseStream = 5;
+// kFuseFlow and kFuseFlowStream are the plain kernel (with ordinary or
+// non-temporal loads) whose phases run across tile boundaries: the chunks
+// of a workgroup's tiles form one stream, so a tile's short last phase is
+// filled with the next tile's first chunks.
+constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3, kFuseSplit = 4, kFuseStream = 5,
+              kFuseFlow = 6, kFuseFlowStream = 7;
 
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
 // (explicit zero points, legacy corr, scale groups smaller than a chunk)

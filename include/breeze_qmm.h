@@ -157,7 +157,7 @@ int i4_rmsnorm_matmul_multi_dev(const float* dX, const float* dNormW, float eps,
  * handle.  flags: 1 block-integer export, 2 argmax, 4 gate/up pair,
  * 8 multi-projection (one segment of N), 16 RMSNorm in that launch,
  * 32 per-block metadata (explicit zero points or small scale groups),
- * 64 legacy corr; n_cu: compute units of the device.  out[0..15] = route
+ * 64 legacy corr; n_cu: compute units of the device.  out[0..16] = route
  * (1 decode in four-row groups, 2 decode in eight-row groups, 3 prefill
  * GEMM, 4 rows kernel, 0 no single launch takes a paired or multi call),
  * stand-alone quantizer (0 none: the decode prologue quantizes, 1 staged
@@ -165,7 +165,8 @@ int i4_rmsnorm_matmul_multi_dev(const float* dX, const float* dNormW, float eps,
  * block pairs, records in LDS, rows per row group, row groups, tile ranges,
  * row groups of a tile range on one XCD, LDS bytes, prefill row pairs,
  * prefill column tiles, grid x, grid y, split-K workgroups per tile (0:
- * none), non-temporal weight loads.  Environment overrides apply as for
+ * none), non-temporal weight loads, phases across tile boundaries.
+ * Environment overrides apply as for
  * a call.  Returns the number of values written (at most nout), or -1. */
 int i4_plan_query(int bits, int M, int K, int N, int flags, int n_cu, int32_t* out, int nout);
 

@@ -667,3 +667,39 @@ def test_stream_loads_are_the_same_bits(gpu, hb, orc, hi_prec, monkeypatch, bits
             assert bits_equal(got, want), mode
     finally:
         hb.free(h)
+
+
+# Phases across tile boundaries (the decode kernel's flow mode): a
+# workgroup's tiles form one stream of chunks, a tile ending inside a phase.
+# Forced on and off, with and without non-temporal loads, over shapes with
+# two to three tiles a workgroup (tiles of 15 chunks, ending on a phase
+# boundary, among them), one to three rows, zero points and the argmax:
+# every output is the oracle's and every index its first maximum.
+@pytest.mark.parametrize("bits,M,K,N,explicit_zeros,argmax", [(4, 1, 4096, 16 * 600, False, False),
+                                                              (4, 2, 4096, 16 * 520, True, False),
+                                                              (8, 1, 5120, 16 * 700, False, True),
+                                                              (8, 3, 2432, 16 * 300, False, True),
+                                                              (4, 3, 1920, 16 * 513, False, False)])
+def test_flow_phases_are_the_same_bits(gpu, hb, orc, hi_prec, monkeypatch, bits, M, K, N, explicit_zeros, argmax):
+    torch = gpu
+    rng = np.random.default_rng(M * 13 + K + N + bits)
+    qw, sc, qz = rng_weights(rng, N, K, bits, np.float32, explicit_zeros)
+    h = hb.prepack(qw, sc, qz, K, N, bits=bits)
+    try:
+        hb.set_hi_prec(True)
+        A = (rng.normal(size=(M, K)) * 2).astype(np.float32)
+        want = orc.matmul(qw, sc, qz, N, K, bits, A, True)
+        for flow, stream in (("1", "0"), ("1", "1"), ("0", "0")):
+            monkeypatch.setenv("BREEZE_HIP_FLOW", flow)
+            monkeypatch.setenv("BREEZE_HIP_STREAM", stream)
+            p = hb.plan(bits, M, K, N, extra=explicit_zeros, argmax=argmax)
+            assert (p["flow"], p["stream"]) == (int(flow), int(stream)), p
+            dA = torch.from_numpy(A).cuda()
+            if argmax:
+                c, idx = hb.matmul_argmax(h, dA, N)
+                assert idx.cpu().tolist() == np.argmax(want, axis=1).tolist(), (flow, stream)
+            else:
+                c = hb.matmul(h, dA, N)
+            assert bits_equal(c.cpu().numpy(), want), (flow, stream)
+    finally:
+        hb.free(h)

@@ -72,9 +72,18 @@ TABLE = [
     ("stream C5 (argmax)", (8, 1, 5120, 151936, dict(argmax=True)), dict(route="decode", stream=1)),
     ("stream W4 K=5120", (4, 1, 5120, 17408, {}), dict(stream=1)),
     ("no stream C1: 11 of 75 slots idle", (8, 1, 4096, 4096, {}), dict(stream=0)),
-    ("no stream C2: 13 of 45 slots idle", (4, 1, 4096, 12288, {}), dict(stream=0)),
     ("no stream: gate/up pair", (4, 1, 5120, 17408, dict(pair=True)), dict(stream=0)),
     ("no stream: split-K", (8, 1, 24576, 64, {}), dict(split=26, stream=0)),
+    # Phases across tile boundaries: several tiles a workgroup, whole chunks
+    # that do not fill whole phases; then one stream of chunks leaves few
+    # slots idle, so those calls read non-temporally too.
+    ("flow C2", (4, 1, 4096, 12288, {}), dict(route="decode", flow=1, stream=1)),
+    ("flow C5", (8, 1, 5120, 151936, dict(argmax=True)), dict(route="decode", flow=1, stream=1)),
+    ("no flow C1: one tile a workgroup", (8, 1, 4096, 4096, {}), dict(flow=0, stream=0)),
+    ("no flow C3: one tile a workgroup", (4, 1, 12288, 4096, {}), dict(flow=0, stream=1)),
+    ("no flow: 30 chunks a tile fill whole phases", (4, 1, 3840, 12288, {}), dict(flow=0)),
+    ("no flow: padded last chunk", (4, 1, 4064, 12288, {}), dict(flow=0)),
+    ("no flow: gate/up pair", (4, 1, 5120, 17408, dict(pair=True)), dict(flow=0)),
     ("stream C3 8 rows (eight-row groups, one row group)", (4, 8, 12288, 4096, {}),
      dict(route="decode8", row_groups=1, stream=1)),
     ("stream W8 16 rows (two row groups)", (8, 16, 5120, 17408, {}), dict(route="decode8", row_groups=2, stream=1)),
@@ -146,6 +155,19 @@ def test_stream_override(hb, monkeypatch):
     assert hb.plan(8, 1, 4096, 4096)["stream"] == 1
     assert hb.plan(4, 1, 5120, 17408, pair=True)["stream"] == 0
     assert hb.plan(4, 1, 5120, 10240, multi=True)["stream"] == 0
+
+
+def test_flow_override(hb, monkeypatch):
+    """BREEZE_HIP_FLOW: 0 / 1 turn phases across tile boundaries off / on
+    wherever they apply (tiles of at least 15 whole chunks, plain calls)."""
+    assert hb.plan(4, 1, 4096, 12288)["flow"] == 1
+    monkeypatch.setenv("BREEZE_HIP_FLOW", "0")
+    assert hb.plan(4, 1, 4096, 12288)["flow"] == 0
+    monkeypatch.setenv("BREEZE_HIP_FLOW", "1")
+    assert hb.plan(8, 1, 4096, 4096)["flow"] == 1  # one tile a workgroup: same phases
+    assert hb.plan(4, 1, 1024, 12288)["flow"] == 0  # 8 chunks a tile
+    assert hb.plan(4, 1, 4064, 12288)["flow"] == 0  # padded last chunk
+    assert hb.plan(4, 1, 5120, 17408, multi=True)["flow"] == 0
 
 
 def test_plan_follows_the_device_size(hb):
