@@ -1138,6 +1138,15 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 //     phase), kStreamMaxGroups (2): W4 K=12288 N=4096 at 8 / 16 / 24 rows
 //     (one / two / three row groups) 13.13 / 19.12 / 29.75 -> 12.65 / 18.99 /
 //     31.79, W8 K=5120 N=17408 at 16 rows 33.13 -> 31.27, W4 28.77 -> 28.50.
+//   flow_phases  plain decode calls whose workgroups hold two tiles or more
+//     of at least 15 whole chunks that do not fill whole phases run their
+//     phases across tile boundaries (one stream of chunks), which leaves
+//     few idle slots, so the non-temporal rule above counts over the
+//     stream.  Plain -> flow with non-temporal loads: W4 K=4096 N=12288
+//     (C2) 7.22 -> 6.98, N=24576 12.25 -> 11.3, W8 K=4096 N=12288 10.5 ->
+//     9.8, W8 K=5120 N=17408 18.9 -> 17.2, N=151936 (C5, with non-temporal
+//     loads before) 122.7 -> 119.3; W4 K=5120 N=17408 and K=17408 N=5120
+//     even.  One tile a workgroup (W4 K=17408 N=64, forced): 8.30 -> 8.63.
 //   kSplitMaxTiles (8), kSplitMinPhases (20)  split-K takes plain decode
 //     calls of at most 8 column tiles whose tiles have 20 phases or more
 //     (15 chunks a phase: W8 K >= 18272, W4 K >= 36512).  The unsplit
