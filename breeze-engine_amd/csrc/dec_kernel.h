@@ -48,17 +48,20 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     a.RS = 4 >> ((misc >> 5) & 3);
     a.RG = (misc >> 8) & 15;
     a.pair_xcd = (misc >> 12) & 1;
-    constexpr bool PAIR = FUSE == kFusePair, NORM = FUSE == kFuseNormMulti;
+    constexpr bool PAIR = FUSE == kFusePair || FUSE == kFusePairFlow || FUSE == kFusePairFlowStream;
+    constexpr bool NORM = FUSE == kFuseNormMulti;
     constexpr bool MULTI = FUSE == kFuseMulti || NORM;
     constexpr bool SPLIT = FUSE == kFuseSplit;
     // Weight chunks are read once per call: with STREAM the loads carry the
     // non-temporal hint, which streams faster where a workgroup reads many
     // tiles (the host decides; the idle loads' L2 re-reads then miss more,
     // which costs where it has few).
-    constexpr bool STREAM = FUSE == kFuseStream || FUSE == kFuseFlowStream;
+    constexpr bool STREAM = FUSE == kFuseStream || FUSE == kFuseFlowStream || FUSE == kFusePairFlowStream;
     // FLOW: phases run across tile boundaries (the host takes it where
-    // workgroups hold several tiles of at least 15 chunks).
-    constexpr bool FLOW = FUSE == kFuseFlow || FUSE == kFuseFlowStream;
+    // workgroups hold several tiles of at least 15 whole chunks); with PAIR
+    // the stream alternates a column tile's gate and up chunks.
+    constexpr bool FLOW = FUSE == kFuseFlow || FUSE == kFuseFlowStream || FUSE == kFusePairFlow ||
+                          FUSE == kFusePairFlowStream;
     static_assert(!SPLIT || FUSED, "split-K quantizes its pieces in the prologue");
     constexpr int JG = BITS == 8 ? 2 : 4;
     constexpr int PP = dec_pitch(JG);
@@ -172,7 +175,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
     const int nT = base_t + (g < rem_t ? 1 : 0);
     const int nbg = a.nbg;
     const int U = SPLIT  ? pb - pa
-                  : FLOW ? (nT * nbg + kProducers - 1) / kProducers
+                  : FLOW ? (nT * nbg * (PAIR ? 2 : 1) + kProducers - 1) / kProducers
                          : nT * npw * (PAIR ? 2 : 1);  // phases of this workgroup
 
     const DecLds lay = dec_lds(min(a.M, a.RS), SPLIT ? split_piece_blocks(npw, nsplit, a.nbg, JG) : a.nblk, JG, P64);
@@ -258,7 +261,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         const bool up = PAIR && ld_sel;
         if constexpr (STREAM) {
             typedef unsigned int u4v __attribute__((ext_vector_type(4)));
-            const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(lw + wi));
+            const u4v t = __builtin_nontemporal_load(reinterpret_cast<const u4v*>((up ? a.W2 : lw) + wi));
             p.w = make_uint4(t.x, t.y, t.z, t.w);
         } else {
             p.w = (up ? a.W2 : lw)[wi];
@@ -279,9 +282,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
         ld_c += kProducers;
         if constexpr (FLOW) {
             // One stream of chunks over the tiles (nbg >= 15: one wrap at
-            // most); past the last tile the loads re-read its last chunk.
+            // most; a gate tile wraps into the same columns' up tile);
+            // past the last tile the loads re-read its last chunk.
             if (ld_c >= nbg) {
-                if (++ld_t < nT) {
+                if (PAIR && ld_sel == 0) {
+                    ld_sel = 1;
+                    ld_c -= nbg;
+                } else if (++ld_t < nT) {
+                    if (PAIR) ld_sel = 0;
                     ld_c -= nbg;
                     ld_w += nbg * 64;
                     ld_s += a.ngrp * 16;
@@ -513,6 +521,19 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 }
             }
         };
+        // FLOW: the stream's tile ends (with PAIR a gate tile's sum waits
+        // for the same columns' up tile).
+        auto tile_end = [&](float v) {
+            if (PAIR && pr_sel == 0) {
+                gate = v;
+                pr_sel = 1;
+            } else {
+                emit(PAIR ? silu_mul(gate, v) : v);
+                if (PAIR) pr_sel = 0;
+                ++pr_t;
+            }
+            tb += nbg;
+        };
         for (int u = 0; u < U; ++u) {
             lds_barrier();
             const float* fp = fbuf + ((u & 1) * 64 + lane) * PP;
@@ -536,10 +557,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                         for (int jb = 0; jb < JG; ++jb) acc = __builtin_fmaf(sv[i][jb], fv[i][jb], acc);
                     }
                     if (rem == kProducers) {
-                        emit(acc);
+                        tile_end(acc);
                         acc = 0.0f;
-                        ++pr_t;
-                        tb += nbg;
                     }
                 } else {
                     // Tile pr_t ends at slot rem - 1 (no padding: the host
@@ -574,9 +593,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                             }
                         }
                     }
-                    emit(out);
-                    ++pr_t;
-                    tb += nbg;
+                    tile_end(out);
                 }
                 continue;
             }
@@ -940,6 +957,10 @@ template <int BITS, bool HP, bool FUSED, bool EXTRA, bool P64>
 hipError_t launch_dec_w(bool* attr_set, const GemvArgs& a, int grid, int lds, int fuse, hipStream_t st) {
     if (fuse == kFusePair)
         return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePair, P64>(attr_set, a, grid, lds, st);
+    if (fuse == kFusePairFlow)
+        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePairFlow, P64>(attr_set, a, grid, lds, st);
+    if (fuse == kFusePairFlowStream)
+        return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFusePairFlowStream, P64>(attr_set, a, grid, lds, st);
     if (fuse == kFuseSplit) {
         if constexpr (FUSED) return launch_dec_t<BITS, HP, FUSED, EXTRA, kDecRing, kFuseSplit, P64>(attr_set, a, grid, lds, st);
         return hipErrorInvalidValue;  // split pieces quantize in the prologue

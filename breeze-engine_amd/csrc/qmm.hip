@@ -782,7 +782,7 @@ struct Workspace {
     size_t hA_cap = 0, hC_cap = 0;
     hipStream_t stream = nullptr;
     int n_cu = 0;
-    bool attr_set[512] = {};  // decode kernel variants with the kernel attribute set
+    bool attr_set[1024] = {};  // decode kernel variants with the kernel attribute set
     bool dec8_attr[64] = {};  // the same for dec8_kernel, per (bits, mode) and (FUSE mode, metadata, LDS records)
     bool pf_attr[256] = {};
 };
@@ -1147,6 +1147,10 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 //     9.8, W8 K=5120 N=17408 18.9 -> 17.2, N=151936 (C5, with non-temporal
 //     loads before) 122.7 -> 119.3; W4 K=5120 N=17408 and K=17408 N=5120
 //     even.  One tile a workgroup (W4 K=17408 N=64, forced): 8.30 -> 8.63.
+//     The gate/up pair's stream alternates each column tile's gate and up
+//     chunks (two stream tiles a column tile): W4 K=5120 N=17408 at 1 / 2 /
+//     4 rows 23.0 / 22.8 / 25.6 -> 21.8 / 21.8 / 24.3 (with non-temporal
+//     loads, which the pair takes only with its phases across tiles).
 //   kSplitMaxTiles (8), kSplitMinPhases (20)  split-K takes plain decode
 //     calls of at most 8 column tiles whose tiles have 20 phases or more
 //     (15 chunks a phase: W8 K >= 18272, W4 K >= 36512).  The unsplit
@@ -1302,11 +1306,11 @@ struct Plan {
 // table).  BREEZE_HIP_FLOW=0 / 1
 // turns it off / on wherever it applies.
 bool flow_phases(const Shape& h, const CallKind& k, const Plan& p, int tiles) {
-    if (k.pair || k.multi || k.norm || k.dots || p.split) return false;
+    if (k.multi || k.norm || k.dots || p.split) return false;
     const int JG = h.bits == 8 ? 2 : 4;
     const int nbg = (h.nblk + JG - 1) / JG;
     if (nbg < kProducers || h.nblk % JG) return false;  // one tile end a phase; no padded chunk
-    const int per_wg = (tiles + p.NG - 1) / p.NG;
+    const int per_wg = (tiles + p.NG - 1) / p.NG * (k.pair ? 2 : 1);  // tiles of the stream
     if (const char* env = std::getenv("BREEZE_HIP_FLOW")) return env[0] == '1';
     return per_wg >= 2 && nbg % kProducers != 0;
 }
@@ -1319,11 +1323,12 @@ bool flow_phases(const Shape& h, const CallKind& k, const Plan& p, int tiles) {
 // the weights through L2); see the routing table.  BREEZE_HIP_STREAM=0 / 1
 // turns them off / on for every plain decode call.
 bool stream_loads(const Shape& h, const CallKind& k, const Plan& p, int producers, int tiles) {
-    if (k.pair || k.multi || k.norm || k.dots || p.split) return false;
+    // A gate/up pair reads non-temporally only with its phases across tiles.
+    if ((k.pair && !p.flow) || k.multi || k.norm || k.dots || p.split) return false;
     if (const char* env = std::getenv("BREEZE_HIP_STREAM")) return env[0] == '1';
     const int JG = h.bits == 8 ? 2 : 4;
     int nbg = (h.nblk + JG - 1) / JG;
-    if (p.flow) nbg *= (tiles + p.NG - 1) / p.NG;  // one stream over the busiest workgroup's tiles
+    if (p.flow) nbg *= (tiles + p.NG - 1) / p.NG * (k.pair ? 2 : 1);  // one stream over the busiest workgroup's tiles
     const int slots = (nbg + producers - 1) / producers * producers;
     return p.RG <= kStreamMaxGroups && (slots - nbg) * kStreamIdleDiv <= slots;
 }
@@ -1618,7 +1623,7 @@ int run(Workspace& w, Scratch& s, Handle* h, const float* dA, int M, float* dC, 
         a.D2 = h2->D;
     }
     const int fz = p.split ? kFuseSplit
-                   : pair  ? kFusePair
+                   : pair  ? (p.flow ? (p.stream ? kFusePairFlowStream : kFusePairFlow) : kFusePair)
                    : mp    ? (mp->norm ? kFuseNormMulti : kFuseMulti)
                    : p.flow   ? (p.stream ? kFuseFlowStream : kFuseFlow)
                    : p.stream ? kFuseStream

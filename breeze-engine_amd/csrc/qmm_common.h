@@ -273,8 +273,10 @@ constexpr int kMaxSeg = 4;
 // non-temporal loads) whose phases run across tile boundaries: the chunks
 // of a workgroup's tiles form one stream, so a tile's short last phase is
 // filled with the next tile's first chunks.
+// kFusePairFlow and kFusePairFlowStream do the same for the gate/up pair,
+// whose stream alternates a column tile's gate and up chunks.
 constexpr int kFusePlain = 0, kFusePair = 1, kFuseMulti = 2, kFuseNormMulti = 3, kFuseSplit = 4, kFuseStream = 5,
-              kFuseFlow = 6, kFuseFlowStream = 7;
+              kFuseFlow = 6, kFuseFlowStream = 7, kFusePairFlow = 8, kFusePairFlowStream = 9;
 
 // One weight chunk of a wave plus its per-column metadata.  EXTRA handles
 // (explicit zero points, legacy corr, scale groups smaller than a chunk)

@@ -72,7 +72,9 @@ TABLE = [
     ("stream C5 (argmax)", (8, 1, 5120, 151936, dict(argmax=True)), dict(route="decode", stream=1)),
     ("stream W4 K=5120", (4, 1, 5120, 17408, {}), dict(stream=1)),
     ("no stream C1: 11 of 75 slots idle", (8, 1, 4096, 4096, {}), dict(stream=0)),
-    ("no stream: gate/up pair", (4, 1, 5120, 17408, dict(pair=True)), dict(stream=0)),
+    ("stream: gate/up pair with phases across tiles", (4, 1, 5120, 17408, dict(pair=True)), dict(flow=1, stream=1)),
+    ("no stream: gate/up pair on the eight-row groups", (4, 20, 5120, 17408, dict(pair=True)),
+     dict(route="decode8", flow=0, stream=0)),
     ("no stream: split-K", (8, 1, 24576, 64, {}), dict(split=26, stream=0)),
     # Phases across tile boundaries: several tiles a workgroup, whole chunks
     # that do not fill whole phases; then one stream of chunks leaves few
@@ -83,7 +85,8 @@ TABLE = [
     ("no flow C3: one tile a workgroup", (4, 1, 12288, 4096, {}), dict(flow=0, stream=1)),
     ("no flow: 30 chunks a tile fill whole phases", (4, 1, 3840, 12288, {}), dict(flow=0)),
     ("no flow: padded last chunk", (4, 1, 4064, 12288, {}), dict(flow=0)),
-    ("no flow: gate/up pair", (4, 1, 5120, 17408, dict(pair=True)), dict(flow=0)),
+    ("flow: gate/up pair (gate and up tiles alternate)", (4, 1, 4096, 4096, dict(pair=True)), dict(flow=1)),
+    ("no flow: multi-projection", (4, 1, 5120, 10240, dict(multi=True)), dict(flow=0, stream=0)),
     ("stream C3 8 rows (eight-row groups, one row group)", (4, 8, 12288, 4096, {}),
      dict(route="decode8", row_groups=1, stream=1)),
     ("stream W8 16 rows (two row groups)", (8, 16, 5120, 17408, {}), dict(route="decode8", row_groups=2, stream=1)),
@@ -147,13 +150,16 @@ def test_split_overrides(hb, monkeypatch):
 
 def test_stream_override(hb, monkeypatch):
     """BREEZE_HIP_STREAM: 0 / 1 turn non-temporal weight loads off / on for
-    every plain decode call (never for fused calls or split-K)."""
+    every plain decode call and gate/up pairs with phases across tiles
+    (never multi-projection calls or split-K)."""
     assert hb.plan(8, 1, 5120, 151936, argmax=True)["stream"] == 1
     monkeypatch.setenv("BREEZE_HIP_STREAM", "0")
     assert hb.plan(8, 1, 5120, 151936, argmax=True)["stream"] == 0
     monkeypatch.setenv("BREEZE_HIP_STREAM", "1")
     assert hb.plan(8, 1, 4096, 4096)["stream"] == 1
-    assert hb.plan(4, 1, 5120, 17408, pair=True)["stream"] == 0
+    assert hb.plan(4, 1, 5120, 17408, pair=True)["stream"] == 1  # a pair with phases across tiles
+    monkeypatch.setenv("BREEZE_HIP_FLOW", "0")
+    assert hb.plan(4, 1, 5120, 17408, pair=True)["stream"] == 0  # a pair without
     assert hb.plan(4, 1, 5120, 10240, multi=True)["stream"] == 0
 
 
