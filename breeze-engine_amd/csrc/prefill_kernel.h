@@ -30,22 +30,27 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     const int nst = (nch + kPfChunks - 1) / kPfChunks;
     const bool odd = a.nblk & 1;
 
-    // Shared part of a chunk (INT8) or stage (INT4): slot k of this wave
-    // loads the 1 KB at x0, u = k * kPfWaves + wave (clamped), lane bytes
-    // x0 + 16*lane.  INT8: x0 = min(u * 1024, kShared - 1024) in the chunk
-    // (overlapping slots write equal bytes).  INT4: raw tile u of the stage
-    // into chunk 0's weight area, or KB u - CT of the raw area.
+    // Shared part of a chunk (INT8) or stage (INT4).
+    // INT8: loads k < kWJ load weight tile min(wave + kPfWaves k, CT - 1)
+    // (a spare load repeats the last tile: same bytes, same place).  Loads
+    // k >= kWJ load the 1 KB of sums and scales at x0 = kWS + 1024 u,
+    // u = (k - kWJ) * kPfWaves + wave (clamped), lane bytes x0 + 16*lane.
+    // INT4: slot k loads unit u = k * kPfWaves + wave (clamped): raw tile u
+    // of the stage into chunk 0's weight area, or KB u - CT of the raw area.
     const char* src0[L::kPerWave];
     uint32_t step[L::kPerWave], gstep[L::kPerWave], x0s[L::kPerWave];
     bool to_raw[L::kPerWave];
 #pragma unroll
     for (int k = 0; k < L::kPerWave; ++k) {
-        const int u = min(k * kPfWaves + wave, L::kUnits - 1);
-        const int x0 = min(u * 1024, L::kShared - 1024);
+        const int u = BITS == 8 ? min((k - L::kWJ) * kPfWaves + wave, L::kSU - 1) : min(k * kPfWaves + wave, L::kUnits - 1);
+        const int x0 = BITS == 8 ? L::kWS + u * 1024 : u * 1024;
         const int x = x0 + 16 * lane;
         x0s[k] = (uint32_t)x0;
         gstep[k] = 0;
+        step[k] = 0;
+        src0[k] = a.W;
         to_raw[k] = false;
+        if (BITS == 8 && k < L::kWJ) continue;
         if (BITS == 4) {
             if (u < CT) {
                 const int tc = min(t0 + u, a.ntiles - 1);
@@ -73,10 +78,6 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                     gstep[k] = 64;
                 }
             }
-        } else if (x < L::kWS) {
-            const int tc = min(t0 + (x >> 10), a.ntiles - 1);
-            src0[k] = a.W + (size_t)tc * nch * 1024 + (x & 1023);
-            step[k] = 1024;
         } else if (x < L::kSB) {
             const int y = x - L::kWS;
             const int tc = min(t0 + (y >> 7), a.ntiles - 1);
@@ -100,7 +101,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     // over the waves: unit wave + 8 i, clamped, so a spare slot repeats the
     // last unit's load (same bytes to the same place).
     constexpr int kRecUnits = 6 * RP, kRecPerWave = (kRecUnits + kPfWaves - 1) / kPfWaves;
-    const char* rec0 = a.R + (size_t)blockIdx.y * (2 * RP) * nch * kRecBytes + 16 * lane;
+    const char* rec0 = a.R + (size_t)blockIdx.y * (2 * RP) * nch * kRecBytes;
     uint32_t rec_src[kRecPerWave], rec_dst[kRecPerWave];
 #pragma unroll
     for (int i = 0; i < kRecPerWave; ++i) {
@@ -115,9 +116,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     constexpr int kDmaChunk = L::kPerWave + kRecPerWave;
     // INT4: only chunk 0 of a stage (first) carries the stage's shared loads;
     // raw is the LDS address of the stage's raw area.
-    auto dma_slot = [&](int c, uint32_t cbase, int d, bool first, uint32_t raw) {
+    auto dma_slot = [&](int c, uint32_t cbase, int d, bool first, uint32_t raw) __attribute__((always_inline)) {
         if (d < L::kPerWave) {
-            if (BITS == 8) {
+            if (BITS == 8 && d < L::kWJ) {
+                const int tile = min(d * kPfWaves + wave, CT - 1);
+                const int tc = min(t0 + tile, a.ntiles - 1);
+                dma16s(a.W + ((size_t)tc * nch + c) * 1024, 16 * lane, cbase + (uint32_t)(tile * 1024));
+            } else if (BITS == 8) {
                 const size_t g = SCM == 1 ? (size_t)((2 * c) >> a.sc_shift) : 0;
                 dma16(src0[d] + (size_t)c * step[d] + g * gstep[d], cbase + x0s[d]);
             } else if (first) {
@@ -127,7 +132,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             }
         } else {
             const int e = d - L::kPerWave;
-            dma16(rec0 + rec_src[e] + (size_t)c * kRecBytes, cbase + rec_dst[e]);
+            dma16s(rec0 + rec_src[e] + (size_t)c * kRecBytes, 16 * lane, cbase + rec_dst[e]);
         }
     };
     // Raw area of stage g (INT4).
@@ -138,7 +143,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     // it exactly.  Two stages wait for all loads and skip those chunks (the
     // loads kept the allocator from fitting the widest shapes' registers).
     constexpr int kStageLoads = BITS == 8 ? kPfChunks * kDmaChunk : kDmaChunk + (kPfChunks - 1) * kRecPerWave;
-    auto issue_stage = [&](int g, int buf) {
+    auto issue_stage = [&](int g, int buf) __attribute__((always_inline)) {
         const uint32_t sbase = lds0 + (uint32_t)(buf * L::kStage);
 #pragma unroll
         for (int cc = 0; cc < kPfChunks; ++cc) {
@@ -152,9 +157,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     // INT4: expands stage g (buffer buf) in place from its raw area (with more
     // than one row pair all threads share the tiles and a workgroup barrier
     // must follow).  Wave w takes tiles w, w + 8, ... (with one row pair, the
-    // tiles of its column part); lane l holds
-    // weight lane l of the tile (column l & 15, k-octet l >> 4), so the LDS
-    // reads and writes are linear.  The nibble sums of a column's four
+    // tiles of its column part); lane l holds weight lane l of the tile
+    // (column l & 15, k-octet l >> 4) and writes that octet of the four
+    // blocks where pf_w_byte puts it.  The nibble sums of a column's four
     // octets (one per 16-lane row) meet by row swaps.
     auto expand = [&](int g, int buf) {
         if constexpr (BITS == 4) {
@@ -185,8 +190,13 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                     hi[b] = (((wv[b] >> 4) & 0x0F0F0F0Fu) + zr) ^ 0x80808080u;
                     nsum[b] = __builtin_amdgcn_udot8(wv[b], 0x11111111u, 0u, false);  // <= 120
                 }
-                *reinterpret_cast<uint4*>(sb + wl) = make_uint4(lo[0], hi[0], lo[1], hi[1]);
-                *reinterpret_cast<uint4*>(sb + L::kChunk + wl) = make_uint4(lo[2], hi[2], lo[3], hi[3]);
+                // Octet o of blocks 0-3 (chunk b >> 1, block b & 1) into the
+                // operand order; this wave alone reads and writes tile t,
+                // and all of its reads of t are done (the writes use them).
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    *reinterpret_cast<uint2*>(sb + (b >> 1) * L::kChunk + t * 1024 + pf_w_byte(4, c, o, b & 1)) =
+                        make_uint2(lo[b], hi[b]);
                 // Per-column nibble sums of blocks (0, 1) and (2, 3), two per
                 // dword, summed over the four rows (octets).
                 uint32_t ps[2] = {nsum[0] | nsum[1] << 16, nsum[2] | nsum[3] << 16};
@@ -225,11 +235,14 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     // 128 * sum(b), is the l-byte MFMA's accumulator input, so that MFMA
     // holds the exact block integer cs, and the lane folds
     // acc = fma(s_a, f32(cs) * s_b, acc) in block order.
-    // Lane l: A row / output column c32 = l & 31, k half kh = l >> 5.  The
-    // operands come from the same LDS layout: a record's lane r + 16 * o
-    // holds k-octet o of row r, and a weight chunk's lane c + 16 * o holds
-    // k-octet o of column c for both blocks, so octets 2 kh and 2 kh + 1 are
-    // two 16-byte reads 256 bytes apart.
+    // Lane l: A row / output column c32 = l & 31, k half kh = l >> 5.  The A
+    // operand is one 16-byte LDS read: records hold k-octets 2 kh and
+    // 2 kh + 1 of a row side by side (pf_rec_byte).  So do expanded INT4
+    // tiles for B; INT8 tiles hold octet o of both blocks side by side, and
+    // B takes two 8-byte halves 256 bytes apart (pf_w_byte).  Reading those
+    // with one ds_read2_b64 straight into the operand was slower than the
+    // register moves after a merged 16-byte read: an 8-byte access at a
+    // 16-byte lane stride uses half the LDS banks.
     auto run32 = [&](auto ctw_tag, int toff) {
         constexpr int CTW = decltype(ctw_tag)::value;
         constexpr int NG = CTW / 2;
@@ -272,18 +285,15 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             constexpr int kAhead = 1;            // groups read ahead
             constexpr int NGB = NG * NB;         // group steps
             constexpr int NS = NGB + (ODD ? NB : 0);
+            constexpr int TL = DMA ? (BOTH ? 2 : 1) * kDmaChunk : 0;  // loads this call issues
             const char* ar = cp + L::kA + 2 * rp * kRecBytes;
             v4i a_h[2], a_l[2];
             float sa[2][16];
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                // Two 8-byte halves 256 bytes apart: one ds_read2_b64 into
-                // the operand's four registers.
-                const char* rb = ar + (c32 >> 4) * kRecBytes + b * 1024 + 16 * ((c32 & 15) + 32 * kh);
-                const uint2 h0 = *reinterpret_cast<const uint2*>(rb), h1 = *reinterpret_cast<const uint2*>(rb + 256);
-                const uint2 l0 = *reinterpret_cast<const uint2*>(rb + 8), l1 = *reinterpret_cast<const uint2*>(rb + 264);
-                a_h[b] = v4i{(int)h0.x, (int)h0.y, (int)h1.x, (int)h1.y};
-                a_l[b] = v4i{(int)l0.x, (int)l0.y, (int)l1.x, (int)l1.y};
+                const char* rb = ar + (c32 >> 4) * kRecBytes + b * 1024 + pf_rec_byte(c32 & 15, 2 * kh);
+                a_h[b] = *reinterpret_cast<const v4i*>(rb);
+                a_l[b] = *reinterpret_cast<const v4i*>(rb + 512);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     // rows 8q + 4kh .. +3: record (q >> 1), row 8 (q & 1) + 4 kh
@@ -297,9 +307,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             }
             // The odd tile: 16x16x32 operands, as in the path above, read at
             // the last group step (its registers are free by then).
-            uint64_t ah[2][2], al[2][2];
+            uint64_t ah[2][2], al[2][2], bwo[2] = {0, 0};
             float so[2][2][4];
-            uint4 bwo = make_uint4(0, 0, 0, 0);
             int2 wso = make_int2(0, 0);
             float sbo2[2] = {0.0f, 0.0f};
             auto load_odd = [&]() {
@@ -308,9 +317,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                 for (int r = 0; r < 2; ++r)
 #pragma unroll
                     for (int b = 0; b < NB; ++b) {
-                        const uint4 q = *reinterpret_cast<const uint4*>(ar + r * kRecBytes + b * 1024 + 16 * lane);
-                        ah[r][b] = (uint64_t)q.y << 32 | q.x;
-                        al[r][b] = (uint64_t)q.w << 32 | q.z;
+                        const char* q = ar + r * kRecBytes + b * 1024 + pf_rec_byte(col, grp);
+                        ah[r][b] = *reinterpret_cast<const uint64_t*>(q);
+                        al[r][b] = *reinterpret_cast<const uint64_t*>(q + 512);
                         const float4 s4 = *reinterpret_cast<const float4*>(ar + r * kRecBytes + kRecA + b * 64 + 16 * grp);
                         so[r][b][0] = s4.x;
                         so[r][b][1] = s4.y;
@@ -318,7 +327,9 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                         so[r][b][3] = s4.w;
                     }
                 const int t = toff + CTW - 1;
-                bwo = *reinterpret_cast<const uint4*>(cp + t * 1024 + 16 * lane);
+#pragma unroll
+                for (int b = 0; b < NB; ++b)
+                    bwo[b] = *reinterpret_cast<const uint64_t*>(cp + t * 1024 + pf_w_byte(BITS, col, grp, b));
                 if (HP) wso = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * col);
                 if (SCM == 2) {
                     const float2 f = *reinterpret_cast<const float2*>(cp + L::kSB + t * 128 + 8 * col);
@@ -336,12 +347,16 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             auto load_group = [&](int g) {
                 if (g >= NG) return;
                 const int t = toff + 2 * g + (c32 >> 4);
-                const char* bp = cp + t * 1024 + 16 * ((c32 & 15) + 32 * kh);
 #pragma unroll
                 for (int b = 0; b < NB; ++b) {
-                    const uint2 lo = *reinterpret_cast<const uint2*>(bp + 8 * b);
-                    const uint2 hi = *reinterpret_cast<const uint2*>(bp + 256 + 8 * b);
-                    bq[g][b] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+                    if (BITS == 8) {
+                        const char* bp = cp + t * 1024 + pf_w_byte(8, c32 & 15, 2 * kh, b);
+                        const uint2 lo = *reinterpret_cast<const uint2*>(bp);
+                        const uint2 hi = *reinterpret_cast<const uint2*>(bp + 256);
+                        bq[g][b] = v4i{(int)lo.x, (int)lo.y, (int)hi.x, (int)hi.y};
+                    } else {
+                        bq[g][b] = *reinterpret_cast<const v4i*>(cp + t * 1024 + pf_w_byte(4, c32 & 15, 2 * kh, b));
+                    }
                 }
                 if (HP) wsg[g] = *reinterpret_cast<const int2*>(cp + L::kWS + t * 128 + 8 * (c32 & 15));
                 if (SCM == 2) {
@@ -355,9 +370,7 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                 }
             };
             auto bop32 = [&](int g, int b) -> v4i { return bq[g][b]; };
-            auto bopo = [&](int b) -> uint64_t {
-                return b == 0 ? ((uint64_t)bwo.y << 32 | bwo.x) : ((uint64_t)bwo.w << 32 | bwo.z);
-            };
+            auto bopo = [&](int b) -> uint64_t { return bwo[b]; };
             v16i h32[NGB > 0 ? NGB : 1], d32[NGB > 0 ? NGB : 1];
             v4i ho[2][2], dov[2][2];
             const v16i z16 = {};
@@ -427,23 +440,20 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
             for (int s = 0; s < NS; ++s) {
                 if (s < NGB && s % NB == 0) load_group(s / NB + kAhead);
                 if (s == NGB - 1) load_odd();
-                if (DMA && s < kDmaChunk) dma_slot(c_next, nbase, s, FIRST, nraw);
-                if (BOTH && s >= kDmaChunk && s < 2 * kDmaChunk)
-                    dma_slot(c_next2, nbase + (uint32_t)L::kChunk, s - kDmaChunk, false, nraw);
+                // Load e of the TL this call issues goes out at step
+                // e NS / TL: evenly over the steps.
+#pragma unroll
+                for (int e = 0; e < TL; ++e) {
+                    if (e * NS / TL != s) continue;
+                    if (e < kDmaChunk) dma_slot(c_next, nbase, e, FIRST, nraw);
+                    else dma_slot(c_next2, nbase + (uint32_t)L::kChunk, e - kDmaChunk, false, nraw);
+                }
                 step_h(s + 1);
                 step_e(s);
                 step_d(s + 1);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (DMA) {
-#pragma unroll
-                for (int d = NS; d < kDmaChunk; ++d) dma_slot(c_next, nbase, d, FIRST, nraw);
-                if (BOTH) {
-#pragma unroll
-                    for (int d = (NS > kDmaChunk ? NS - kDmaChunk : 0); d < kDmaChunk; ++d)
-                        dma_slot(c_next2, nbase + (uint32_t)L::kChunk, d, false, nraw);
-                }
-            }
+
         };
 
         static_assert(kPfChunks == 2, "stage loop");

@@ -303,8 +303,8 @@ __global__ __launch_bounds__(256) void quantize_rec_kernel(const float* __restri
                                                            int nch, int Mpad, uint8_t* __restrict__ R) {
     // A wave per (16-row tile, block j): lane (r, o) = (lane >> 2, lane & 3)
     // quantizes k-octet o of row r, the 4 lanes of a row one block, and
-    // writes the octet's 16-byte record slot [8 h bytes | 8 l bytes].  The
-    // wave's 64 slots are the block's whole 1 KB part of the record.
+    // writes its 8 h bytes at pf_rec_byte(r, o) of the block's 1 KB and its
+    // 8 l bytes 512 bytes later.  The wave fills the whole 1 KB.
     const int g = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int o = lane & 3, r = lane >> 2;
     const int nb2 = 2 * nch;
@@ -322,7 +322,8 @@ __global__ __launch_bounds__(256) void quantize_rec_kernel(const float* __restri
     quant4x8<HP>(v0, v1, s, ph, pl);
     uint8_t* rec = R + ((size_t)mt * nch + (j >> 1)) * kRecBytes;
     const int b = j & 1;
-    *reinterpret_cast<uint4*>(rec + b * 1024 + (o * 16 + r) * 16) = make_uint4(ph.x, ph.y, pl.x, pl.y);
+    *reinterpret_cast<uint2*>(rec + b * 1024 + pf_rec_byte(r, o)) = ph;
+    *reinterpret_cast<uint2*>(rec + b * 1024 + 512 + pf_rec_byte(r, o)) = pl;
     if (o == 0) *reinterpret_cast<float*>(rec + kRecA + (b * 16 + r) * 4) = s;
 }
 

@@ -573,10 +573,22 @@ constexpr int kLdsMax = 160 * 1024;
 constexpr int kPfWaves = 8;
 // Chunks per ring stage.
 constexpr int kPfChunks = 2;
-// Activation record per (16-row tile, chunk): [block 2][lane 64][h 8 B, l 8 B]
-// in MFMA A-operand order (lane: row lane&15, k-octet lane>>4), then the
-// block scales [block 2][row 16] float.
+// Activation record per (16-row tile, chunk): per block 1 KB, h bytes then
+// l bytes, each [k half 2][row 16][16 B]: the 16 bytes of (row r, k half kh)
+// are k-octets 2 kh and 2 kh + 1 of row r, the v_mfma_i32_32x32x32_i8 A
+// operand of lane r + 16 kh (one 16-byte LDS read, no register moves).  Then
+// the block scales [block 2][row 16] float.
 constexpr int kRecA = 2048, kRecBytes = kRecA + 128;
+// Byte of (row r, k-octet o) in a block's h half of a record.
+__host__ __device__ constexpr int pf_rec_byte(int r, int o) { return 16 * (r + 16 * (o >> 1)) + 8 * (o & 1); }
+// Byte of (column c, k-octet o) of block b in a weight tile's 1 KB in LDS.
+// INT8 tiles arrive by DMA in the decode chunk order (octet o of both blocks
+// at 16 (c + 16 o)), so a 32x32x32 B operand takes two 8-byte halves.  INT4
+// tiles are expanded in LDS into [column half][k half][block][column c & 7]
+// [16 B]: one conflict-free 16-byte read per operand.
+__host__ __device__ constexpr int pf_w_byte(int bits, int c, int o, int b) {
+    return bits == 8 ? 16 * (c + 16 * o) + 8 * b : 16 * ((c & 7) + 8 * b + 16 * (o >> 1) + 32 * (c >> 3)) + 8 * (o & 1);
+}
 
 struct PfArgs {
     const char* W;   // INT8: [ntiles][nch][64 lanes][16 B]; INT4: [ntiles][nbg][64][16 B]
@@ -603,7 +615,10 @@ template <int CT, int SCM, int BITS, int RP, int S>
 struct PfLayout {
     static constexpr int kWS = CT * 1024;
     static constexpr int kSB = kWS + CT * 128;
-    static constexpr int kShared = kSB + (SCM == 2 ? CT * 128 : SCM == 1 ? CT * 64 : 0);
+    static constexpr int kSharedUsed = kSB + (SCM == 2 ? CT * 128 : SCM == 1 ? CT * 64 : 0);
+    // INT8 pads the sums and scales to whole KB, so that their 1 KB loads
+    // never overlap the weight tiles (which land permuted).
+    static constexpr int kShared = BITS == 8 ? kWS + (kSharedUsed - kWS + 1023) / 1024 * 1024 : kSharedUsed;
     static constexpr int kA = kShared;
     static constexpr int kChunk = kA + 2 * RP * kRecBytes;
     static constexpr int kStage = kPfChunks * kChunk;
@@ -612,10 +627,15 @@ struct PfLayout {
     static constexpr int kRaw = (kRawUsed + 1023) / 1024 * 1024;
     static constexpr int kRawOff = S * kStage;  // raw area r at kRawOff + r * kRaw
     static constexpr int kNRaw = RP == 1 ? S : S - 1;
-    // DMA units of 1 KB per stage (INT8: per chunk): INT8 the chunk's shared
-    // part, INT4 the CT raw tiles and the raw area.
-    static constexpr int kUnits = BITS == 8 ? (kShared + 1023) / 1024 : CT + kRaw / 1024;
-    static constexpr int kPerWave = (kUnits + kPfWaves - 1) / kPfWaves;
+    // INT8, per chunk: CT weight tiles of 1 KB, kWJ a wave; then the sums
+    // and scales in kSU units of 1 KB, kSJ a wave.
+    static constexpr int kWJ = BITS == 8 ? (CT + kPfWaves - 1) / kPfWaves : 0;
+    static constexpr int kSU = BITS == 8 ? (kShared - kWS) / 1024 : 0;
+    static constexpr int kSJ = (kSU + kPfWaves - 1) / kPfWaves;
+    // INT4, per stage: the CT raw tiles and the raw area in units of 1 KB.
+    static constexpr int kUnits = CT + kRaw / 1024;
+    // Shared loads a wave issues per chunk (INT8) or stage (INT4).
+    static constexpr int kPerWave = BITS == 8 ? kWJ + kSJ : (kUnits + kPfWaves - 1) / kPfWaves;
     static constexpr int kBytes = kRawOff + kNRaw * kRaw;
     static_assert(kShared % 64 == 0 && kBytes <= 160 * 1024, "layout");
 };
@@ -628,6 +648,13 @@ __device__ inline uint32_t lds_address(const void* p) {
 __device__ inline void dma16(const void* src, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(lds) : "memory");
 }
+
+// The same from a uniform base and a per-lane 32-bit byte offset: the address
+// arithmetic stays on the scalar unit.
+__device__ inline void dma16s(const void* base, uint32_t off, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
+}
+
 
 // s_waitcnt immediate: vmcnt(n), no wait on the other counters.
 __host__ __device__ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
