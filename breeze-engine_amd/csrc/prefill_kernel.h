@@ -157,21 +157,25 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     // INT4: expands stage g (buffer buf) in place from its raw area (with more
     // than one row pair all threads share the tiles and a workgroup barrier
     // must follow).  Wave w takes tiles w, w + 8, ... (with one row pair, the
-    // tiles of its column part); lane l holds weight lane l of the tile
-    // (column l & 15, k-octet l >> 4) and writes that octet of the four
-    // blocks where pf_w_byte puts it.  The nibble sums of a column's four
-    // octets (one per 16-lane row) meet by row swaps.
+    // tiles of its column part); each lane takes one (column, k-octet) of
+    // the tile and writes that octet of the four blocks where pf_w_byte puts
+    // it.  The nibble sums of a column's four octets meet across lanes.
     auto expand = [&](int g, int buf) {
         if constexpr (BITS == 4) {
             char* sb = pf_lds + buf * L::kStage;
             const char* raw = pf_lds + L::kRawOff + (g % L::kNRaw) * L::kRaw;
-            const int c = lane & 15, o = lane >> 4, cc = o & 1;
+            // Lane l expands octet o of column c of the tile, with
+            // c = (l & 7) + 8 ((l >> 4) & 1) and o = ((l >> 3) & 1) + 2 (l >> 5):
+            // eight lanes read 128 contiguous raw bytes, and sixteen lanes
+            // write 128 contiguous bytes of operands (pf_w_byte), so neither
+            // side has bank conflicts.
+            const int c = (lane & 7) + 8 * ((lane >> 4) & 1), o = ((lane >> 3) & 1) + 2 * (lane >> 5), cc = o & 1;
             // One row pair: each wave expands the tiles of its own column
             // part, which no other wave reads, so no barrier has to follow.
             const int t_beg = RP == 1 ? part_t0 : wave, t_end = RP == 1 ? part_t0 + part_nt : CT;
             const int t_step = RP == 1 ? 1 : kPfWaves;
             for (int t = t_beg; t < t_end; t += t_step) {
-                const int wl = t * 1024 + 16 * lane;
+                const int wl = t * 1024 + 16 * (c + 16 * o);
                 const uint4 w = *reinterpret_cast<const uint4*>(sb + wl);
                 const uint32_t z = SCM == 2 ? *reinterpret_cast<const uint32_t*>(raw + L::kRawZ + t * 64 + 4 * c)
                                             : 0x08080808u;
@@ -198,14 +202,14 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
                     *reinterpret_cast<uint2*>(sb + (b >> 1) * L::kChunk + t * 1024 + pf_w_byte(4, c, o, b & 1)) =
                         make_uint2(lo[b], hi[b]);
                 // Per-column nibble sums of blocks (0, 1) and (2, 3), two per
-                // dword, summed over the four rows (octets).
+                // dword, summed over the four octets: lanes l, l ^ 32 (o ^ 2)
+                // by a half swap, then l ^ 8 (o ^ 1) by a row rotate of 8.
                 uint32_t ps[2] = {nsum[0] | nsum[1] << 16, nsum[2] | nsum[3] << 16};
 #pragma unroll
                 for (int q = 0; q < 2; ++q) {
                     const auto s32 = __builtin_amdgcn_permlane32_swap(ps[q], ps[q], false, false);
                     const uint32_t y = s32[0] + s32[1];
-                    const auto s16 = __builtin_amdgcn_permlane16_swap(y, y, false, false);
-                    ps[q] = s16[0] + s16[1];
+                    ps[q] = y + (uint32_t)__builtin_amdgcn_update_dpp(0, (int)y, 0x128, 0xF, 0xF, false);
                 }
                 char* cb = sb + cc * L::kChunk;
                 if (o < 2) {
