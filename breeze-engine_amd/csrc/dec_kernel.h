@@ -341,14 +341,16 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
             // sums of squares (two runs of 4 terms in a lane, their sum, a
             // 4-lane DPP sum: the 8-lane sum of 4-term runs, pair by pair) go to
             // the idle phase buffer, every wave adds up each row's (a lane
-            // run of at most 8, a 16-lane DPP sum, the 4 row sums: at most
-            // 20 roundings a term) and norm_mean_from_bound decides the
-            // mean; a row it does not decide takes the in-order sum.  Any
+            // run of at most 6, a 16-lane DPP sum, the 4 row sums by lane
+            // swaps: at most 18 roundings a term) and norm_mean_from_bound_r
+            // decides the mean; a row it does not decide takes the in-order
+            // sum.  Any
             // summation order serves: the mean either comes from the bound,
             // which proves it equal to the reference's, or from the in-order
             // sum itself.
             float inv_r[NORM ? 4 : 1];
             if constexpr (NORM) {
+                const double rK = 1.0 / (double)a.K;  // ahead of the loads' use: off the critical path
                 double* nsq = reinterpret_cast<double*>(fbuf);
                 auto sumsq = [&](int p, const Oct& v) {
                     const int blk = p * qb + (tid >> 2);
@@ -372,15 +374,22 @@ __global__ __launch_bounds__(kDecWaves * 64) void dec_kernel(const void* act, co
                 for (int r = 0; r < 4; ++r) {
                     inv_r[r] = 0.0f;
                     if (r >= Mr || npass == 0) continue;
-                    double v = 0.0;
-                    for (int i = lane; i < a.nblk; i += 64) v += nsq[r * a.nblk + i];
-                    v = sum16_f64(v);
-                    v = (__builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 0)) +
-                         __builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 16))) +
-                        (__builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 32)) +
-                         __builtin_bit_cast(double, readlane64(__builtin_bit_cast(long long, v), 48)));
+                    // A lane's run: at most 6 block sums (384 row-blocks),
+                    // all read before the first add; the zeros past nblk
+                    // add exactly.
+                    double t[kNormRun];
+#pragma unroll
+                    for (int j = 0; j < kNormRun; ++j) {
+                        const int i = lane + 64 * j;
+                        t[j] = i < a.nblk ? nsq[r * a.nblk + i] : 0.0;
+                    }
+                    double v = t[0];
+#pragma unroll
+                    for (int j = 1; j < kNormRun; ++j) v += t[j];
+                    v = sum_rows_f64(sum16_f64(v));
                     float mean;
-                    if (a.norm_exact || !(v - v == 0.0) || !norm_mean_from_bound(v, a.K, 0, &mean))
+                    if (a.norm_exact || a.nblk > 64 * kNormRun || !(v - v == 0.0) ||
+                        !norm_mean_from_bound_r(v, a.K, rK, 0, &mean))
                         mean = (float)(norm_sumsq_inorder<8>(a.A + (size_t)(m0 + r) * a.K, a.K) / (double)a.K);
                     inv_r[r] = 1.0f / sqrtf(mean + a.norm_eps);
                 }

@@ -1175,7 +1175,6 @@ void fill_args(const Handle* h, GemvArgs& a, int M) {
 // across tile boundaries).
 constexpr int kFusedMaxBlocks = 512, kFusedMaxBlocks2 = 768;
 constexpr int kFusedCapBlocks = kQuantPasses * 256;  // what the prologue can quantize
-constexpr int kNormFusedMaxBlocks = 3 * 128;
 constexpr int kDecMaxRows = 32, kDecMaxGroups = 8;
 constexpr int kDec8MaxRows = 32;  // four row groups of eight
 constexpr int kPairMaxRows4 = 16;

@@ -213,6 +213,10 @@ constexpr int kProducers = kDecWaves - 1;
 // barrier waits for the slowest quantizer.  More blocks take all sixteen
 // waves (at most kQuantPasses passes of 256).
 constexpr int kQuantEarlyBlocks = 128, kQuantPasses = 6;
+// Most row-blocks a launch with the RMSNorm in its prologue takes (two
+// quantize passes), and so the longest lane run of block sums per row.
+constexpr int kNormFusedMaxBlocks = 3 * 128;
+constexpr int kNormRun = (kNormFusedMaxBlocks + 63) / 64;
 
 struct GemvArgs {
     const uint4* W;
@@ -369,6 +373,41 @@ __device__ inline bool norm_mean_from_bound(double T, int H, int per, float* mea
     const float lo = (float)((T - E) / (double)H), hi = (float)((T + E) / (double)H);
     *mean = lo;
     return lo == hi;
+}
+
+// The same decision with rH = RN(1 / H) in place of the two divisions (rH
+// can be formed before T is known).  With u = 2^-53 and Q = T / H,
+// q = RN(T rH) is within 2.01 u Q of Q, so ss / H lies within
+// E / H + 2.01 u Q of q.  D = (E rH + 2^-50 q)(1 + 2^-10) exceeds that by at
+// least 1.98 u q, more than the rounding of q -/+ D, so RN(q - D) and
+// RN(q + D) bracket every ss / H, and (float) of both agreeing decides it as
+// above.  T must be finite and >= 0; a sum of float squares is 0 or
+// >= 2^-298, far above double underflow, so the relative bounds hold.
+__device__ inline bool norm_mean_from_bound_r(double T, int H, double rH, int per, float* mean) {
+    const double E = (double)(H + per + 24) * 0x1p-53 * T * (1.0 + 0x1p-10);
+    const double q = T * rH;
+    const double D = (E * rH + q * 0x1p-50) * (1.0 + 0x1p-10);
+    const float lo = (float)(q - D), hi = (float)(q + D);
+    *mean = lo;
+    return lo == hi;
+}
+
+// Sum of a double over the four 16-lane rows of a wave, the same in every
+// lane: rows (0 + 2) and (1 + 3) by a half swap, then those two by a row
+// swap (two roundings a term).
+__device__ inline double sum_rows_f64(double v) {
+    auto swap_add = [](double x, bool half) {
+        const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+        const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+        const auto l = half ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                            : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+        const auto h = half ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                            : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+        const double a = __builtin_bit_cast(double, (unsigned long long)h[0] << 32 | l[0]);
+        const double c = __builtin_bit_cast(double, (unsigned long long)h[1] << 32 | l[1]);
+        return a + c;
+    };
+    return swap_add(swap_add(v, true), false);
 }
 
 __device__ inline long long readlane64(long long v, int l) {
