@@ -42,7 +42,8 @@ __global__ __launch_bounds__(kPfWaves * 64) void prefill_kernel(PfArgs a) {
     bool to_raw[L::kPerWave];
 #pragma unroll
     for (int k = 0; k < L::kPerWave; ++k) {
-        const int u = BITS == 8 ? min((k - L::kWJ) * kPfWaves + wave, L::kSU - 1) : min(k * kPfWaves + wave, L::kUnits - 1);
+        const int u = BITS == 8 ? min((k - L::kWJ) * kPfWaves + wave, L::kSU - 1)
+                                : min(k * kPfWaves + wave, L::kUnits - 1);
         const int x0 = BITS == 8 ? L::kWS + u * 1024 : u * 1024;
         const int x = x0 + 16 * lane;
         x0s[k] = (uint32_t)x0;

@@ -655,8 +655,8 @@ struct PfLayout {
     static constexpr int kWS = CT * 1024;
     static constexpr int kSB = kWS + CT * 128;
     static constexpr int kSharedUsed = kSB + (SCM == 2 ? CT * 128 : SCM == 1 ? CT * 64 : 0);
-    // INT8 pads the sums and scales to whole KB, so that their 1 KB loads
-    // never overlap the weight tiles (which land permuted).
+    // INT8 pads the sums and scales to whole KB: their 1 KB loads start
+    // where the weight tiles end and must not run into the records.
     static constexpr int kShared = BITS == 8 ? kWS + (kSharedUsed - kWS + 1023) / 1024 * 1024 : kSharedUsed;
     static constexpr int kA = kShared;
     static constexpr int kChunk = kA + 2 * RP * kRecBytes;
@@ -693,7 +693,6 @@ __device__ inline void dma16(const void* src, uint32_t lds) {
 __device__ inline void dma16s(const void* base, uint32_t off, uint32_t lds) {
     asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds) : "memory");
 }
-
 
 // s_waitcnt immediate: vmcnt(n), no wait on the other counters.
 __host__ __device__ constexpr int vm_wait(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
